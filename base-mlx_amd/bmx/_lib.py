@@ -1,0 +1,95 @@
+"""ctypes binding of libbmx.so (the C ABI declared in include/bmx.h).
+
+The library is built in-tree (``make -C base-mlx_amd``) to
+``base-mlx_amd/lib/libbmx.so``.  There is no fallback: if the library is
+missing, every call raises :class:`BmxNotBuilt`.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.normpath(os.path.join(_HERE, "..", "lib", "libbmx.so"))
+
+BMX_OK = 0
+BMX_E_ARG = -1
+BMX_E_SHAPE = -2
+BMX_E_UNSUPPORTED = -3
+BMX_E_KV_CAPACITY = -4
+BMX_E_ALLOC = -5
+BMX_E_ALIGN = -6
+
+_ERR_NAMES = {
+    BMX_E_ARG: "BMX_E_ARG",
+    BMX_E_SHAPE: "BMX_E_SHAPE",
+    BMX_E_UNSUPPORTED: "BMX_E_UNSUPPORTED",
+    BMX_E_KV_CAPACITY: "BMX_E_KV_CAPACITY",
+    BMX_E_ALLOC: "BMX_E_ALLOC",
+    BMX_E_ALIGN: "BMX_E_ALIGN",
+}
+
+
+class BmxNotBuilt(RuntimeError):
+    """libbmx.so is not present: build it with ``make -C base-mlx_amd``."""
+
+
+class BmxError(RuntimeError):
+    """A non-zero return code from the C ABI (mirrors Error::Inference)."""
+
+    def __init__(self, code: int, message: str):
+        self.code = code
+        name = _ERR_NAMES.get(code, f"hipError_t {code}" if code > 0 else str(code))
+        super().__init__(f"{name}: {message}")
+
+
+_lock = threading.Lock()
+_lib = None
+
+c_p = ctypes.c_void_p
+c_i64 = ctypes.c_int64
+c_int = ctypes.c_int
+c_u64 = ctypes.c_uint64
+c_f = ctypes.c_float
+
+# name -> (restype, argtypes); every symbol declared in include/bmx.h
+SIGNATURES = {
+    "bmx_last_error": (ctypes.c_char_p, []),
+    "bmx_abi_version": (c_int, []),
+    "bmx_qmatmul_affine": (c_int, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_int, c_int, c_p]),
+    "bmx_dequantize_affine": (c_int, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_int, c_int, c_p]),
+    "bmx_dequant_gather": (c_int, [c_p, c_i64, c_i64, c_p, c_p, c_p, c_p, c_i64, c_int, c_int, c_p]),
+    "bmx_init_qlinear": (c_int, [c_u64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p]),
+    "bmx_fill_normal_bf16": (c_int, [c_u64, c_i64, c_f, c_p, c_p]),
+}
+
+
+def load():
+    """Load libbmx.so once and attach signatures; raise if it is not built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise BmxNotBuilt(f"{LIB_PATH} not found; run `make -C base-mlx_amd`")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    return load().bmx_last_error().decode("utf-8", "replace")
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise BmxError(rc, last_error())
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))

@@ -1,0 +1,59 @@
+// C-ABI entry points for the quantized matmul and the library's error state.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "bmx_device.h"
+
+namespace bmx {
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return BMX_OK;
+  return set_error(static_cast<int>(e), "%s: %s", what, hipGetErrorString(e));
+}
+
+int check_launch(const char* what) { return check_hip(hipGetLastError(), what); }
+
+}  // namespace bmx
+
+using namespace bmx;
+
+extern "C" const char* bmx_last_error(void) { return g_last_error; }
+
+extern "C" int bmx_abi_version(void) { return (1 << 16) | 0; }
+
+extern "C" int bmx_qmatmul_affine(const bmx_bf16* x, const uint32_t* w, const bmx_bf16* scales,
+                                  const bmx_bf16* biases, bmx_bf16* y, int64_t M, int64_t N, int64_t K,
+                                  int group_size, int bits, void* stream) {
+  if (bits != 4 || group_size != 64)
+    return set_error(BMX_E_UNSUPPORTED, "qmatmul: only bits=4, group_size=64 (got %d, %d)", bits, group_size);
+  if (!x || !w || !scales || !biases || !y) return set_error(BMX_E_ARG, "qmatmul: null pointer");
+  if (M < 0 || N <= 0 || K <= 0 || K % 64 || N > INT32_MAX || K > INT32_MAX)
+    return set_error(BMX_E_SHAPE, "qmatmul: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
+                     (long long)K);
+  if (M == 0) return BMX_OK;
+  QmvParams p{};
+  p.ldx = K;
+  p.nseg = 1;
+  p.N = static_cast<int>(N);
+  p.K = static_cast<int>(K);
+  p.seg[0] = QmvSegment{w, scales, biases, y, static_cast<int>(N), 0};
+  for (int64_t m0 = 0; m0 < M; m0 += 8) {
+    p.x = x + m0 * K;
+    p.m = static_cast<int>(M - m0 < 8 ? M - m0 : 8);
+    p.seg[0].y = y + m0 * N;
+    if (int rc = launch_qmv(p, QMV_STORE, as_stream(stream))) return rc;
+  }
+  return BMX_OK;
+}

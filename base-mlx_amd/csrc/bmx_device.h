@@ -1,0 +1,54 @@
+// Device-side helpers shared by the bmx HIP kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bmx_internal.h"
+
+namespace bmx {
+
+// bf16 is carried as raw uint16_t bits everywhere.
+__device__ __forceinline__ float bf2f(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+// f32 -> bf16, round to nearest even; NaN stays a (quiet) NaN.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+// acc + a.lo*b.lo + a.hi*b.hi with bf16 operands and an fp32 accumulator
+// (v_dot2c_f32_bf16).  bf16 x bf16 products are exact in fp32.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum_xor(T v, int width) {
+  for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Same counter-based generator as the oracle (splitmix64 finalizer).
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint64_t rand64_mixed(uint64_t mixed_seed, uint64_t idx) {
+  return mix64(mixed_seed + (idx + 1u) * 0x9E3779B97F4A7C15ull);
+}
+__device__ __forceinline__ int32_t irwin4(uint64_t r) {
+  return static_cast<int32_t>((r & 0xffffu) + ((r >> 16) & 0xffffu) +
+                              ((r >> 32) & 0xffffu) + ((r >> 48) & 0xffffu)) -
+         131070;
+}
+
+}  // namespace bmx
