@@ -43,7 +43,8 @@ struct QmvParams {
   const uint16_t* res;     // QMV_RESIDUAL: [M, N] added to the product (may alias y)
   const uint16_t* norm_w;  // optional fused RMSNorm of x: weight [K]
   float eps;
-  int kp;  // K columns staged in LDS per phase (multiple of 64)
+  int kp;      // K columns staged in LDS per phase (set by launch_qmv)
+  int sb_vec;  // s/b staged with 16-byte loads (set by launch_qmv)
 };
 
 // Validates shapes/alignment and launches the qmv kernel family.

@@ -8,19 +8,24 @@
 //   y[m,n] = sum_g s[n,g] * sum_{k in g} q[n,k] x[m,k] + b[n,g] * sum_{k in g} x[m,k]
 // with fp32 accumulation and a bf16 result.
 //
-// Work decomposition.  A wave owns 64/S output rows; each row is served by
-// S lanes that stride over the row's 64-wide groups.  Per group a lane
-// issues two 16-byte loads of packed W (64 nibbles) and one bf16 load each
-// of s and b.  x is staged once per workgroup in LDS, pair-permuted so that
-// the nibble pairs (q_e, q_{e+4}) of a packed word line up with
-// (x_e, x_{e+4}):
-//   (w & 0x000F000F) | 0x43004300  ==  bf16 pair (128 + q0, 128 + q4)
-// which feeds v_dot2c_f32_bf16 directly.  The +128 offset is removed per
-// group with the precomputed group sum Sx:
-//   sum_k q x = D - 128 Sx,  so  y += s * D + (b - 128 s) * Sx.
-// Each x chunk of 64 bytes occupies 80 bytes of LDS so that the 16-byte
-// reads of 8 consecutive lanes land in distinct banks.  Lanes of a row are
-// reduced with cross-lane xor shuffles.
+// Work decomposition.  A workgroup owns RB = 4 * 64/S consecutive output
+// rows; each row is served by S lanes of one wave that stride over the
+// row's 16-byte chunks of packed W (32 nibbles, half a 64-wide group), so
+// S consecutive lanes read S*16 contiguous bytes of a row per load.  The
+// main loop issues exactly one vector-memory instruction per 16 bytes of W:
+// everything else it needs comes from LDS, staged once per workgroup with
+// 16-byte loads --
+//   * x, pair-permuted so that the nibble pairs (q_e, q_{e+4}) of a packed
+//     word line up with (x_e, x_{e+4}):
+//       (w & 0x000F000F) | 0x43004300 == bf16 pair (128 + q0, 128 + q4)
+//     which feeds v_dot2c_f32_bf16 directly;
+//   * per-chunk sums Sx, which remove the +128 offset:
+//       sum_k q x = D - 128 Sx,  so  y += s * D + (b - 128 s) * Sx;
+//   * the workgroup's rows of s and b, interleaved as (s | b << 16).
+// W loads run U chunks ahead in a register ring; the first U are issued
+// before the staging so HBM latency overlaps it.  Each 64-byte x chunk
+// occupies 80 bytes of LDS so the 16-byte reads of 8 consecutive lanes
+// land in distinct banks.  Lanes of a row are reduced with xor shuffles.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -29,6 +34,8 @@
 
 namespace bmx {
 namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kChunkBytes = 80;  // 64 data bytes + 16 pad per 32 x values
@@ -60,40 +67,68 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NH = (EPI == QMV_SWIGLU) ? 2 : 1;  // weight rows per lane
   constexpr int SLOTS = 64 / S;
+  constexpr int RB = (kThreads / 64) * SLOTS;  // rows per workgroup
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int slot = lane / S;
   const int sl = lane % S;
   const int M = p.m;
   const int K = p.K;
+  const int G = K / 64;
   const int CP = p.kp / 32;  // x chunks per phase
   const int GP = p.kp / 64;  // groups per phase
-  unsigned char* xs = smem;
-  float* sxs = reinterpret_cast<float*>(smem + MT * CP * kChunkBytes);
-  float* red = sxs + MT * GP;  // [4 waves][MT] for the RMSNorm prologue
+  unsigned char* xs = smem;                                                 // [MT][CP] x 80 B
+  float* sxs = reinterpret_cast<float*>(smem + MT * CP * kChunkBytes);      // [MT][CP]
+  uint32_t* sbs = reinterpret_cast<uint32_t*>(sxs + MT * CP);               // [NH][RB][GP]
+  float* red = reinterpret_cast<float*>(sbs + NH * RB * GP);                // [4][MT]
 
-  const int row = (blockIdx.x * (kThreads / 64) + wave) * SLOTS + slot;
+  const int row0 = blockIdx.x * RB;
+  const int rl = wave * SLOTS + slot;  // row within the workgroup
+  const int row = row0 + rl;
   const bool valid = row < p.N;
-  const int rr = valid ? row : 0;
 
+  // segment + local row of a global output row
+  auto seg_of = [&](int r) {
+    int sg = 0;
+    if (EPI != QMV_SWIGLU) {
+      if (p.nseg > 1 && r >= p.seg[1].row0) sg = 1;
+      if (p.nseg > 2 && r >= p.seg[2].row0) sg = 2;
+    }
+    return sg;
+  };
   const uint32_t* wrow[NH];
-  const uint16_t* srow[NH];
-  const uint16_t* brow[NH];
   int seg = 0;
-  if (EPI == QMV_SWIGLU) {
+  {
+    const int rr = valid ? row : 0;
+    if constexpr (EPI == QMV_SWIGLU) {
+#pragma unroll
+      for (int h = 0; h < NH; h++) wrow[h] = p.seg[h].w + static_cast<int64_t>(rr) * (K / 8);
+    } else {
+      seg = seg_of(rr);
+      wrow[0] = p.seg[seg].w + static_cast<int64_t>(rr - p.seg[seg].row0) * (K / 8);
+    }
+  }
+
+  // Register ring of U chunks (see header).
+  constexpr int U = (NH == 1 && MT == 1) ? 8 : 4;
+  constexpr int XU = 4;  // x words per thread per staging batch
+  constexpr int SU = 2;  // s|b units per thread per staging batch
+  uint4 wv[U][NH];
+  auto load_chunk = [&](int u, int c) {
 #pragma unroll
     for (int h = 0; h < NH; h++) {
-      wrow[h] = p.seg[h].w + static_cast<int64_t>(rr) * (K / 8);
-      srow[h] = p.seg[h].s + static_cast<int64_t>(rr) * (K / 64);
-      brow[h] = p.seg[h].b + static_cast<int64_t>(rr) * (K / 64);
+      // W is streamed exactly once: nontemporal loads keep it out of the way
+      const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[h] + c * 4));
+      wv[u][h] = make_uint4(t.x, t.y, t.z, t.w);
     }
-  } else {
-    if (p.nseg > 1 && rr >= p.seg[1].row0) seg = 1;
-    if (p.nseg > 2 && rr >= p.seg[2].row0) seg = 2;
-    const int lr = rr - p.seg[seg].row0;
-    wrow[0] = p.seg[seg].w + static_cast<int64_t>(lr) * (K / 8);
-    srow[0] = p.seg[seg].s + static_cast<int64_t>(lr) * (K / 64);
-    brow[0] = p.seg[seg].b + static_cast<int64_t>(lr) * (K / 64);
+  };
+  // the first phase's loads go out before anything else
+  {
+    const int nc0 = min(p.kp, K) / 32;
+    const int n_i0 = sl < nc0 ? (nc0 - sl + S - 1) / S : 0;
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (u < n_i0) load_chunk(u, sl + S * u);
   }
 
   // Optional fused RMSNorm of x (fast::rms_norm, qwen3.rs:50-55):
@@ -135,106 +170,166 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
 #pragma unroll
     for (int m = 0; m < MT; m++) acc[h][m] = 0.0f;
 
-  // Register ring of U groups: loads for the first U groups of a phase are
-  // issued before x is staged, so HBM latency overlaps the staging.
-  constexpr int U = (NH == 1 && MT == 1) ? 4 : 2;
-  uint4 wv[U][NH][2];
-  float sv[U][NH], bv[U][NH];
-  auto load_group = [&](int u, int gk) {
-#pragma unroll
-    for (int h = 0; h < NH; h++) {
-      const uint4* wp = reinterpret_cast<const uint4*>(wrow[h] + gk * 8);
-      wv[u][h][0] = wp[0];
-      wv[u][h][1] = wp[1];
-      sv[u][h] = bf2f(srow[h][gk]);
-      bv[u][h] = bf2f(brow[h][gk]);
-    }
-  };
-
   for (int k0 = 0; k0 < K; k0 += p.kp) {
     const int kpp = min(p.kp, K - k0);
     const int words = kpp / 8;  // multiple of 8
     const int total = MT * words;
-    const int gpp = kpp / 64;
+    const int ncp = kpp / 32;   // chunks in this phase
+    const int gpp = kpp / 64;   // groups in this phase
+    const int cbase = k0 / 32;
     const int gbase = k0 / 64;
-    const int n_i = sl < gpp ? (gpp - sl + S - 1) / S : 0;  // groups of this lane
+    const int n_i = sl < ncp ? (ncp - sl + S - 1) / S : 0;  // chunks of this lane
+    if (k0 > 0) {
 #pragma unroll
-    for (int u = 0; u < U; u++)
-      if (u < n_i) load_group(u, gbase + sl + S * u);
+      for (int u = 0; u < U; u++)
+        if (u < n_i) load_chunk(u, cbase + sl + S * u);
+    }
     __syncthreads();  // previous phase finished reading LDS
-    // ---- stage x[:, k0:k0+kpp] pair-permuted, plus group sums ----
-    for (int base = 0; base < total; base += kThreads) {
-      const int idx = base + threadIdx.x;
-      const bool act = idx < total;
-      const int m = act ? idx / words : 0;
-      const int j = act ? idx - m * words : 0;
-      uint4 d = make_uint4(0, 0, 0, 0);
-      float part = 0.0f;
-      if (act && m < M) {
-        const int k = k0 + j * 8;
-        d = *reinterpret_cast<const uint4*>(p.x + m * p.ldx + k);
-        if (p.norm_w != nullptr) {
-          uint4 wn = *reinterpret_cast<const uint4*>(p.norm_w + k);
-          uint32_t dv[4] = {d.x, d.y, d.z, d.w}, wq[4] = {wn.x, wn.y, wn.z, wn.w};
+    // ---- stage x[:, k0:k0+kpp] (pair-permuted, chunk sums) and the
+    //      workgroup's s|b words.  Each batch issues all of its loads before
+    //      consuming any, so their latencies overlap (and overlap W). ----
+    const int gunits = gpp / 8;  // 16-byte s/b units per row
+    const int sb_units = p.sb_vec ? NH * RB * gunits : NH * RB * gpp;
+    for (int b0x = 0, b0s = 0; b0x < total || b0s < sb_units; b0x += kThreads * XU, b0s += kThreads * SU) {
+      uint4 xr[XU];
+      uint4 sr[SU], br[SU];
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            float lo = bf2f(wq[i] & 0xffffu) * round_bf(bf2f(dv[i] & 0xffffu) * inv[m]);
-            float hi = bf2f(wq[i] >> 16) * round_bf(bf2f(dv[i] >> 16) * inv[m]);
-            dv[i] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
-          }
-          d = make_uint4(dv[0], dv[1], dv[2], dv[3]);
+      for (int i = 0; i < XU; i++) {
+        const int idx = b0x + i * kThreads + threadIdx.x;
+        xr[i] = make_uint4(0, 0, 0, 0);
+        if (idx < total) {
+          const int m = idx / words;
+          if (m < M) xr[i] = *reinterpret_cast<const uint4*>(p.x + m * p.ldx + k0 + (idx - m * words) * 8);
         }
-        uint32_t dv[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) part += bf2f(dv[i] & 0xffffu) + bf2f(dv[i] >> 16);
       }
-      // group of 64 values = 8 consecutive words = 8 consecutive lanes
-      part += __shfl_xor(part, 1, 64);
-      part += __shfl_xor(part, 2, 64);
-      part += __shfl_xor(part, 4, 64);
-      if (act) {
-        *reinterpret_cast<uint4*>(xs + (m * CP + (j >> 2)) * kChunkBytes + (j & 3) * 16) =
-            permute_pairs(d);
-        if ((j & 7) == 0) sxs[m * GP + (j >> 3)] = part;
+      if (p.sb_vec) {
+#pragma unroll
+        for (int i = 0; i < SU; i++) {
+          const int e = b0s + i * kThreads + threadIdx.x;
+          if (e < sb_units) {
+            const int h = e / (RB * gunits);
+            const int rem = e - h * (RB * gunits);
+            const int r = rem / gunits;
+            const int gr = row0 + r;
+            if (gr < p.N) {
+              const int sg = (EPI == QMV_SWIGLU) ? h : seg_of(gr);
+              const int64_t off = static_cast<int64_t>(gr - (EPI == QMV_SWIGLU ? 0 : p.seg[sg].row0)) * G +
+                                  gbase + (rem - r * gunits) * 8;
+              sr[i] = *reinterpret_cast<const uint4*>(p.seg[sg].s + off);
+              br[i] = *reinterpret_cast<const uint4*>(p.seg[sg].b + off);
+            }
+          }
+        }
+      }
+      // consume x
+#pragma unroll
+      for (int i = 0; i < XU; i++) {
+        const int idx = b0x + i * kThreads + threadIdx.x;
+        const bool act = idx < total;
+        const int m = act ? idx / words : 0;
+        const int j = act ? idx - m * words : 0;
+        uint4 d = xr[i];
+        float part = 0.0f;
+        if (act && m < M) {
+          if (p.norm_w != nullptr) {
+            const uint4 wn = *reinterpret_cast<const uint4*>(p.norm_w + k0 + j * 8);
+            uint32_t dv[4] = {d.x, d.y, d.z, d.w}, wq[4] = {wn.x, wn.y, wn.z, wn.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              float lo = bf2f(wq[q] & 0xffffu) * round_bf(bf2f(dv[q] & 0xffffu) * inv[m]);
+              float hi = bf2f(wq[q] >> 16) * round_bf(bf2f(dv[q] >> 16) * inv[m]);
+              dv[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+            }
+            d = make_uint4(dv[0], dv[1], dv[2], dv[3]);
+          }
+          const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+          for (int q = 0; q < 4; q++) part += bf2f(dv[q] & 0xffffu) + bf2f(dv[q] >> 16);
+        }
+        // chunk of 32 values = 4 consecutive words = 4 consecutive lanes
+        part += __shfl_xor(part, 1, 64);
+        part += __shfl_xor(part, 2, 64);
+        if (act) {
+          *reinterpret_cast<uint4*>(xs + (m * CP + (j >> 2)) * kChunkBytes + (j & 3) * 16) = permute_pairs(d);
+          if ((j & 3) == 0) sxs[m * CP + (j >> 2)] = part;
+        }
+      }
+      // consume s|b
+      if (p.sb_vec) {
+#pragma unroll
+        for (int i = 0; i < SU; i++) {
+          const int e = b0s + i * kThreads + threadIdx.x;
+          if (e < sb_units) {
+            const int h = e / (RB * gunits);
+            const int rem = e - h * (RB * gunits);
+            const int r = rem / gunits;
+            if (row0 + r < p.N) {
+              const uint32_t s4[4] = {sr[i].x, sr[i].y, sr[i].z, sr[i].w};
+              const uint32_t b4[4] = {br[i].x, br[i].y, br[i].z, br[i].w};
+              uint32_t* dst = sbs + (h * RB + r) * GP + (rem - r * gunits) * 8;
+#pragma unroll
+              for (int q = 0; q < 4; q++) {
+                dst[2 * q] = (s4[q] & 0xffffu) | (b4[q] << 16);
+                dst[2 * q + 1] = (s4[q] >> 16) | (b4[q] & 0xffff0000u);
+              }
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < SU; i++) {
+          const int e = b0s + i * kThreads + threadIdx.x;
+          if (e < sb_units) {
+            const int h = e / (RB * gpp);
+            const int rem = e - h * (RB * gpp);
+            const int r = rem / gpp;
+            const int g = rem - r * gpp;
+            const int gr = row0 + r;
+            if (gr < p.N) {
+              const int sg = (EPI == QMV_SWIGLU) ? h : seg_of(gr);
+              const int64_t off = static_cast<int64_t>(gr - (EPI == QMV_SWIGLU ? 0 : p.seg[sg].row0)) * G + gbase + g;
+              sbs[(h * RB + r) * GP + g] = static_cast<uint32_t>(p.seg[sg].s[off]) |
+                                           (static_cast<uint32_t>(p.seg[sg].b[off]) << 16);
+            }
+          }
+        }
       }
     }
     __syncthreads();
 
-    // ---- stream W over this phase's groups ----
+    // ---- stream W over this phase's chunks ----
     for (int i0 = 0; i0 < n_i; i0 += U) {
 #pragma unroll
       for (int u = 0; u < U; u++) {
         const int i = i0 + u;
         if (i < n_i) {
-          const int g = sl + S * i;
-          float bb[NH];
+          const int c = sl + S * i;  // chunk within the phase
+          float sv[NH], bb[NH];
 #pragma unroll
-          for (int h = 0; h < NH; h++) bb[h] = bv[u][h] - 128.0f * sv[u][h];
+          for (int h = 0; h < NH; h++) {
+            const uint32_t sb = sbs[(h * RB + rl) * GP + (c >> 1)];
+            sv[h] = bf2f(sb & 0xffffu);
+            bb[h] = bf2f(sb >> 16) - 128.0f * sv[h];
+          }
 #pragma unroll
           for (int m = 0; m < MT; m++) {
             if (m < M) {
-              const unsigned char* c0 = xs + (m * CP + 2 * g) * kChunkBytes;
-              const uint4* x0 = reinterpret_cast<const uint4*>(c0);
-              const uint4* x1 = reinterpret_cast<const uint4*>(c0 + kChunkBytes);
-              uint4 xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-              const float sx = sxs[m * GP + g];
+              const uint4* xp = reinterpret_cast<const uint4*>(xs + (m * CP + c) * kChunkBytes);
+              const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+              const float sx = sxs[m * CP + c];
 #pragma unroll
               for (int h = 0; h < NH; h++) {
                 float d = 0.0f;
-                d = word_dot(wv[u][h][0].x, xv[0], d);
-                d = word_dot(wv[u][h][0].y, xv[1], d);
-                d = word_dot(wv[u][h][0].z, xv[2], d);
-                d = word_dot(wv[u][h][0].w, xv[3], d);
-                d = word_dot(wv[u][h][1].x, xv[4], d);
-                d = word_dot(wv[u][h][1].y, xv[5], d);
-                d = word_dot(wv[u][h][1].z, xv[6], d);
-                d = word_dot(wv[u][h][1].w, xv[7], d);
-                acc[h][m] += sv[u][h] * d;
+                d = word_dot(wv[u][h].x, x0, d);
+                d = word_dot(wv[u][h].y, x1, d);
+                d = word_dot(wv[u][h].z, x2, d);
+                d = word_dot(wv[u][h].w, x3, d);
+                acc[h][m] += sv[h] * d;
                 acc[h][m] += bb[h] * sx;
               }
             }
           }
-          if (i + U < n_i) load_group(u, gbase + g + S * U);
+          if (i + U < n_i) load_chunk(u, cbase + c + S * U);
         }
       }
     }
@@ -250,10 +345,10 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
 #pragma unroll
     for (int m = 0; m < MT; m++) {
       if (m >= M) break;
-      if (EPI == QMV_STORE) {
+      if constexpr (EPI == QMV_STORE) {
         const QmvSegment& sg = p.seg[seg];
         sg.y[static_cast<int64_t>(m) * sg.rows + (row - sg.row0)] = f2bf(acc[0][m]);
-      } else if (EPI == QMV_RESIDUAL) {
+      } else if constexpr (EPI == QMV_RESIDUAL) {
         // x = x + o_proj(attn) in bf16 (qwen3.rs:520-521, 541)
         const int64_t o = static_cast<int64_t>(m) * p.N + row;
         const float r = bf2f(p.res[o]);
@@ -261,7 +356,7 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
       } else {
         // silu(gate) * up, each MLX op rounding to bf16 (kernels.rs:73-74)
         const float g = round_bf(acc[0][m]);
-        const float u = round_bf(acc[1][m]);
+        const float u = round_bf(acc[NH - 1][m]);
         const float sg = round_bf(1.0f / (1.0f + expf(-g)));
         const float a = round_bf(g * sg);
         p.seg[0].y[static_cast<int64_t>(m) * p.N + row] = f2bf(a * u);
@@ -303,12 +398,12 @@ int launch_epi(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t ld
 // Lanes per row: balance lane utilisation (groups per row vs S) against
 // the number of waves the launch puts on the 256 CUs.
 int pick_lanes_per_row(int N, int K) {
-  const int G = K / 64;
+  const int C = K / 32;  // 16-byte chunks per row
   int best = 64;
   double best_score = -1.0;
   for (int S = 8; S <= 64; S *= 2) {
-    const int iters = (G + S - 1) / S;
-    const double util = static_cast<double>(G) / (static_cast<double>(S) * iters);
+    const int iters = (C + S - 1) / S;
+    const double util = static_cast<double>(C) / (static_cast<double>(S) * iters);
     const double waves = static_cast<double>(N) * S / 64.0;
     const double fill = std::min(1.0, waves / 2048.0);
     const double score = util * fill;
@@ -335,21 +430,28 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
     if (!aligned(p.seg[i].w, 16)) return set_error(BMX_E_ALIGN, "qmv: W must be 16-byte aligned");
   }
   int mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : p.m <= 5 ? 5 : 8;
-  // LDS per phase: MT * kp * (80/32 + 4/64) bytes
-  int kp = static_cast<int>(kLdsBudget / (mt * 2.5625));
-  kp = std::max(64, (kp / 64) * 64);
-  p.kp = std::min(kp, p.K);
-  const int CP = p.kp / 32, GP = p.kp / 64;
-  const size_t lds = static_cast<size_t>(mt) * CP * kChunkBytes + static_cast<size_t>(mt) * GP * 4 +
-                     4 * static_cast<size_t>(mt) * 4;
-  int S = (mt == 1) ? pick_lanes_per_row(p.N, p.K) : (p.K / 64 >= 64 ? 64 : 16);
+  int S = (mt == 1) ? pick_lanes_per_row(p.N, p.K) : (p.K / 32 >= 64 ? 64 : 16);
   // Tuning override: BMX_QMV_LANES = lanes per output row (8/16/32/64).
   if (const char* e = getenv("BMX_QMV_LANES")) {
     const int v = atoi(e);
     if (v == 16 || v == 64 || (mt == 1 && (v == 8 || v == 32))) S = v;
   }
+  const int nh = epi == QMV_SWIGLU ? 2 : 1;
   const int rows_per_block = (kThreads / 64) * (64 / S);
+  // LDS per phase: x chunks (80 B + 4 B sum per 32 columns per x row) and
+  // the workgroup's s|b words (4 B per 64 columns per weight row).
+  const double per_col = mt * (kChunkBytes + 4) / 32.0 + nh * rows_per_block * 4 / 64.0;
+  int kp = static_cast<int>(kLdsBudget / per_col);
+  kp = std::max(512, (kp / 512) * 512);
+  p.kp = std::min(kp, p.K);
+  const int CP = p.kp / 32, GP = p.kp / 64;
+  const size_t lds = static_cast<size_t>(mt) * CP * (kChunkBytes + 4) +
+                     static_cast<size_t>(nh) * rows_per_block * GP * 4 + 4 * static_cast<size_t>(mt) * 4;
   const int blocks = (p.N + rows_per_block - 1) / rows_per_block;
+  // 16-byte staging of s/b needs whole 8-group units at 16-byte alignment
+  p.sb_vec = (p.K % 512) == 0;
+  for (int i = 0; i < p.nseg; i++)
+    p.sb_vec = p.sb_vec && aligned(p.seg[i].s, 16) && aligned(p.seg[i].b, 16);
   switch (mt) {
     case 1: return launch_epi<1>(epi, S, p, blocks, lds, stream);
     case 2: return launch_epi<2>(epi, S, p, blocks, lds, stream);
