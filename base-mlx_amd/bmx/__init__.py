@@ -131,3 +131,269 @@ def fill_normal_bf16(seed: int, shape, sigma: float = 1.0, device="cuda", stream
     call("bmx_fill_normal_bf16", ctypes.c_uint64(seed), out.numel(), ctypes.c_float(sigma_to_c(sigma)), _ptr(out),
          _stream(stream))
     return out
+
+
+# ---------------------------------------------------------------------------
+# ops around the matmul
+# ---------------------------------------------------------------------------
+def rms_norm(x, w, eps=1e-6, out=None, stream=None):
+    """fast::rms_norm over the last axis (bf16)."""
+    torch = _torch()
+    _require_cuda(x, w)
+    out = torch.empty_like(x) if out is None else out
+    dim = x.shape[-1]
+    call("bmx_rms_norm", _ptr(x), _ptr(w), _ptr(out), x.numel() // dim, dim, ctypes.c_float(eps), _stream(stream))
+    return out
+
+
+def rope(x, theta, offset, out=None, stream=None):
+    """fast::rope(x [H, T, D], D, traditional=False, theta, 1.0, offset)."""
+    torch = _torch()
+    _require_cuda(x)
+    H, T, D = x.shape
+    out = torch.empty_like(x) if out is None else out
+    call("bmx_rope", _ptr(x), _ptr(out), H, T, D, ctypes.c_float(theta), offset, _stream(stream))
+    return out
+
+
+def slice_update(src, update, start, stop, strides, stream=None):
+    """mlx_ext::slice_update: src[start:stop:strides] = update, in place; returns src."""
+    import numpy as np
+
+    _require_cuda(src, update)
+    nd = src.dim()
+    arrs = [np.ascontiguousarray(a, np.int64) for a in (list(src.shape), start, stop, strides)]
+    if any(a.size != nd for a in arrs):
+        raise BmxError(BMX_E_ARG, "start/stop/strides must have one entry per axis")
+    p = [a.ctypes.data_as(ctypes.c_void_p) for a in arrs]
+    call("bmx_slice_update", _ptr(src), nd, p[0], _ptr(update), p[1], p[2], p[3], _stream(stream))
+    return src
+
+
+def qk_norm_rope_kv(q, k, v, q_norm, k_norm, k_cache, v_cache, offset, eps=1e-6, theta=1e6, stream=None):
+    """Fused QK-norm + RoPE + KV write; returns q_out [Hq, M, 128]."""
+    torch = _torch()
+    _require_cuda(q, k, v, q_norm, k_norm, k_cache, v_cache)
+    Hkv, cap, D = k_cache.shape
+    M = q.shape[0]
+    Hq = q.shape[-1] // D
+    q_out = torch.empty(Hq, M, D, dtype=torch.bfloat16, device=q.device)
+    call("bmx_qk_norm_rope_kv", _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm), _ptr(q_out), _ptr(k_cache),
+         _ptr(v_cache), M, Hq, Hkv, D, cap, offset, ctypes.c_float(eps), ctypes.c_float(theta), _stream(stream))
+    return q_out
+
+
+def attention(q, k_cache, v_cache, offset, scale=None, use_workspace=True, stream=None):
+    """GQA SDPA of q [Hq, M, D] over cache rows [0, offset + M); returns [M, Hq*D]."""
+    torch = _torch()
+    _require_cuda(q, k_cache, v_cache)
+    Hq, M, D = q.shape
+    Hkv, cap, _ = k_cache.shape
+    scale = 1.0 / (D ** 0.5) if scale is None else scale
+    out = torch.empty(M, Hq * D, dtype=torch.bfloat16, device=q.device)
+    nbytes = load().bmx_attention_workspace_bytes(Hq, M) if use_workspace else 0
+    ws = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=q.device) if use_workspace else None
+    call("bmx_attention_gqa", _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), Hq, Hkv, M, D, cap, offset,
+         ctypes.c_float(scale), _ptr(ws), nbytes, _stream(stream))
+    return out
+
+
+def argmax_rows(x, stream=None):
+    torch = _torch()
+    _require_cuda(x)
+    n = x.shape[-1]
+    out = torch.empty(x.numel() // n, dtype=torch.int32, device=x.device)
+    call("bmx_argmax_rows", _ptr(x), x.numel() // n, n, _ptr(out), _stream(stream))
+    return out
+
+
+def silu_mul(g, u, stream=None):
+    torch = _torch()
+    _require_cuda(g, u)
+    y = torch.empty_like(g)
+    call("bmx_silu_mul", _ptr(g), _ptr(u), _ptr(y), g.numel(), _stream(stream))
+    return y
+
+
+def add(a, b, stream=None):
+    torch = _torch()
+    _require_cuda(a, b)
+    y = torch.empty_like(a)
+    call("bmx_add", _ptr(a), _ptr(b), _ptr(y), a.numel(), _stream(stream))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# Qwen3 model / KV cache / generation (host mirror of the reference's
+# Qwen3, KvCache, LoadedModel::generate_text and speculative::generate)
+# ---------------------------------------------------------------------------
+class Qwen3Config(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in
+                ("hidden", "inter", "layers", "n_heads", "n_kv_heads", "head_dim", "vocab", "tied",
+                 "group_size", "bits")] + [("eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+
+def qwen3_config(hidden, inter, layers, n_heads, n_kv_heads, head_dim=128, vocab=151936, tied=1, eps=1e-6,
+                 rope_theta=1e6):
+    return Qwen3Config(hidden, inter, layers, n_heads, n_kv_heads, head_dim, vocab, tied, 64, 4, eps, rope_theta)
+
+
+# Qwen3-shaped configurations of the benchmark workloads
+QWEN3_0_6B = dict(hidden=1024, inter=3072, layers=28, n_heads=16, n_kv_heads=8)
+QWEN3_4B = dict(hidden=2560, inter=9728, layers=36, n_heads=32, n_kv_heads=8)
+QWEN3_8B = dict(hidden=4096, inter=12288, layers=36, n_heads=32, n_kv_heads=8)
+QWEN3_32B = dict(hidden=5120, inter=25600, layers=64, n_heads=64, n_kv_heads=8, tied=0)
+
+_HIP = None
+
+
+def _hip():
+    global _HIP
+    if _HIP is None:
+        _HIP = ctypes.CDLL("libamdhip64.so")
+        _HIP.hipMemcpy.restype = ctypes.c_int
+        _HIP.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    return _HIP
+
+
+def device_to_numpy(ptr, shape, dtype):
+    """Copy `shape` elements of `dtype` at device address `ptr` into a numpy array."""
+    import numpy as np
+
+    out = np.empty(shape, dtype)
+    rc = _hip().hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ptr), out.nbytes, 2)
+    if rc != 0:
+        raise BmxError(rc, "hipMemcpy device->host failed")
+    return out
+
+
+class KvCache:
+    """bmx_kv_cache: [layers, 2, n_kv_heads, capacity, 128] bf16 on the GPU."""
+
+    def __init__(self, model, capacity):
+        self.model = model
+        h = ctypes.c_void_p()
+        call("bmx_kv_create", model.h, capacity, ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            load().bmx_kv_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def seq_len(self):
+        return load().bmx_kv_seq_len(self.h)
+
+    @property
+    def capacity(self):
+        return load().bmx_kv_capacity(self.h)
+
+    def reset(self):
+        load().bmx_kv_reset(self.h)
+
+    def truncate(self, target):
+        load().bmx_kv_truncate(self.h, target)
+
+    def fill_synthetic(self, seed, seq_len, stream=None):
+        call("bmx_kv_fill_synthetic", self.h, ctypes.c_uint64(seed), seq_len, _stream(stream))
+
+    def layer_numpy(self, layer, kv):
+        """Host copy of K (kv=0) or V (kv=1) of one layer: [n_kv_heads, capacity, 128] uint16."""
+        import numpy as np
+
+        c = self.model.cfg
+        cap = self.capacity
+        n = c.n_kv_heads * cap * c.head_dim
+        base = load().bmx_kv_data(self.h) + 2 * n * (2 * layer + kv)
+        return device_to_numpy(base, (c.n_kv_heads, cap, c.head_dim), np.uint16)
+
+
+class Qwen3:
+    """Random-init Qwen3 on the GPU behind the C ABI (bmx_qwen3_*)."""
+
+    def __init__(self, cfg, seed, sigma=0.02, max_tokens=256):
+        self.cfg = cfg
+        h = ctypes.c_void_p()
+        call("bmx_qwen3_create_random", ctypes.byref(cfg), ctypes.c_uint64(seed), ctypes.c_double(sigma), max_tokens,
+             ctypes.byref(h))
+        self.h = h
+        self.max_tokens = max_tokens
+
+    def close(self):
+        if self.h:
+            load().bmx_qwen3_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def new_cache(self, capacity):
+        return KvCache(self, capacity)
+
+    def qlinear_numpy(self, layer, slot):
+        """Host copies (w uint32, s uint16, b uint16) of one projection."""
+        import numpy as np
+
+        w, s, b = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        N, K = ctypes.c_int(), ctypes.c_int()
+        call("bmx_qwen3_qlinear", self.h, layer, slot, ctypes.byref(w), ctypes.byref(s), ctypes.byref(b),
+             ctypes.byref(N), ctypes.byref(K))
+        n, k = N.value, K.value
+        return (device_to_numpy(w.value, (n, k // 8), np.uint32), device_to_numpy(s.value, (n, k // 64), np.uint16),
+                device_to_numpy(b.value, (n, k // 64), np.uint16))
+
+    def forward(self, cache, tokens, all_logits=False, stream=None):
+        """Qwen3::forward / forward_multi: logits bf16 [vocab] or [M, vocab] (torch, on the GPU)."""
+        import numpy as np
+
+        torch = _torch()
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        M = toks.size
+        out = torch.empty(M if all_logits else 1, self.cfg.vocab, dtype=torch.bfloat16, device="cuda")
+        call("bmx_qwen3_forward", self.h, cache.h, toks.ctypes.data_as(ctypes.c_void_p), M, int(all_logits), _ptr(out),
+             _stream(stream))
+        return out if all_logits else out[0]
+
+    def decode_step(self, cache, token, want_logits=False, stream=None):
+        torch = _torch()
+        nxt = ctypes.c_uint32()
+        out = torch.empty(self.cfg.vocab, dtype=torch.bfloat16, device="cuda") if want_logits else None
+        call("bmx_qwen3_decode_step", self.h, cache.h, ctypes.c_uint32(int(token)), ctypes.byref(nxt), _ptr(out),
+             _stream(stream))
+        return (nxt.value, out) if want_logits else nxt.value
+
+    def generate_greedy(self, cache, prompt, max_new, eos=(151645, 151643), stream=None):
+        import numpy as np
+
+        p = np.ascontiguousarray(prompt, np.uint32)
+        e = np.ascontiguousarray(eos, np.uint32)
+        out = np.empty(max_new, np.uint32)
+        n = ctypes.c_int()
+        call("bmx_generate_greedy", self.h, cache.h, p.ctypes.data_as(ctypes.c_void_p), p.size, max_new,
+             e.ctypes.data_as(ctypes.c_void_p), e.size, out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(n),
+             _stream(stream))
+        return out[: n.value]
+
+
+def speculative_generate(target, tcache, draft, dcache, prompt, max_new, spec_k=5, eos=(151645, 151643), stream=None):
+    import numpy as np
+
+    p = np.ascontiguousarray(prompt, np.uint32)
+    e = np.ascontiguousarray(eos, np.uint32)
+    out = np.empty(max_new + spec_k, np.uint32)
+    n = ctypes.c_int()
+    stats = np.zeros(3, np.int64)
+    call("bmx_speculative_generate", target.h, tcache.h, draft.h, dcache.h, p.ctypes.data_as(ctypes.c_void_p), p.size,
+         max_new, spec_k, e.ctypes.data_as(ctypes.c_void_p), e.size, out.ctypes.data_as(ctypes.c_void_p),
+         ctypes.byref(n), stats.ctypes.data_as(ctypes.c_void_p), _stream(stream))
+    return out[: n.value], stats

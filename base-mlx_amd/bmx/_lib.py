@@ -62,6 +62,33 @@ SIGNATURES = {
     "bmx_dequant_gather": (c_int, [c_p, c_i64, c_i64, c_p, c_p, c_p, c_p, c_i64, c_int, c_int, c_p]),
     "bmx_init_qlinear": (c_int, [c_u64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p]),
     "bmx_fill_normal_bf16": (c_int, [c_u64, c_i64, c_f, c_p, c_p]),
+    "bmx_rms_norm": (c_int, [c_p, c_p, c_p, c_i64, c_i64, c_f, c_p]),
+    "bmx_rope": (c_int, [c_p, c_p, c_i64, c_i64, c_i64, c_f, c_i64, c_p]),
+    "bmx_slice_update": (c_int, [c_p, c_int, c_p, c_p, c_p, c_p, c_p, c_p]),
+    "bmx_qk_norm_rope_kv": (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int,
+                                    c_int, c_f, c_f, c_p]),
+    "bmx_attention_gqa": (c_int, [c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_int, c_f, c_p,
+                                  ctypes.c_size_t, c_p]),
+    "bmx_attention_workspace_bytes": (ctypes.c_size_t, [c_int, c_int]),
+    "bmx_argmax_rows": (c_int, [c_p, c_i64, c_i64, c_p, c_p]),
+    "bmx_silu_mul": (c_int, [c_p, c_p, c_p, c_i64, c_p]),
+    "bmx_add": (c_int, [c_p, c_p, c_p, c_i64, c_p]),
+    "bmx_qwen3_create_random": (c_int, [c_p, c_u64, ctypes.c_double, c_int, c_p]),
+    "bmx_qwen3_destroy": (None, [c_p]),
+    "bmx_qwen3_qlinear": (c_int, [c_p, c_int, c_int, c_p, c_p, c_p, c_p, c_p]),
+    "bmx_kv_create": (c_int, [c_p, c_int, c_p]),
+    "bmx_kv_destroy": (None, [c_p]),
+    "bmx_kv_seq_len": (c_int, [c_p]),
+    "bmx_kv_capacity": (c_int, [c_p]),
+    "bmx_kv_reset": (None, [c_p]),
+    "bmx_kv_truncate": (None, [c_p, c_int]),
+    "bmx_kv_data": (c_p, [c_p]),
+    "bmx_kv_fill_synthetic": (c_int, [c_p, c_u64, c_int, c_p]),
+    "bmx_qwen3_forward": (c_int, [c_p, c_p, c_p, c_int, c_int, c_p, c_p]),
+    "bmx_qwen3_decode_step": (c_int, [c_p, c_p, ctypes.c_uint32, c_p, c_p, c_p]),
+    "bmx_generate_greedy": (c_int, [c_p, c_p, c_p, c_int, c_int, c_p, c_int, c_p, c_p, c_p]),
+    "bmx_speculative_generate": (c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_p, c_int, c_p, c_p, c_p,
+                                         c_p]),
 }
 
 

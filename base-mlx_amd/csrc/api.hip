@@ -43,17 +43,18 @@ extern "C" int bmx_qmatmul_affine(const bmx_bf16* x, const uint32_t* w, const bm
     return set_error(BMX_E_SHAPE, "qmatmul: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
                      (long long)K);
   if (M == 0) return BMX_OK;
+  if (M > 8) {
+    if (M > INT32_MAX) return set_error(BMX_E_SHAPE, "qmatmul: M too large");
+    return launch_qmm(x, w, scales, biases, y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
+                      as_stream(stream));
+  }
   QmvParams p{};
   p.ldx = K;
   p.nseg = 1;
   p.N = static_cast<int>(N);
   p.K = static_cast<int>(K);
   p.seg[0] = QmvSegment{w, scales, biases, y, static_cast<int>(N), 0};
-  for (int64_t m0 = 0; m0 < M; m0 += 8) {
-    p.x = x + m0 * K;
-    p.m = static_cast<int>(M - m0 < 8 ? M - m0 : 8);
-    p.seg[0].y = y + m0 * N;
-    if (int rc = launch_qmv(p, QMV_STORE, as_stream(stream))) return rc;
-  }
-  return BMX_OK;
+  p.x = x;
+  p.m = static_cast<int>(M);
+  return launch_qmv(p, QMV_STORE, as_stream(stream));
 }

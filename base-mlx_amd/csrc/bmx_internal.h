@@ -50,4 +50,34 @@ struct QmvParams {
 // Validates shapes/alignment and launches the qmv kernel family.
 int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream);
 
+// ---- other kernels (one launch each, errors recorded) --------------------
+int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M,
+               int N, int K, hipStream_t stream);
+int launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t rows, int dim, float eps,
+                    hipStream_t stream);
+struct RopeTable {
+  float inv_freq[128];  // theta^(-i/(D/2)), i < D/2 <= 128, evaluated in double
+};
+RopeTable make_rope_table(int D, float theta);
+int launch_qk_norm_rope_kv(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                           const uint16_t* k_norm, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int M,
+                           int Hq, int Hkv, int D, int cap, int offset, const int* offset_dev, float eps,
+                           const RopeTable& tab, hipStream_t stream);
+size_t attention_workspace_floats(int Hq, int M, int ns);
+int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* ws,
+                     size_t ws_floats, int Hq, int Hkv, int M, int D, int cap, int offset, const int* offset_dev,
+                     int L_max, float scale, hipStream_t stream);
+int launch_argmax(const uint16_t* x, int64_t rows, int64_t n, uint32_t* out, hipStream_t stream);
+int launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* y, int64_t n, hipStream_t stream);
+int launch_add(const uint16_t* a, const uint16_t* b, uint16_t* y, int64_t n, hipStream_t stream);
+int launch_tokens_to_ids(const uint32_t* src, int32_t* dst, int n, hipStream_t stream);
+int launch_add_scalar(int* v, int d, hipStream_t stream);
+int launch_dequant_gather(const int32_t* ids, int64_t M, int64_t rows, const uint32_t* w, const uint16_t* s,
+                          const uint16_t* b, uint16_t* out, int64_t K, hipStream_t stream);
+int launch_init_qlinear(uint64_t seed, int64_t N, int64_t K, float c, uint32_t* w, uint16_t* s, uint16_t* b,
+                        hipStream_t stream);
+int launch_fill_kv_synthetic(uint16_t* data, int64_t rows, int cap, int hd, int seq_len, uint64_t seed, float c,
+                             hipStream_t stream);
+uint64_t host_mix64(uint64_t z);
+
 }  // namespace bmx

@@ -48,6 +48,18 @@ __global__ void __launch_bounds__(256)
 }
 
 }  // namespace
+
+int launch_dequant_gather(const int32_t* ids, int64_t M, int64_t rows, const uint32_t* w, const uint16_t* s,
+                          const uint16_t* b, uint16_t* out, int64_t K, hipStream_t stream) {
+  if (M <= 0) return BMX_OK;
+  if (M > 65535) return set_error(BMX_E_SHAPE, "dequant_gather: M=%lld > 65535", (long long)M);
+  if (!aligned(out, 16)) return set_error(BMX_E_ALIGN, "dequant_gather: out not 16-byte aligned");
+  const int64_t words = K / 8;
+  hipLaunchKernelGGL(dequant_gather_kernel, dim3(static_cast<unsigned>((words + 255) / 256), static_cast<unsigned>(M)),
+                     dim3(256), 0, stream, ids, rows, w, s, b, out, K);
+  return check_launch("dequant_gather");
+}
+
 }  // namespace bmx
 
 using namespace bmx;
@@ -77,11 +89,5 @@ extern "C" int bmx_dequant_gather(const int32_t* ids, int64_t M, int64_t rows, c
                                   int group_size, int bits, void* stream) {
   if (int rc = check_format("dequant_gather", K, group_size, bits)) return rc;
   if (!ids || !w || !scales || !biases || !out) return set_error(BMX_E_ARG, "dequant_gather: null pointer");
-  if (M <= 0) return BMX_OK;
-  if (M > 65535) return set_error(BMX_E_SHAPE, "dequant_gather: M=%lld > 65535", (long long)M);
-  if (!aligned(out, 16)) return set_error(BMX_E_ALIGN, "dequant_gather: out not 16-byte aligned");
-  const int64_t words = K / 8;
-  hipLaunchKernelGGL(dequant_gather_kernel, dim3(static_cast<unsigned>((words + 255) / 256), static_cast<unsigned>(M)),
-                     dim3(256), 0, as_stream(stream), ids, rows, w, scales, biases, out, K);
-  return check_launch("dequant_gather");
+  return launch_dequant_gather(ids, M, rows, w, scales, biases, out, K, as_stream(stream));
 }

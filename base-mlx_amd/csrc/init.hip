@@ -9,12 +9,6 @@
 namespace bmx {
 namespace {
 
-uint64_t host_mix64(uint64_t z) {
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-  return z ^ (z >> 31);
-}
-
 __device__ __forceinline__ float normal_at(uint64_t mseed, uint64_t idx, float c) {
   return __fmul_rn(static_cast<float>(irwin4(rand64_mixed(mseed, idx))), c);
 }
@@ -73,7 +67,45 @@ __global__ void __launch_bounds__(256)
   if (i < n) out[i] = f2bf(normal_at(mseed, static_cast<uint64_t>(i), c));
 }
 
+// KV positions [0, seq_len) of every (layer, k|v, head) row get approx
+// N(0,1) values at counter (row * cap + t) * hd + d.
+__global__ void __launch_bounds__(256)
+    fill_kv_kernel(uint16_t* __restrict__ data, int64_t rows, int cap, int hd, int seq_len, uint64_t mseed, float c) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t per_row = static_cast<int64_t>(seq_len) * hd;
+  if (i >= rows * per_row) return;
+  const int64_t r = i / per_row, rem = i - r * per_row;
+  const int64_t idx = r * cap * hd + rem;
+  data[idx] = f2bf(normal_at(mseed, static_cast<uint64_t>(idx), c));
+}
+
 }  // namespace
+
+uint64_t host_mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+int launch_init_qlinear(uint64_t seed, int64_t N, int64_t K, float c, uint32_t* w, uint16_t* s, uint16_t* b,
+                        hipStream_t stream) {
+  if (N <= 0 || K <= 0 || K % 64) return set_error(BMX_E_SHAPE, "init_qlinear: N=%lld K=%lld", (long long)N, (long long)K);
+  if (!aligned(w, 16)) return set_error(BMX_E_ALIGN, "init_qlinear: W not 16-byte aligned");
+  const int64_t groups = N * (K / 64);
+  hipLaunchKernelGGL(init_qlinear_kernel, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256), 0, stream,
+                     host_mix64(seed), N, K, c, w, s, b);
+  return check_launch("init_qlinear");
+}
+
+int launch_fill_kv_synthetic(uint16_t* data, int64_t rows, int cap, int hd, int seq_len, uint64_t seed, float c,
+                             hipStream_t stream) {
+  const int64_t n = rows * seq_len * hd;
+  if (n <= 0) return BMX_OK;
+  hipLaunchKernelGGL(fill_kv_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, data, rows,
+                     cap, hd, seq_len, host_mix64(seed), c);
+  return check_launch("fill_kv");
+}
+
 }  // namespace bmx
 
 using namespace bmx;
@@ -81,13 +113,7 @@ using namespace bmx;
 extern "C" int bmx_init_qlinear(uint64_t seed, int64_t N, int64_t K, float c, uint32_t* w,
                                 bmx_bf16* scales, bmx_bf16* biases, void* stream) {
   if (!w || !scales || !biases) return set_error(BMX_E_ARG, "init_qlinear: null pointer");
-  if (N <= 0 || K <= 0 || K % 64) return set_error(BMX_E_SHAPE, "init_qlinear: N=%lld K=%lld", (long long)N, (long long)K);
-  if (!aligned(w, 16)) return set_error(BMX_E_ALIGN, "init_qlinear: W not 16-byte aligned");
-  const int64_t groups = N * (K / 64);
-  const int64_t blocks = (groups + 255) / 256;
-  hipLaunchKernelGGL(init_qlinear_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     as_stream(stream), host_mix64(seed), N, K, c, w, scales, biases);
-  return check_launch("init_qlinear");
+  return launch_init_qlinear(seed, N, K, c, w, scales, biases, as_stream(stream));
 }
 
 extern "C" int bmx_fill_normal_bf16(uint64_t seed, int64_t n, float c, bmx_bf16* out, void* stream) {

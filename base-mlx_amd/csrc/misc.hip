@@ -1,0 +1,140 @@
+// Greedy argmax and the elementwise ops of a Qwen3 block (gfx950).
+//
+// Semantics restated:
+//   argmax / argmax_axis over the last axis (engine.rs:195-202,
+//     speculative.rs:168-173, 289-293): index of the largest value, the
+//     first such index on ties, as uint32;
+//   mlp_block activation silu(g) * up (model/kernels.rs:73-74): each MLX op
+//     rounds to bf16 -- sigmoid, g * sigmoid, then * up;
+//   residual add `&x + &y` in bf16 (qwen3.rs:521, 541).
+#include <math.h>
+
+#include "bmx_device.h"
+
+namespace bmx {
+namespace {
+
+constexpr int kArgThreads = 1024;
+
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// one workgroup per row
+__global__ void __launch_bounds__(kArgThreads)
+    argmax_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t* __restrict__ out) {
+  __shared__ float sv[kArgThreads / 64];
+  __shared__ uint32_t si[kArgThreads / 64];
+  const uint16_t* xr = x + static_cast<int64_t>(blockIdx.x) * n;
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  for (int64_t i = threadIdx.x; i < n; i += kArgThreads) {
+    const float v = bf2f(xr[i]);
+    if (better(v, static_cast<uint32_t>(i), bv, bi)) {
+      bv = v;
+      bi = static_cast<uint32_t>(i);
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const uint32_t oi = __shfl_xor(bi, off, 64);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgThreads / 64; w++)
+      if (better(sv[w], si[w], bv, bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    // all -inf / NaN rows: index 0
+    out[blockIdx.x] = bi == 0xffffffffu ? 0u : bi;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u, uint16_t* __restrict__ y,
+                    int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float gv = bf2f(g[i]);
+  const float sg = round_bf(1.0f / (1.0f + expf(-gv)));
+  const float a = round_bf(gv * sg);
+  y[i] = f2bf(a * bf2f(u[i]));
+}
+
+__global__ void __launch_bounds__(256)
+    add_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint16_t* y, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) y[i] = f2bf(bf2f(a[i]) + bf2f(b[i]));
+}
+
+// dst[i] = src[i] (token ids u32 -> i32 for the embedding gather)
+__global__ void tokens_to_ids_kernel(const uint32_t* __restrict__ src, int32_t* __restrict__ dst, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = static_cast<int32_t>(src[i]);
+}
+
+__global__ void add_scalar_kernel(int* v, int d) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) *v += d;
+}
+
+}  // namespace
+
+int launch_argmax(const uint16_t* x, int64_t rows, int64_t n, uint32_t* out, hipStream_t stream) {
+  if (rows <= 0) return BMX_OK;
+  if (n <= 0 || n > UINT32_MAX) return set_error(BMX_E_SHAPE, "argmax: n=%lld", (long long)n);
+  if (rows > INT32_MAX) return set_error(BMX_E_SHAPE, "argmax: rows=%lld", (long long)rows);
+  hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(rows)), dim3(kArgThreads), 0, stream, x, n, out);
+  return check_launch("argmax");
+}
+
+int launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* y, int64_t n, hipStream_t stream) {
+  if (n <= 0) return BMX_OK;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, g, u, y, n);
+  return check_launch("silu_mul");
+}
+
+int launch_add(const uint16_t* a, const uint16_t* b, uint16_t* y, int64_t n, hipStream_t stream) {
+  if (n <= 0) return BMX_OK;
+  hipLaunchKernelGGL(add_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, a, b, y, n);
+  return check_launch("add");
+}
+
+int launch_tokens_to_ids(const uint32_t* src, int32_t* dst, int n, hipStream_t stream) {
+  if (n <= 0) return BMX_OK;
+  hipLaunchKernelGGL(tokens_to_ids_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, src, dst, n);
+  return check_launch("tokens_to_ids");
+}
+
+int launch_add_scalar(int* v, int d, hipStream_t stream) {
+  hipLaunchKernelGGL(add_scalar_kernel, dim3(1), dim3(64), 0, stream, v, d);
+  return check_launch("add_scalar");
+}
+
+}  // namespace bmx
+
+using namespace bmx;
+
+extern "C" int bmx_argmax_rows(const bmx_bf16* x, int64_t rows, int64_t n, uint32_t* out, void* stream) {
+  if (!x || !out) return set_error(BMX_E_ARG, "argmax: null pointer");
+  return launch_argmax(x, rows, n, out, as_stream(stream));
+}
+
+extern "C" int bmx_silu_mul(const bmx_bf16* gate, const bmx_bf16* up, bmx_bf16* y, int64_t n, void* stream) {
+  if (!gate || !up || !y) return set_error(BMX_E_ARG, "silu_mul: null pointer");
+  return launch_silu_mul(gate, up, y, n, as_stream(stream));
+}
+
+extern "C" int bmx_add(const bmx_bf16* a, const bmx_bf16* b, bmx_bf16* y, int64_t n, void* stream) {
+  if (!a || !b || !y) return set_error(BMX_E_ARG, "add: null pointer");
+  return launch_add(a, b, y, n, as_stream(stream));
+}

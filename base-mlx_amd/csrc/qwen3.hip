@@ -1,0 +1,676 @@
+// Qwen3 forward, KV cache, greedy and speculative generation over the bmx
+// kernels: the host side of the drop-in, mirroring the reference's model
+// and engine surface.
+//
+//   bmx_qwen3_*          <-> Qwen3 { load, forward, forward_multi }
+//                            (crates/base-mlx-core/src/model/qwen3.rs:164-563)
+//   bmx_kv_*             <-> KvCache { reset, truncate, seq_len }
+//                            (qwen3.rs:109-162)
+//   bmx_generate_greedy  <-> LoadedModel::generate_text with greedy pick_next
+//                            (crates/base-mlx-core/src/engine.rs:100-202)
+//   bmx_speculative_generate <-> speculative::generate
+//                            (crates/base-mlx-core/src/speculative.rs:57-286)
+//
+// Device layout.  Each projection keeps the MLX format (W [N, K/8] u32,
+// s/b [N, K/64] bf16).  The KV cache is one buffer [L, 2, Hkv, cap, 128]
+// bf16 (the reference's per-layer [Hkv, KV_PREALLOC, 128] pairs, capacity a
+// parameter); truncate rewinds seq_len and keeps the buffer, as the comment
+// at qwen3.rs:146-149 intends.
+//
+// Per layer at M <= 8 (decode, verify): one qmv for q|k|v with the input
+// RMSNorm fused, one fused QK-norm + RoPE + KV write, attention (+ split
+// combine), o_proj qmv with the residual add fused, gate|up qmv with the
+// post-attention RMSNorm and SwiGLU fused, down qmv with the residual add
+// fused.  At M > 8 (prefill) the norms, SwiGLU and adds run as their own
+// kernels around the MFMA qmm.  The M = 1 decode step is captured once per
+// cache into a HIP graph that reads the token and position from device
+// memory, so a decode step is one graph launch.
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <atomic>
+#include <vector>
+
+#include "bmx_device.h"
+
+namespace bmx {
+namespace {
+
+constexpr double kIrwin4Std = 37837.226523565;  // sqrt((65536^2 - 1) / 3)
+enum { SLOT_Q, SLOT_K, SLOT_V, SLOT_O, SLOT_GATE, SLOT_UP, SLOT_DOWN, NSLOT };
+
+struct QLin {
+  uint32_t* w = nullptr;
+  uint16_t* s = nullptr;
+  uint16_t* b = nullptr;
+  int N = 0, K = 0;
+};
+
+struct Layer {
+  QLin p[NSLOT];
+  uint16_t *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+};
+
+uint64_t tensor_seed(uint64_t model_seed, int layer, int slot) {
+  return host_mix64(model_seed * 0xD1B54A32D192ED03ull + static_cast<uint64_t>(static_cast<int64_t>(layer + 16)) * 64u +
+                    static_cast<uint64_t>(slot));
+}
+
+__global__ void fill_ones_kernel(uint16_t* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0x3f80;
+}
+
+}  // namespace
+}  // namespace bmx
+
+using namespace bmx;
+
+struct bmx_kv_cache {
+  uint64_t id = 0;  // unique per cache: keys the captured decode graph
+  int layers = 0, nkv = 0, hd = 0, cap = 0;
+  int seq_len = 0;
+  uint16_t* data = nullptr;  // [layers, 2, nkv, cap, hd]
+  uint16_t* k(int l) { return data + static_cast<size_t>(l) * 2 * nkv * cap * hd; }
+  uint16_t* v(int l) { return k(l) + static_cast<size_t>(nkv) * cap * hd; }
+};
+
+struct bmx_qwen3 {
+  bmx_qwen3_config cfg{};
+  int max_tokens = 0;
+  QLin embed, lm_head;
+  uint16_t* final_norm = nullptr;
+  std::vector<Layer> layers;
+  RopeTable rope{};
+  std::vector<void*> allocs;
+  // workspace (rows = max_tokens)
+  uint16_t *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *att = nullptr,
+           *o = nullptr, *g = nullptr, *u = nullptr, *a = nullptr, *logits1 = nullptr;
+  float* attn_ws = nullptr;
+  size_t attn_ws_floats = 0;
+  int32_t* ids = nullptr;     // [max_tokens] token ids for the embedding gather
+  uint32_t* tok_u = nullptr;  // [max(max_tokens, 64)] token staging
+  uint32_t* next_tok = nullptr;  // argmax output of the decode step
+  int* pos = nullptr;            // decode position (device)
+  uint32_t* host_tok = nullptr;    // pinned [64]: token / position / argmax exchange
+  uint32_t* host_stage = nullptr;  // pinned [max_tokens]: prompt upload staging
+  hipEvent_t stage_done = nullptr; // host_stage may be rewritten once this fired
+  hipStream_t own_stream = nullptr;  // used when the caller passes the null stream
+  // decode graph
+  hipGraphExec_t graph = nullptr;
+  uint64_t graph_cache = 0;  // id of the cache the graph was captured for
+  hipStream_t graph_stream = nullptr;
+};
+
+namespace {
+
+int dalloc(bmx_qwen3* m, void** p, size_t bytes) {
+  if (bytes == 0) bytes = 16;
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) return set_error(BMX_E_ALLOC, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  m->allocs.push_back(*p);
+  return BMX_OK;
+}
+
+template <typename T>
+int dalloc_t(bmx_qwen3* m, T** p, size_t count) {
+  return dalloc(m, reinterpret_cast<void**>(p), count * sizeof(T));
+}
+
+int alloc_qlin(bmx_qwen3* m, QLin* q, int N, int K) {
+  q->N = N;
+  q->K = K;
+  if (int rc = dalloc_t(m, &q->w, static_cast<size_t>(N) * (K / 8))) return rc;
+  if (int rc = dalloc_t(m, &q->s, static_cast<size_t>(N) * (K / 64))) return rc;
+  return dalloc_t(m, &q->b, static_cast<size_t>(N) * (K / 64));
+}
+
+int ones(bmx_qwen3* m, uint16_t** p, int n, hipStream_t st) {
+  if (int rc = dalloc_t(m, p, static_cast<size_t>(n))) return rc;
+  hipLaunchKernelGGL(fill_ones_kernel, dim3((n + 255) / 256), dim3(256), 0, st, *p, n);
+  return check_launch("fill_ones");
+}
+
+int qmv(const bmx_qwen3* m, const uint16_t* x, int M, const QLin& w, uint16_t* y, hipStream_t st,
+        const uint16_t* norm = nullptr) {
+  QmvParams p{};
+  p.x = x;
+  p.ldx = w.K;
+  p.nseg = 1;
+  p.seg[0] = QmvSegment{w.w, w.s, w.b, y, w.N, 0};
+  p.m = M;
+  p.N = w.N;
+  p.K = w.K;
+  p.norm_w = norm;
+  p.eps = m->cfg.eps;
+  return launch_qmv(p, QMV_STORE, st);
+}
+
+const QLin& head_of(const bmx_qwen3* m) { return m->cfg.tied ? m->embed : m->lm_head; }
+
+// One forward over M tokens whose ids are already in m->ids, at position
+// cache->seq_len (or *pos_dev when graph-captured).  logits: [rows, vocab]
+// (rows = M if all_logits else 1).
+int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* pos_dev, bool all_logits,
+                   uint16_t* logits, hipStream_t st) {
+  const bmx_qwen3_config& cf = m->cfg;
+  const int H = cf.hidden, I = cf.inter, nq = cf.n_heads, nkv = cf.n_kv_heads, hd = cf.head_dim;
+  const int qd = nq * hd, kvd = nkv * hd;
+  const float scale = 1.0f / sqrtf(static_cast<float>(hd));  // qwen3.rs:324
+  const int L_max = pos_dev ? c->cap : offset + M;
+  // x = embed.lookup(tokens)  (qwen3.rs:328-333)
+  if (int rc = launch_dequant_gather(m->ids, M, cf.vocab, m->embed.w, m->embed.s, m->embed.b, m->x, H, st)) return rc;
+  for (int l = 0; l < cf.layers; l++) {
+    const Layer& L = m->layers[l];
+    // ---- qkv_block: rms_norm + q/k/v projections (kernels.rs:28-46) ----
+    if (M <= 8) {
+      QmvParams p{};
+      p.x = m->x;
+      p.ldx = H;
+      p.nseg = 3;
+      p.seg[0] = QmvSegment{L.p[SLOT_Q].w, L.p[SLOT_Q].s, L.p[SLOT_Q].b, m->q, qd, 0};
+      p.seg[1] = QmvSegment{L.p[SLOT_K].w, L.p[SLOT_K].s, L.p[SLOT_K].b, m->k, kvd, qd};
+      p.seg[2] = QmvSegment{L.p[SLOT_V].w, L.p[SLOT_V].s, L.p[SLOT_V].b, m->v, kvd, qd + kvd};
+      p.m = M;
+      p.N = qd + 2 * kvd;
+      p.K = H;
+      p.norm_w = L.in_norm;
+      p.eps = cf.eps;
+      if (int rc = launch_qmv(p, QMV_STORE, st)) return rc;
+    } else {
+      if (int rc = launch_rms_norm(m->x, L.in_norm, m->h, M, H, cf.eps, st)) return rc;
+      if (int rc = launch_qmm(m->h, L.p[SLOT_Q].w, L.p[SLOT_Q].s, L.p[SLOT_Q].b, m->q, M, qd, H, st)) return rc;
+      if (int rc = launch_qmm(m->h, L.p[SLOT_K].w, L.p[SLOT_K].s, L.p[SLOT_K].b, m->k, M, kvd, H, st)) return rc;
+      if (int rc = launch_qmm(m->h, L.p[SLOT_V].w, L.p[SLOT_V].s, L.p[SLOT_V].b, m->v, M, kvd, H, st)) return rc;
+    }
+    // ---- QK-norm, RoPE at the cache offset, KV write (qwen3.rs:392-489) ----
+    if (int rc = launch_qk_norm_rope_kv(m->q, m->k, m->v, L.q_norm, L.k_norm, m->qr, c->k(l), c->v(l), M, nq, nkv,
+                                        hd, c->cap, offset, pos_dev, cf.eps, m->rope, st))
+      return rc;
+    // ---- SDPA over [0, offset + M) with the causal-offset mask (qwen3.rs:491-518) ----
+    if (int rc = launch_attention(m->qr, c->k(l), c->v(l), m->att, m->attn_ws, m->attn_ws_floats, nq, nkv, M, hd,
+                                  c->cap, offset, pos_dev, L_max, scale, st))
+      return rc;
+    // ---- o_proj + residual (qwen3.rs:520-521) ----
+    if (M <= 8) {
+      QmvParams p{};
+      p.x = m->att;
+      p.ldx = qd;
+      p.nseg = 1;
+      p.seg[0] = QmvSegment{L.p[SLOT_O].w, L.p[SLOT_O].s, L.p[SLOT_O].b, m->x, H, 0};
+      p.m = M;
+      p.N = H;
+      p.K = qd;
+      p.res = m->x;
+      if (int rc = launch_qmv(p, QMV_RESIDUAL, st)) return rc;
+    } else {
+      if (int rc = launch_qmm(m->att, L.p[SLOT_O].w, L.p[SLOT_O].s, L.p[SLOT_O].b, m->o, M, H, qd, st)) return rc;
+      if (int rc = launch_add(m->x, m->o, m->x, static_cast<int64_t>(M) * H, st)) return rc;
+    }
+    // ---- mlp_block + residual (kernels.rs:55-78; qwen3.rs:523-541) ----
+    if (M <= 8) {
+      QmvParams p{};
+      p.x = m->x;
+      p.ldx = H;
+      p.nseg = 2;
+      p.seg[0] = QmvSegment{L.p[SLOT_GATE].w, L.p[SLOT_GATE].s, L.p[SLOT_GATE].b, m->a, I, 0};
+      p.seg[1] = QmvSegment{L.p[SLOT_UP].w, L.p[SLOT_UP].s, L.p[SLOT_UP].b, m->a, I, 0};
+      p.m = M;
+      p.N = I;
+      p.K = H;
+      p.norm_w = L.post_norm;
+      p.eps = cf.eps;
+      if (int rc = launch_qmv(p, QMV_SWIGLU, st)) return rc;
+      QmvParams d{};
+      d.x = m->a;
+      d.ldx = I;
+      d.nseg = 1;
+      d.seg[0] = QmvSegment{L.p[SLOT_DOWN].w, L.p[SLOT_DOWN].s, L.p[SLOT_DOWN].b, m->x, H, 0};
+      d.m = M;
+      d.N = H;
+      d.K = I;
+      d.res = m->x;
+      if (int rc = launch_qmv(d, QMV_RESIDUAL, st)) return rc;
+    } else {
+      if (int rc = launch_rms_norm(m->x, L.post_norm, m->h, M, H, cf.eps, st)) return rc;
+      if (int rc = launch_qmm(m->h, L.p[SLOT_GATE].w, L.p[SLOT_GATE].s, L.p[SLOT_GATE].b, m->g, M, I, H, st)) return rc;
+      if (int rc = launch_qmm(m->h, L.p[SLOT_UP].w, L.p[SLOT_UP].s, L.p[SLOT_UP].b, m->u, M, I, H, st)) return rc;
+      if (int rc = launch_silu_mul(m->g, m->u, m->a, static_cast<int64_t>(M) * I, st)) return rc;
+      if (int rc = launch_qmm(m->a, L.p[SLOT_DOWN].w, L.p[SLOT_DOWN].s, L.p[SLOT_DOWN].b, m->o, M, H, I, st)) return rc;
+      if (int rc = launch_add(m->x, m->o, m->x, static_cast<int64_t>(M) * H, st)) return rc;
+    }
+  }
+  // ---- final norm, last row unless all logits, tied head (qwen3.rs:545-555) ----
+  const QLin& head = head_of(m);
+  const int rows = all_logits ? M : 1;
+  const uint16_t* xin = all_logits ? m->x : m->x + static_cast<size_t>(M - 1) * H;
+  if (rows <= 8) return qmv(m, xin, rows, head, logits, st, m->final_norm);
+  if (int rc = launch_rms_norm(xin, m->final_norm, m->h, rows, H, cf.eps, st)) return rc;
+  return launch_qmm(m->h, head.w, head.s, head.b, logits, rows, cf.vocab, H, st);
+}
+
+// Decode step with token and position in device memory: ids <- tok_u[0],
+// forward, argmax -> next_tok, pos += 1.  Captured into a graph.
+int decode_step_device(bmx_qwen3* m, bmx_kv_cache* c, hipStream_t st) {
+  if (int rc = launch_tokens_to_ids(m->tok_u, m->ids, 1, st)) return rc;
+  if (int rc = forward_device(m, c, 1, 0, m->pos, false, m->logits1, st)) return rc;
+  if (int rc = launch_argmax(m->logits1, 1, m->cfg.vocab, m->next_tok, st)) return rc;
+  if (int rc = check_hip(hipMemcpyAsync(m->tok_u, m->next_tok, 4, hipMemcpyDeviceToDevice, st), "copy token")) return rc;
+  return launch_add_scalar(m->pos, 1, st);
+}
+
+void drop_graph(bmx_qwen3* m) {
+  if (m->graph) (void)hipGraphExecDestroy(m->graph);
+  m->graph = nullptr;
+  m->graph_cache = 0;
+}
+
+int ensure_graph(bmx_qwen3* m, bmx_kv_cache* c, hipStream_t st) {
+  if (m->graph && m->graph_cache == c->id && m->graph_stream == st) return BMX_OK;
+  drop_graph(m);
+  hipGraph_t g = nullptr;
+  if (int rc = check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture")) return rc;
+  int rc = decode_step_device(m, c, st);
+  hipError_t e = hipStreamEndCapture(st, &g);
+  if (rc) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (int r2 = check_hip(e, "end capture")) return r2;
+  e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (int r2 = check_hip(e, "graph instantiate")) return r2;
+  m->graph_cache = c->id;
+  m->graph_stream = st;
+  return BMX_OK;
+}
+
+bool is_eos(uint32_t t, const uint32_t* eos, int n_eos) {
+  for (int i = 0; i < n_eos; i++)
+    if (eos[i] == t) return true;
+  return false;
+}
+
+// tokens (host) -> m->ids (device) through the pinned staging buffer
+int upload_tokens(bmx_qwen3* m, const uint32_t* tokens, int M, hipStream_t st) {
+  for (int i = 0; i < M; i++)
+    if (tokens[i] >= static_cast<uint32_t>(m->cfg.vocab))
+      return set_error(BMX_E_ARG, "token %u at %d outside vocab %d", tokens[i], i, m->cfg.vocab);
+  if (int rc = check_hip(hipEventSynchronize(m->stage_done), "stage wait")) return rc;
+  memcpy(m->host_stage, tokens, static_cast<size_t>(M) * 4);
+  if (int rc = check_hip(hipMemcpyAsync(m->tok_u, m->host_stage, static_cast<size_t>(M) * 4, hipMemcpyHostToDevice, st),
+                         "upload tokens"))
+    return rc;
+  if (int rc = check_hip(hipEventRecord(m->stage_done, st), "stage record")) return rc;
+  return launch_tokens_to_ids(m->tok_u, m->ids, M, st);
+}
+
+hipStream_t pick_stream(bmx_qwen3* m, void* stream) {
+  return stream ? as_stream(stream) : m->own_stream;
+}
+
+}  // namespace
+
+// ======================================================================
+// C ABI
+// ======================================================================
+
+extern "C" int bmx_qwen3_create_random(const bmx_qwen3_config* cfg, uint64_t seed, double sigma, int max_tokens,
+                                       bmx_qwen3** out) {
+  if (!cfg || !out) return set_error(BMX_E_ARG, "qwen3_create: null pointer");
+  *out = nullptr;
+  if (cfg->bits != 4 || cfg->group_size != 64)
+    return set_error(BMX_E_UNSUPPORTED, "qwen3_create: only bits=4, group_size=64");
+  if (cfg->head_dim != 128 || cfg->n_heads % cfg->n_kv_heads || cfg->hidden % 64 || cfg->inter % 64 ||
+      (cfg->n_heads * cfg->head_dim) % 64 || cfg->layers <= 0 || cfg->vocab <= 0)
+    return set_error(BMX_E_SHAPE, "qwen3_create: unsupported shape");
+  if (max_tokens < 1 || max_tokens > 65535) return set_error(BMX_E_ARG, "qwen3_create: max_tokens=%d", max_tokens);
+  bmx_qwen3* m = new bmx_qwen3();
+  m->cfg = *cfg;
+  m->max_tokens = max_tokens;
+  m->rope = make_rope_table(cfg->head_dim, cfg->rope_theta);
+  const int H = cfg->hidden, I = cfg->inter, qd = cfg->n_heads * cfg->head_dim, kvd = cfg->n_kv_heads * cfg->head_dim;
+  const float c = static_cast<float>(sigma / kIrwin4Std);
+  hipStream_t st = nullptr;
+  int rc = alloc_qlin(m, &m->embed, cfg->vocab, H);
+  if (!rc) rc = launch_init_qlinear(tensor_seed(seed, -1, 0), cfg->vocab, H, c, m->embed.w, m->embed.s, m->embed.b, st);
+  if (!rc && !cfg->tied) {
+    rc = alloc_qlin(m, &m->lm_head, cfg->vocab, H);
+    if (!rc) rc = launch_init_qlinear(tensor_seed(seed, -2, 0), cfg->vocab, H, c, m->lm_head.w, m->lm_head.s, m->lm_head.b, st);
+  }
+  if (!rc) rc = ones(m, &m->final_norm, H, st);
+  m->layers.resize(cfg->layers);
+  const int dims[NSLOT][2] = {{qd, H}, {kvd, H}, {kvd, H}, {H, qd}, {I, H}, {I, H}, {H, I}};
+  for (int l = 0; !rc && l < cfg->layers; l++) {
+    Layer& L = m->layers[l];
+    for (int sl = 0; !rc && sl < NSLOT; sl++) {
+      rc = alloc_qlin(m, &L.p[sl], dims[sl][0], dims[sl][1]);
+      if (!rc) rc = launch_init_qlinear(tensor_seed(seed, l, sl), dims[sl][0], dims[sl][1], c, L.p[sl].w, L.p[sl].s, L.p[sl].b, st);
+    }
+    if (!rc) rc = ones(m, &L.in_norm, H, st);
+    if (!rc) rc = ones(m, &L.post_norm, H, st);
+    if (!rc) rc = ones(m, &L.q_norm, cfg->head_dim, st);
+    if (!rc) rc = ones(m, &L.k_norm, cfg->head_dim, st);
+  }
+  // workspace
+  const size_t T = static_cast<size_t>(max_tokens);
+  if (!rc) rc = dalloc_t(m, &m->x, T * H);
+  if (!rc) rc = dalloc_t(m, &m->h, T * H);
+  if (!rc) rc = dalloc_t(m, &m->q, T * qd);
+  if (!rc) rc = dalloc_t(m, &m->k, T * kvd);
+  if (!rc) rc = dalloc_t(m, &m->v, T * kvd);
+  if (!rc) rc = dalloc_t(m, &m->qr, T * qd);
+  if (!rc) rc = dalloc_t(m, &m->att, T * qd);
+  if (!rc) rc = dalloc_t(m, &m->o, T * H);
+  if (!rc) rc = dalloc_t(m, &m->g, T * I);
+  if (!rc) rc = dalloc_t(m, &m->u, T * I);
+  if (!rc) rc = dalloc_t(m, &m->a, T * I);
+  if (!rc) rc = dalloc_t(m, &m->logits1, static_cast<size_t>(cfg->vocab));
+  m->attn_ws_floats = attention_workspace_floats(cfg->n_heads, 16, 64);
+  if (!rc) rc = dalloc_t(m, &m->attn_ws, m->attn_ws_floats);
+  if (!rc) rc = dalloc_t(m, &m->ids, T);
+  if (!rc) rc = dalloc_t(m, &m->tok_u, T < 64 ? 64 : T);
+  if (!rc) rc = dalloc_t(m, &m->next_tok, 64);
+  if (!rc) rc = dalloc_t(m, &m->pos, 16);
+  if (!rc) rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&m->host_tok), 64 * sizeof(uint32_t), hipHostMallocDefault), "hipHostMalloc");
+  if (!rc) rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&m->host_stage), T * sizeof(uint32_t), hipHostMallocDefault), "hipHostMalloc");
+  if (!rc) rc = check_hip(hipEventCreateWithFlags(&m->stage_done, hipEventDisableTiming), "event create");
+  if (!rc) rc = check_hip(hipEventRecord(m->stage_done, st), "event record");
+  if (!rc) rc = check_hip(hipStreamCreate(&m->own_stream), "stream create");
+  if (!rc) rc = check_hip(hipStreamSynchronize(st), "init sync");
+  if (rc) {
+    bmx_qwen3_destroy(m);
+    return rc;
+  }
+  *out = m;
+  return BMX_OK;
+}
+
+extern "C" void bmx_qwen3_destroy(bmx_qwen3* m) {
+  if (!m) return;
+  (void)hipDeviceSynchronize();
+  drop_graph(m);
+  for (void* p : m->allocs) (void)hipFree(p);
+  if (m->host_tok) (void)hipHostFree(m->host_tok);
+  if (m->host_stage) (void)hipHostFree(m->host_stage);
+  if (m->stage_done) (void)hipEventDestroy(m->stage_done);
+  if (m->own_stream) (void)hipStreamDestroy(m->own_stream);
+  delete m;
+}
+
+extern "C" int bmx_qwen3_qlinear(bmx_qwen3* m, int layer, int slot, uint32_t** w, bmx_bf16** s, bmx_bf16** b, int* N,
+                                 int* K) {
+  if (!m || !w || !s || !b || !N || !K) return set_error(BMX_E_ARG, "qwen3_qlinear: null pointer");
+  const QLin* q = nullptr;
+  if (layer == -1) q = &m->embed;
+  else if (layer == -2) q = &head_of(m);
+  else if (layer >= 0 && layer < m->cfg.layers && slot >= 0 && slot < NSLOT) q = &m->layers[layer].p[slot];
+  else return set_error(BMX_E_ARG, "qwen3_qlinear: layer %d slot %d", layer, slot);
+  *w = q->w;
+  *s = q->s;
+  *b = q->b;
+  *N = q->N;
+  *K = q->K;
+  return BMX_OK;
+}
+
+extern "C" int bmx_kv_create(const bmx_qwen3* m, int capacity, bmx_kv_cache** out) {
+  if (!m || !out) return set_error(BMX_E_ARG, "kv_create: null pointer");
+  *out = nullptr;
+  if (capacity <= 0) return set_error(BMX_E_ARG, "kv_create: capacity=%d", capacity);
+  static std::atomic<uint64_t> next_id{1};
+  bmx_kv_cache* c = new bmx_kv_cache();
+  c->id = next_id.fetch_add(1);
+  c->layers = m->cfg.layers;
+  c->nkv = m->cfg.n_kv_heads;
+  c->hd = m->cfg.head_dim;
+  c->cap = capacity;
+  const size_t n = static_cast<size_t>(c->layers) * 2 * c->nkv * capacity * c->hd;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&c->data), n * 2);
+  if (e != hipSuccess) {
+    delete c;
+    return set_error(BMX_E_ALLOC, "kv_create: hipMalloc(%zu): %s", n * 2, hipGetErrorString(e));
+  }
+  // the reference seeds the cache from a zeros buffer (qwen3.rs:457-488)
+  e = hipMemset(c->data, 0, n * 2);
+  if (e != hipSuccess) {
+    (void)hipFree(c->data);
+    delete c;
+    return check_hip(e, "kv_create: memset");
+  }
+  *out = c;
+  return BMX_OK;
+}
+
+extern "C" void bmx_kv_destroy(bmx_kv_cache* c) {
+  if (!c) return;
+  (void)hipDeviceSynchronize();
+  (void)hipFree(c->data);
+  delete c;
+}
+
+extern "C" int bmx_kv_seq_len(const bmx_kv_cache* c) { return c ? c->seq_len : 0; }
+extern "C" int bmx_kv_capacity(const bmx_kv_cache* c) { return c ? c->cap : 0; }
+extern "C" void bmx_kv_reset(bmx_kv_cache* c) {
+  if (c) c->seq_len = 0;
+}
+extern "C" void bmx_kv_truncate(bmx_kv_cache* c, int target) {
+  if (!c || target >= c->seq_len) return;  // qwen3.rs:150-153
+  c->seq_len = target < 0 ? 0 : target;
+}
+extern "C" bmx_bf16* bmx_kv_data(bmx_kv_cache* c) { return c ? c->data : nullptr; }
+
+extern "C" int bmx_kv_fill_synthetic(bmx_kv_cache* c, uint64_t seed, int seq_len, void* stream) {
+  if (!c) return set_error(BMX_E_ARG, "kv_fill_synthetic: null cache");
+  if (seq_len < 0 || seq_len > c->cap) return set_error(BMX_E_KV_CAPACITY, "kv_fill_synthetic: %d > %d", seq_len, c->cap);
+  if (int rc = launch_fill_kv_synthetic(c->data, static_cast<int64_t>(c->layers) * 2 * c->nkv, c->cap, c->hd, seq_len,
+                                        seed, static_cast<float>(1.0 / kIrwin4Std), as_stream(stream)))
+    return rc;
+  if (int rc = check_hip(hipStreamSynchronize(as_stream(stream)), "kv fill sync")) return rc;
+  c->seq_len = seq_len;
+  return BMX_OK;
+}
+
+extern "C" int bmx_qwen3_forward(bmx_qwen3* m, bmx_kv_cache* c, const uint32_t* tokens, int M, int all_logits,
+                                 bmx_bf16* logits, void* stream) {
+  if (!m || !c || !tokens || !logits) return set_error(BMX_E_ARG, "qwen3_forward: null pointer");
+  if (M <= 0) return set_error(BMX_E_ARG, "qwen3_forward: M=%d", M);
+  if (M > m->max_tokens) return set_error(BMX_E_SHAPE, "qwen3_forward: M=%d > max_tokens %d", M, m->max_tokens);
+  if (c->layers != m->cfg.layers || c->nkv != m->cfg.n_kv_heads)  // qwen3.rs:351-358
+    return set_error(BMX_E_SHAPE, "cache layer count %d != model layers %d", c->layers, m->cfg.layers);
+  if (c->seq_len + M > c->cap)  // qwen3.rs:423-428
+    return set_error(BMX_E_KV_CAPACITY, "KV cache exhausted: requested %d positions, max %d", c->seq_len + M, c->cap);
+  hipStream_t st = pick_stream(m, stream);
+  if (int rc = upload_tokens(m, tokens, M, st)) return rc;
+  if (int rc = forward_device(m, c, M, c->seq_len, nullptr, all_logits != 0, logits, st)) return rc;
+  c->seq_len += M;  // qwen3.rs:557
+  return BMX_OK;
+}
+
+// One greedy decode step on device: token tok (host) at position seq_len,
+// through the captured graph; the argmax lands in *next (host).
+static int graph_step(bmx_qwen3* m, bmx_kv_cache* c, hipStream_t st, uint32_t tok, uint32_t* next) {
+  if (c->seq_len + 1 > c->cap)
+    return set_error(BMX_E_KV_CAPACITY, "KV cache exhausted: requested %d positions, max %d", c->seq_len + 1, c->cap);
+  if (int rc = ensure_graph(m, c, st)) return rc;
+  m->host_tok[0] = tok;
+  m->host_tok[1] = static_cast<uint32_t>(c->seq_len);
+  if (int rc = check_hip(hipMemcpyAsync(m->tok_u, &m->host_tok[0], 4, hipMemcpyHostToDevice, st), "set token")) return rc;
+  if (int rc = check_hip(hipMemcpyAsync(m->pos, &m->host_tok[1], 4, hipMemcpyHostToDevice, st), "set pos")) return rc;
+  if (int rc = check_hip(hipGraphLaunch(m->graph, st), "graph launch")) return rc;
+  if (int rc = check_hip(hipMemcpyAsync(&m->host_tok[2], m->next_tok, 4, hipMemcpyDeviceToHost, st), "read token"))
+    return rc;
+  if (int rc = check_hip(hipStreamSynchronize(st), "decode sync")) return rc;
+  c->seq_len += 1;
+  *next = m->host_tok[2];
+  return BMX_OK;
+}
+
+extern "C" int bmx_qwen3_decode_step(bmx_qwen3* m, bmx_kv_cache* c, uint32_t token, uint32_t* next_token,
+                                     bmx_bf16* logits, void* stream) {
+  if (!m || !c || !next_token) return set_error(BMX_E_ARG, "decode_step: null pointer");
+  if (token >= static_cast<uint32_t>(m->cfg.vocab)) return set_error(BMX_E_ARG, "decode_step: token %u", token);
+  hipStream_t st = pick_stream(m, stream);
+  if (int rc = graph_step(m, c, st, token, next_token)) return rc;
+  if (logits)
+    return check_hip(hipMemcpy(logits, m->logits1, static_cast<size_t>(m->cfg.vocab) * 2, hipMemcpyDeviceToDevice),
+                     "copy logits");
+  return BMX_OK;
+}
+
+extern "C" int bmx_generate_greedy(bmx_qwen3* m, bmx_kv_cache* c, const uint32_t* prompt, int P, int max_new,
+                                   const uint32_t* eos, int n_eos, uint32_t* out, int* n_out, void* stream) {
+  if (!m || !c || !prompt || !out || !n_out || (n_eos > 0 && !eos)) return set_error(BMX_E_ARG, "generate: null pointer");
+  *n_out = 0;
+  if (P <= 0 || max_new <= 0) return set_error(BMX_E_ARG, "generate: P=%d max_new=%d", P, max_new);
+  hipStream_t st = pick_stream(m, stream);
+  // prefill in chunks of max_tokens (a single forward in the reference,
+  // engine.rs:107; chunking changes no result: every op is row-wise or
+  // causal over the cache)
+  int done = 0;
+  while (done < P) {
+    const int mm = std::min(P - done, m->max_tokens);
+    const bool last = done + mm == P;
+    if (c->seq_len + mm > c->cap)
+      return set_error(BMX_E_KV_CAPACITY, "KV cache exhausted: requested %d positions, max %d", c->seq_len + mm, c->cap);
+    if (int rc = upload_tokens(m, prompt + done, mm, st)) return rc;
+    if (int rc = forward_device(m, c, mm, c->seq_len, nullptr, false, m->logits1, st)) return rc;
+    c->seq_len += mm;
+    done += mm;
+    if (last) {
+      if (int rc = launch_argmax(m->logits1, 1, m->cfg.vocab, m->next_tok, st)) return rc;
+    }
+  }
+  if (int rc = check_hip(hipMemcpyAsync(&m->host_tok[2], m->next_tok, 4, hipMemcpyDeviceToHost, st), "read token"))
+    return rc;
+  if (int rc = check_hip(hipStreamSynchronize(st), "prefill sync")) return rc;
+  uint32_t next = m->host_tok[2];
+  int produced = 0, n = 0;
+  // loop of engine.rs:112-124
+  for (;;) {
+    produced++;
+    if (is_eos(next, eos, n_eos)) break;
+    out[n++] = next;
+    if (produced >= max_new) break;
+    uint32_t nx;
+    if (int rc = graph_step(m, c, st, next, &nx)) {
+      *n_out = n;
+      return rc;
+    }
+    next = nx;
+  }
+  *n_out = n;
+  return BMX_OK;
+}
+
+// Verify forward for the speculative loop: tokens (host) -> argmax of every
+// row (host).
+static int forward_argmax(bmx_qwen3* m, bmx_kv_cache* c, const uint32_t* toks, int M, bool all, uint32_t* preds,
+                          uint16_t* logits, hipStream_t st) {
+  if (c->seq_len + M > c->cap)
+    return set_error(BMX_E_KV_CAPACITY, "KV cache exhausted: requested %d positions, max %d", c->seq_len + M, c->cap);
+  if (int rc = upload_tokens(m, toks, M, st)) return rc;
+  if (int rc = forward_device(m, c, M, c->seq_len, nullptr, all, logits, st)) return rc;
+  c->seq_len += M;
+  const int rows = all ? M : 1;
+  if (int rc = launch_argmax(logits, rows, m->cfg.vocab, m->next_tok, st)) return rc;
+  if (int rc = check_hip(hipMemcpyAsync(&m->host_tok[8], m->next_tok, rows * 4, hipMemcpyDeviceToHost, st), "read preds"))
+    return rc;
+  if (int rc = check_hip(hipStreamSynchronize(st), "verify sync")) return rc;
+  memcpy(preds, &m->host_tok[8], rows * 4);
+  return BMX_OK;
+}
+
+extern "C" int bmx_speculative_generate(bmx_qwen3* target, bmx_kv_cache* tc, bmx_qwen3* draft, bmx_kv_cache* dc,
+                                        const uint32_t* prompt, int P, int max_new, int spec_k, const uint32_t* eos,
+                                        int n_eos, uint32_t* out, int* n_out, int64_t* stats, void* stream) {
+  if (!target || !tc || !draft || !dc || !prompt || !out || !n_out || (n_eos > 0 && !eos))
+    return set_error(BMX_E_ARG, "speculative: null pointer");
+  *n_out = 0;
+  if (draft->cfg.vocab != target->cfg.vocab)  // check_compatible, speculative.rs:40-54
+    return set_error(BMX_E_ARG, "draft/target vocab mismatch: target=%d draft=%d", target->cfg.vocab, draft->cfg.vocab);
+  if (spec_k < 2 || spec_k > 8) return set_error(BMX_E_ARG, "speculative: spec_k=%d outside 2..8", spec_k);
+  if (spec_k > target->max_tokens) return set_error(BMX_E_SHAPE, "speculative: spec_k > target max_tokens");
+  hipStream_t st = pick_stream(target, stream);
+  int64_t iters = 0, proposed = 0, accepted = 0;
+  int n = 0, rc = BMX_OK;
+  uint32_t leader = 0, dnext = 0;
+  uint16_t* tlog = nullptr;
+  // target verify logits: [spec_k, vocab]
+  if ((rc = check_hip(hipMalloc(reinterpret_cast<void**>(&tlog), static_cast<size_t>(spec_k) * target->cfg.vocab * 2),
+                      "verify logits")))
+    return rc;
+  // prefill both (speculative.rs:75-79): only the target's last row is used
+  // and the draft's logits are discarded, so only those rows are computed
+  {
+    int done = 0;
+    while (!rc && done < P) {
+      const int mm = std::min(P - done, target->max_tokens);
+      uint32_t pr;
+      rc = forward_argmax(target, tc, prompt + done, mm, false, &pr, target->logits1, st);
+      leader = pr;
+      done += mm;
+    }
+    done = 0;
+    while (!rc && done < P) {
+      const int mm = std::min(P - done, draft->max_tokens);
+      uint32_t pr;
+      rc = forward_argmax(draft, dc, prompt + done, mm, false, &pr, draft->logits1, st);
+      done += mm;
+    }
+  }
+  if (rc || is_eos(leader, eos, n_eos)) goto done;
+  out[n++] = leader;
+  if ((rc = graph_step(draft, dc, st, leader, &dnext))) goto done;  // :104
+  while (n < max_new) {
+    uint32_t drafts[8], vin[8], preds[8];
+    int nd = 0;
+    for (int i = 0; i < spec_k - 1; i++) {  // :124-137
+      const uint32_t d = dnext;
+      drafts[nd++] = d;
+      if ((rc = graph_step(draft, dc, st, d, &dnext))) goto done;
+      if (is_eos(d, eos, n_eos)) break;
+    }
+    vin[0] = leader;
+    for (int i = 0; i < nd; i++) vin[i + 1] = drafts[i];
+    if ((rc = forward_argmax(target, tc, vin, nd + 1, true, preds, tlog, st))) goto done;  // :146-173
+    proposed += nd;
+    iters++;
+    int na = 0;
+    uint32_t bonus = preds[nd];
+    for (int i = 0; i < nd; i++) {  // :175-192
+      if (preds[i] == drafts[i]) na++;
+      else {
+        bonus = preds[i];
+        break;
+      }
+    }
+    accepted += na;
+    bool stop = false;
+    for (int i = 0; i < na; i++) {  // :201-211
+      if (n >= max_new || is_eos(drafts[i], eos, n_eos)) {
+        stop = true;
+        break;
+      }
+      out[n++] = drafts[i];
+    }
+    if (stop || n >= max_new || is_eos(bonus, eos, n_eos)) break;
+    out[n++] = bonus;
+    // rewind both caches to prompt + emitted - 1 (:227, :234), keeping the buffers
+    bmx_kv_truncate(tc, P + n - 1);
+    bmx_kv_truncate(dc, P + n - 1);
+    leader = bonus;
+    if ((rc = graph_step(draft, dc, st, leader, &dnext))) goto done;  // :238-239
+  }
+done:
+  *n_out = n;
+  if (stats) {
+    stats[0] = iters;
+    stats[1] = proposed;
+    stats[2] = accepted;
+  }
+  (void)hipFree(tlog);
+  return rc;
+}

@@ -95,6 +95,152 @@ int bmx_init_qlinear(uint64_t seed, int64_t N, int64_t K, float c, uint32_t *w,
 /* out[i] = bf16(approx-normal(seed, i) * c) */
 int bmx_fill_normal_bf16(uint64_t seed, int64_t n, float c, bmx_bf16 *out, void *stream);
 
+/* ------------------------------------------------------------------ */
+/* Ops of a Qwen3 attention / MLP block                                 */
+/* ------------------------------------------------------------------ */
+
+/* y[r,:] = w * bf16(x[r,:] * rsqrt(mean(x[r,:]^2) + eps)), fp32 inside;
+ * dim % 8 == 0, 16-byte aligned pointers.
+ * Replaces: mlx_rs::fast::rms_norm via RmsNorm::forward
+ *   (crates/base-mlx-core/src/model/qwen3.rs:44-55). */
+int bmx_rms_norm(const bmx_bf16 *x, const bmx_bf16 *w, bmx_bf16 *y, int64_t rows, int64_t dim, float eps,
+                 void *stream);
+
+/* Rotate-half RoPE over [H, T, D]: for i < D/2, angle = (offset + t) *
+ * theta^(-i/(D/2)); y may alias x.
+ * Replaces: mlx_rs::fast::rope(x, D, traditional=false, theta, 1.0, offset)
+ *   (crates/base-mlx-core/src/model/qwen3.rs:410-413). */
+int bmx_rope(const bmx_bf16 *x, bmx_bf16 *y, int64_t H, int64_t T, int64_t D, float theta, int64_t offset,
+             void *stream);
+
+/* In place: src[start[d]:stop[d]:strides[d] for each axis d] = update
+ * (numpy semantics, positive strides, ndim <= 8).  shape/start/stop/strides
+ * are HOST arrays; src and update are device bf16.
+ * Replaces: mlx_ext::slice_update(src, update, start, stop, strides)
+ *   (crates/base-mlx-core/src/mlx_ext.rs:36-64) -- always in place. */
+int bmx_slice_update(bmx_bf16 *src, int ndim, const int64_t *shape, const bmx_bf16 *update,
+                     const int64_t *start, const int64_t *stop, const int64_t *strides, void *stream);
+
+/* Fused QK-norm + RoPE + KV write for M new tokens at cache position
+ * `offset` (head_dim 128):  q [M, n_heads*128], k, v [M, n_kv_heads*128]
+ * (projection outputs) -> q_out [n_heads, M, 128] (normed, rotated) and
+ * k_cache/v_cache [n_kv_heads, capacity, 128] rows offset..offset+M-1.
+ * offset + M > capacity returns BMX_E_KV_CAPACITY and writes nothing.
+ * Replaces: the per-layer sequence of Qwen3::forward_internal
+ *   q_norm/k_norm -> transpose -> fast::rope -> mlx_ext::slice_update
+ *   (crates/base-mlx-core/src/model/qwen3.rs:392-489). */
+int bmx_qk_norm_rope_kv(const bmx_bf16 *q, const bmx_bf16 *k, const bmx_bf16 *v, const bmx_bf16 *q_norm,
+                        const bmx_bf16 *k_norm, bmx_bf16 *q_out, bmx_bf16 *k_cache, bmx_bf16 *v_cache, int M,
+                        int n_heads, int n_kv_heads, int head_dim, int capacity, int offset, float eps,
+                        float theta, void *stream);
+
+/* GQA attention of M queries q [n_heads, M, 128] over keys/values
+ * k_cache, v_cache [n_kv_heads, capacity, 128] rows 0..offset+M-1:
+ * out [M, n_heads*128] = softmax(scale q k^T + mask) v, query head h using
+ * kv head h / (n_heads / n_kv_heads); for M > 1 query t sees keys
+ * j <= offset + t.  `workspace` (may be NULL: no key split) holds split
+ * partials; bmx_attention_workspace_bytes(n_heads, M) is enough.
+ * Replaces: mlx_rs::fast::scaled_dot_product_attention with the
+ *   causal_mask_offset mask (crates/base-mlx-core/src/model/qwen3.rs:491-518,
+ *   629-653). */
+int bmx_attention_gqa(const bmx_bf16 *q, const bmx_bf16 *k_cache, const bmx_bf16 *v_cache, bmx_bf16 *out,
+                      int n_heads, int n_kv_heads, int M, int head_dim, int capacity, int offset, float scale,
+                      void *workspace, size_t workspace_bytes, void *stream);
+size_t bmx_attention_workspace_bytes(int n_heads, int M);
+
+/* out[r] = index of the max of x[r, 0:n] (first index on ties), uint32.
+ * Replaces: argmax / argmax_axis in pick_next and the speculative loop
+ *   (crates/base-mlx-core/src/engine.rs:195-202;
+ *   crates/base-mlx-core/src/speculative.rs:168-173, 289-293). */
+int bmx_argmax_rows(const bmx_bf16 *x, int64_t rows, int64_t n, uint32_t *out, void *stream);
+
+/* y = bf16(bf16(g * bf16(sigmoid(g))) * up), elementwise.
+ * Replaces: nn::silu(gate) * up in mlp_block
+ *   (crates/base-mlx-core/src/model/kernels.rs:73-74). */
+int bmx_silu_mul(const bmx_bf16 *gate, const bmx_bf16 *up, bmx_bf16 *y, int64_t n, void *stream);
+/* y = bf16(a + b); y may alias a or b.
+ * Replaces: the residual adds `&x + &attn`, `&x + &mlp_out[0]`
+ *   (crates/base-mlx-core/src/model/qwen3.rs:521, 541). */
+int bmx_add(const bmx_bf16 *a, const bmx_bf16 *b, bmx_bf16 *y, int64_t n, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Qwen3 model, KV cache, generation                                   */
+/* ------------------------------------------------------------------ */
+
+/* Shape parameters (ModelConfig, crates/base-mlx-core/src/model/config.rs:11-201). */
+typedef struct {
+  int hidden, inter, layers, n_heads, n_kv_heads, head_dim, vocab;
+  int tied;              /* tie_word_embeddings */
+  int group_size, bits;  /* quantization: 64, 4 */
+  float eps, rope_theta;
+} bmx_qwen3_config;
+
+typedef struct bmx_qwen3 bmx_qwen3;
+typedef struct bmx_kv_cache bmx_kv_cache;
+
+/* A Qwen3 with seeded random-init weights (projections approx N(0, sigma)
+ * quantized as bmx_init_qlinear, norms 1) and workspace for forwards of up
+ * to max_tokens tokens.
+ * Replaces: Qwen3::load (crates/base-mlx-core/src/model/qwen3.rs:194-295) for
+ *   the benchmark workloads, which use random-init weights. */
+int bmx_qwen3_create_random(const bmx_qwen3_config *cfg, uint64_t seed, double sigma, int max_tokens,
+                            bmx_qwen3 **out);
+void bmx_qwen3_destroy(bmx_qwen3 *model);
+/* Device pointers of a projection: layer >= 0 with slot 0..6 = q,k,v,o,
+ * gate,up,down; layer -1 = embed_tokens; layer -2 = lm head (tied: embed).
+ * Mirrors the tensor map of Qwen3::load (qwen3.rs:205-273). */
+int bmx_qwen3_qlinear(bmx_qwen3 *model, int layer, int slot, uint32_t **w, bmx_bf16 **scales,
+                      bmx_bf16 **biases, int *N, int *K);
+
+/* KV cache [layers, 2, n_kv_heads, capacity, 128] bf16, zero-filled.
+ * Replaces: KvCache (crates/base-mlx-core/src/model/qwen3.rs:109-162) with the
+ *   capacity a parameter instead of KV_PREALLOC (qwen3.rs:125). */
+int bmx_kv_create(const bmx_qwen3 *model, int capacity, bmx_kv_cache **out);
+void bmx_kv_destroy(bmx_kv_cache *cache);
+int bmx_kv_seq_len(const bmx_kv_cache *cache);
+int bmx_kv_capacity(const bmx_kv_cache *cache);
+/* KvCache::reset (qwen3.rs:131-135) */
+void bmx_kv_reset(bmx_kv_cache *cache);
+/* KvCache::truncate (qwen3.rs:150-161): no-op if target >= seq_len; keeps
+ * the preallocated buffer (only seq_len moves). */
+void bmx_kv_truncate(bmx_kv_cache *cache, int target);
+bmx_bf16 *bmx_kv_data(bmx_kv_cache *cache);
+/* Positions [0, seq_len) of every K/V row <- approx N(0,1) (counter
+ * (row * capacity + t) * 128 + d); sets seq_len.  Synchronises `stream`.
+ * No counterpart in the reference: a stand-in for a long prefill when
+ * only later decode steps are measured. */
+int bmx_kv_fill_synthetic(bmx_kv_cache *cache, uint64_t seed, int seq_len, void *stream);
+
+/* Forward of M tokens (HOST array) at position seq_len; logits (device)
+ * [M, vocab] if all_logits else [1, vocab] (last row); seq_len += M.
+ * Errors (no state change): BMX_E_KV_CAPACITY if seq_len + M > capacity,
+ * BMX_E_SHAPE on a cache/model mismatch, BMX_E_ARG on a token >= vocab.
+ * Replaces: Qwen3::forward / forward_multi
+ *   (crates/base-mlx-core/src/model/qwen3.rs:302-312). */
+int bmx_qwen3_forward(bmx_qwen3 *model, bmx_kv_cache *cache, const uint32_t *tokens, int M, int all_logits,
+                      bmx_bf16 *logits, void *stream);
+/* One decode step for `token` through the captured decode graph; writes
+ * the greedy next token to *next_token (host) and, if logits != NULL, the
+ * logits (device [vocab]).  Synchronises the stream.
+ * Replaces: Qwen3::forward(&[next]) + pick_next (engine.rs:114-124, 195-202). */
+int bmx_qwen3_decode_step(bmx_qwen3 *model, bmx_kv_cache *cache, uint32_t token, uint32_t *next_token,
+                          bmx_bf16 *logits, void *stream);
+/* Greedy generation: prefill `prompt` (host, P tokens), then decode until
+ * an eos token (not emitted) or max_new tokens; out (host) receives the
+ * tokens, *n_out their count.
+ * Replaces: LoadedModel::generate_text with temperature 0
+ *   (crates/base-mlx-core/src/engine.rs:100-144, 146-153, 217-223). */
+int bmx_generate_greedy(bmx_qwen3 *model, bmx_kv_cache *cache, const uint32_t *prompt, int P, int max_new,
+                        const uint32_t *eos, int n_eos, uint32_t *out, int *n_out, void *stream);
+/* Greedy speculative decoding with verify width spec_k (leader + spec_k-1
+ * drafts; the reference fixes SPEC_K = 4).  out needs max_new entries;
+ * stats (optional, 3 entries): iterations, proposed, accepted.
+ * Replaces: speculative::generate (crates/base-mlx-core/src/speculative.rs:57-286). */
+int bmx_speculative_generate(bmx_qwen3 *target, bmx_kv_cache *target_cache, bmx_qwen3 *draft,
+                             bmx_kv_cache *draft_cache, const uint32_t *prompt, int P, int max_new, int spec_k,
+                             const uint32_t *eos, int n_eos, uint32_t *out, int *n_out, int64_t *stats,
+                             void *stream);
+
 #ifdef __cplusplus
 }
 #endif

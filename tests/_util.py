@@ -46,3 +46,11 @@ def bf16_ulp_diff(a_bits, b_bits):
         return np.where(h & 0x8000, -(h & 0x7FFF), h & 0x7FFF)
 
     return np.abs(key(a_bits) - key(b_bits))
+
+
+def l2_rel_err(y, ref):
+    """||y - ref||_2 / ||ref||_2  (the end-to-end logits tolerance metric)."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.linalg.norm(ref)
+    return float(np.linalg.norm(y - ref) / (den if den > 0 else 1.0))

@@ -1,0 +1,130 @@
+"""GPU parity of the ops around the matmul and of the MFMA qmm against the
+CPU oracle on identical inputs (bf16 out; tolerances in each test)."""
+import numpy as np
+import pytest
+
+from _util import bf16_to_f32, bf16_ulp_diff, max_rel_err, to_torch_bf16, torch_bf16_bits, u32_of
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(y_bits, ref_bits, ulps=2, floor=1e-3):
+    y = bf16_to_f32(y_bits).astype(np.float64)
+    r = bf16_to_f32(ref_bits).astype(np.float64)
+    ok = np.abs(y - r) <= np.maximum(ulps * np.abs(r) * 2.0 ** -7, floor * np.max(np.abs(r)))
+    return ok.mean()
+
+
+def test_rms_norm(gpu, orc):
+    x = gpu.fill_normal_bf16(1, (37, 2560), sigma=2.0)
+    w = gpu.fill_normal_bf16(2, (2560,), sigma=0.5)
+    y = gpu.rms_norm(x, w, 1e-6)
+    ref = orc.rms_norm(torch_bf16_bits(x), torch_bf16_bits(w), 1e-6)
+    assert _close(torch_bf16_bits(y), ref) == 1.0
+
+
+@pytest.mark.parametrize("offset", [0, 1, 4095])
+def test_rope(gpu, orc, offset):
+    x = gpu.fill_normal_bf16(3, (8, 5, 128))
+    y = gpu.rope(x, 1e6, offset)
+    ref = orc.rope(torch_bf16_bits(x), 1e6, offset)
+    assert _close(torch_bf16_bits(y), ref) == 1.0
+
+
+def test_slice_update(gpu, orc):
+    import torch
+
+    src = gpu.fill_normal_bf16(4, (8, 64, 128))
+    upd = gpu.fill_normal_bf16(5, (4, 3, 32))
+    ref = torch_bf16_bits(src).copy()
+    gpu.slice_update(src, upd, [1, 2, 0], [8, 9, 128], [2, 3, 4])
+    ref[1:8:2, 2:9:3, 0:128:4] = torch_bf16_bits(upd)
+    np.testing.assert_array_equal(torch_bf16_bits(src), ref)
+    with pytest.raises(gpu.BmxError):
+        gpu.slice_update(src, upd, [1, 2, 0], [8, 9, 129], [2, 3, 4])
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M,offset", [(1, 0), (1, 100), (5, 60), (20, 0), (20, 13)])
+def test_qk_norm_rope_kv(gpu, orc, M, offset):
+    import torch
+
+    Hq, Hkv, cap = 32, 8, 128
+    q = gpu.fill_normal_bf16(6, (M, Hq * 128), sigma=3.0)
+    k = gpu.fill_normal_bf16(7, (M, Hkv * 128), sigma=3.0)
+    v = gpu.fill_normal_bf16(8, (M, Hkv * 128))
+    qn = gpu.fill_normal_bf16(9, (128,), sigma=0.3)
+    kn = gpu.fill_normal_bf16(10, (128,), sigma=0.3)
+    kc = torch.zeros(Hkv, cap, 128, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    qo = gpu.qk_norm_rope_kv(q, k, v, qn, kn, kc, vc, offset, 1e-6, 1e6)
+    torch.cuda.synchronize()
+    # oracle: per-head norm, [H, M, 128] transpose, rope, slice write
+    qb = orc.rms_norm(torch_bf16_bits(q).reshape(M * Hq, 128), torch_bf16_bits(qn)).reshape(M, Hq, 128)
+    kb = orc.rms_norm(torch_bf16_bits(k).reshape(M * Hkv, 128), torch_bf16_bits(kn)).reshape(M, Hkv, 128)
+    qr = orc.rope(np.ascontiguousarray(qb.transpose(1, 0, 2)), 1e6, offset)
+    kr = orc.rope(np.ascontiguousarray(kb.transpose(1, 0, 2)), 1e6, offset)
+    assert _close(torch_bf16_bits(qo), qr) == 1.0
+    kcg, vcg = torch_bf16_bits(kc), torch_bf16_bits(vc)
+    assert _close(kcg[:, offset:offset + M], kr) == 1.0
+    np.testing.assert_array_equal(vcg[:, offset:offset + M], torch_bf16_bits(v).reshape(M, Hkv, 128).transpose(1, 0, 2))
+    # nothing outside the written rows
+    assert not kcg[:, :offset].any() and not kcg[:, offset + M:].any()
+    with pytest.raises(gpu.BmxError) as ei:
+        gpu.qk_norm_rope_kv(q, k, v, qn, kn, kc, vc, cap - M + 1)
+    assert ei.value.code == gpu.BMX_E_KV_CAPACITY
+
+
+@pytest.mark.parametrize("Hq,Hkv,M,offset", [(32, 8, 1, 0), (32, 8, 1, 4095), (32, 8, 1, 777), (16, 8, 1, 31),
+                                             (32, 8, 5, 2043), (64, 8, 5, 300), (32, 8, 37, 0), (32, 8, 40, 100)])
+def test_attention(gpu, orc, Hq, Hkv, M, offset):
+    cap = offset + M + 5
+    q = gpu.fill_normal_bf16(11, (Hq, M, 128))
+    kc = gpu.fill_normal_bf16(12, (Hkv, cap, 128))
+    vc = gpu.fill_normal_bf16(13, (Hkv, cap, 128))
+    scale = 1 / np.sqrt(128)
+    ref = orc.sdpa(torch_bf16_bits(q), torch_bf16_bits(kc), torch_bf16_bits(vc), offset + M, offset, M > 1,
+                   np.float32(scale))
+    for ws in (True, False):
+        y = gpu.attention(q, kc, vc, offset, scale, use_workspace=ws)
+        yb = torch_bf16_bits(y)
+        assert max_rel_err(bf16_to_f32(yb), bf16_to_f32(ref)) < 1e-2
+        assert _close(yb, ref, ulps=2, floor=2e-3) > 0.999
+
+
+def test_argmax(gpu, orc):
+    x = gpu.fill_normal_bf16(14, (6, 151936))
+    xb = torch_bf16_bits(x).copy()
+    xb[1, 7] = xb[1, 151000] = orc.f32_to_bf16(np.array([30.0], np.float32))[0]
+    xb[2, :] = 0x3F80
+    got = gpu.argmax_rows(to_torch_bf16(xb)).cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), orc.argmax_rows(xb))
+    assert got[1] == 7 and got[2] == 0
+
+
+def test_silu_mul_and_add(gpu, orc):
+    g = gpu.fill_normal_bf16(15, (3, 9728), sigma=3.0)
+    u = gpu.fill_normal_bf16(16, (3, 9728))
+    y = torch_bf16_bits(gpu.silu_mul(g, u))
+    ref = orc.silu_mul(torch_bf16_bits(g), torch_bf16_bits(u))
+    assert np.max(bf16_ulp_diff(y, ref)) <= 1
+    s = torch_bf16_bits(gpu.add(g, u))
+    np.testing.assert_array_equal(s, orc.f32_to_bf16(bf16_to_f32(torch_bf16_bits(g)) + bf16_to_f32(torch_bf16_bits(u))))
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 256, 2560), (16, 1024, 2560), (64, 4096, 2560), (128, 2560, 9728),
+                                   (300, 1000, 1024), (37, 151936, 2560)])
+def test_qmm_vs_oracle(gpu, orc, M, N, K):
+    import torch
+
+    print(f"qmm M={M} N={N} K={K}", flush=True)
+    w, s, b = gpu.init_qlinear(7000 + M, N, K)
+    x = gpu.fill_normal_bf16(8000 + M, (M, K))
+    y = gpu.quantized_matmul(x, w, s, b)
+    torch.cuda.synchronize()
+    xb, wq, sb, bb = torch_bf16_bits(x), u32_of(w), torch_bf16_bits(s), torch_bf16_bits(b)
+    ref64 = orc.qmatmul_f64(xb, wq, sb, bb)
+    yb = torch_bf16_bits(y)
+    assert max_rel_err(bf16_to_f32(yb), ref64) < 1e-2
+    # same group decomposition as the oracle: within 2 bf16 ulps of it
+    assert _close(yb, orc.qmatmul(xb, wq, sb, bb), ulps=2, floor=1e-4) == 1.0

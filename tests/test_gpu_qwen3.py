@@ -1,0 +1,168 @@
+"""End-to-end parity of the GPU Qwen3 (C-ABI driver) against the CPU
+oracle on identical seeded weights: logits of every position within 2e-2
+relative (L2 over the vocabulary; bf16 activations / fp32 accumulation
+through every layer) and greedy top-1 agreement; cache semantics; greedy
+and speculative decoding."""
+import numpy as np
+import pytest
+
+from _util import bf16_to_f32, l2_rel_err, torch_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(hidden=512, inter=1536, layers=3, n_heads=8, n_kv_heads=2, head_dim=128, vocab=4096)
+
+
+def _pair(gpu, orc, seed=1, max_tokens=64, **kw):
+    shape = {**SMALL, **kw}
+    gm = gpu.Qwen3(gpu.qwen3_config(**shape), seed, 0.02, max_tokens=max_tokens)
+    om = orc.Qwen3(orc.make_config(**shape), seed, 0.02)
+    return gm, om
+
+
+def test_weights_bit_identical(gpu, orc):
+    gm, om = _pair(gpu, orc)
+    for layer, slot in [(-1, 0), (0, 0), (1, 4), (2, 6)]:
+        gw = gm.qlinear_numpy(layer, slot)
+        ow = om.qlinear(layer, slot)
+        for a, b in zip(gw, ow):
+            np.testing.assert_array_equal(a, b)
+
+
+def _check_logits(g, o, tol=2e-2):
+    g = bf16_to_f32(torch_bf16_bits(g)).reshape(o.shape).astype(np.float64)
+    o = bf16_to_f32(o).astype(np.float64)
+    rows = g.reshape(-1, g.shape[-1])
+    orows = o.reshape(-1, o.shape[-1])
+    errs = [l2_rel_err(a, b) for a, b in zip(rows, orows)]
+    agree = np.mean(np.argmax(rows, 1) == np.argmax(orows, 1))
+    print(f"logits rel err (L2) max {max(errs):.2e}, top-1 agreement {agree:.3f}", flush=True)
+    assert max(errs) < tol, errs
+    return agree
+
+
+@pytest.mark.parametrize("P", [1, 5, 8, 20, 64])
+def test_prefill_logits(gpu, orc, P):
+    gm, om = _pair(gpu, orc)
+    toks = orc.fill_tokens(100 + P, P, SMALL["vocab"])
+    gc, oc = gm.new_cache(128), om.new_cache(128)
+    g = gm.forward(gc, toks, all_logits=True)
+    o = om.forward(oc, toks, all_logits=True)
+    assert _check_logits(g, o) >= 0.9
+    assert gc.seq_len == oc.seq_len == P
+    # the KV cache rows written match the oracle's
+    for layer in range(SMALL["layers"]):
+        for kv in (0, 1):
+            ref = oc.data()[layer, kv][:, :P]
+            got = gc.layer_numpy(layer, kv)[:, :P]
+            assert l2_rel_err(bf16_to_f32(got), bf16_to_f32(ref)) < 2e-2, (layer, kv)
+
+
+def test_decode_steps_graph_vs_oracle(gpu, orc):
+    """Teacher-forced decode: the graph-captured M = 1 step after a prefill."""
+    gm, om = _pair(gpu, orc, seed=2)
+    prompt = orc.fill_tokens(7, 12, SMALL["vocab"])
+    gc, oc = gm.new_cache(64), om.new_cache(64)
+    gm.forward(gc, prompt)
+    om.forward(oc, prompt)
+    stream = orc.fill_tokens(8, 10, SMALL["vocab"])
+    agree = []
+    for t in stream:
+        nxt, g = gm.decode_step(gc, int(t), want_logits=True)
+        o = om.forward(oc, [t])
+        agree.append(_check_logits(g, o[None]))
+        assert nxt == int(np.argmax(bf16_to_f32(torch_bf16_bits(g))))
+    assert gc.seq_len == oc.seq_len == 22
+    assert np.mean(agree) >= 0.9
+
+
+def test_verify_width_5_after_prefill(gpu, orc):
+    gm, om = _pair(gpu, orc, seed=3)
+    prompt = orc.fill_tokens(9, 30, SMALL["vocab"])
+    gc, oc = gm.new_cache(64), om.new_cache(64)
+    gm.forward(gc, prompt)
+    om.forward(oc, prompt)
+    v = orc.fill_tokens(10, 5, SMALL["vocab"])
+    assert _check_logits(gm.forward(gc, v, all_logits=True), om.forward(oc, v, all_logits=True)) >= 0.8
+
+
+def test_cache_errors_and_truncate(gpu, orc):
+    gm, _ = _pair(gpu, orc, seed=4)
+    c = gm.new_cache(16)
+    toks = orc.fill_tokens(11, 12, SMALL["vocab"])
+    gm.forward(c, toks)
+    with pytest.raises(gpu.BmxError) as ei:
+        gm.forward(c, toks[:5])
+    assert ei.value.code == gpu.BMX_E_KV_CAPACITY and c.seq_len == 12
+    with pytest.raises(gpu.BmxError):
+        gm.forward(c, [SMALL["vocab"]])  # token outside the vocabulary
+    a = gm.forward(c, toks[:3], all_logits=True)
+    c.truncate(12)
+    b = gm.forward(c, toks[:3], all_logits=True)
+    np.testing.assert_array_equal(torch_bf16_bits(a), torch_bf16_bits(b))
+    other = gpu.Qwen3(gpu.qwen3_config(**{**SMALL, "layers": 2}), 1, max_tokens=8)
+    with pytest.raises(gpu.BmxError) as ei:
+        other.forward(c, toks[:1])
+    assert ei.value.code == gpu.BMX_E_SHAPE
+
+
+def test_greedy_generation_vs_oracle(gpu, orc):
+    gm, om = _pair(gpu, orc, seed=5)
+    prompt = orc.fill_tokens(12, 16, SMALL["vocab"])
+    g = gm.generate_greedy(gm.new_cache(128), prompt, 32, eos=())
+    o = orc.generate_greedy(om, om.new_cache(128), prompt, 32, eos=())
+    assert len(g) == len(o) == 32
+    # free-running greedy diverges after the first near-tie flip; the
+    # prefix before it must agree
+    first = int(np.argmax(g != o)) if np.any(g != o) else len(g)
+    assert first >= 4, (g, o)
+
+
+def test_greedy_stops_at_eos(gpu, orc):
+    gm, _ = _pair(gpu, orc, seed=6)
+    prompt = orc.fill_tokens(13, 8, SMALL["vocab"])
+    g = gm.generate_greedy(gm.new_cache(64), prompt, 12, eos=())
+    stop = int(g[3])
+    g2 = gm.generate_greedy(gm.new_cache(64), prompt, 12, eos=(stop,))
+    first = int(np.argmax(g == stop))
+    np.testing.assert_array_equal(g2, g[:first])
+
+
+def test_speculative_matches_greedy(gpu, orc):
+    target, _ = _pair(gpu, orc, seed=7)
+    draft = gpu.Qwen3(gpu.qwen3_config(**{**SMALL, "layers": 1}), 8, max_tokens=64)
+    prompt = orc.fill_tokens(14, 10, SMALL["vocab"])
+    greedy = target.generate_greedy(target.new_cache(128), prompt, 24, eos=())
+    spec, stats = gpu.speculative_generate(target, target.new_cache(128), draft, draft.new_cache(128), prompt, 24,
+                                           spec_k=5, eos=())
+    assert len(spec) == 24 and stats[0] > 0
+    first = int(np.argmax(spec != greedy)) if np.any(spec != greedy) else len(spec)
+    assert first >= 8, (spec, greedy)
+    twin = gpu.Qwen3(gpu.qwen3_config(**SMALL), 7, max_tokens=64)
+    spec2, stats2 = gpu.speculative_generate(target, target.new_cache(128), twin, twin.new_cache(128), prompt, 24,
+                                             spec_k=5, eos=())
+    assert stats2[2] >= 0.8 * stats2[1]
+
+
+def test_qwen3_4b_shape_prefill_and_decode(gpu, orc):
+    """Full Qwen3-4B shape (36 layers, 151936 vocab): short prefill + 3 decode steps.
+
+    Through 36 bf16 layers of a random-init model the logits are as
+    sensitive to fp32 summation order as they are to anything else: the
+    oracle against itself with only its group-accumulation order reversed
+    differs by 2.6-3.0e-2 (L2) on this very prompt and flips 1 of 9 argmaxes.
+    The bar here is therefore 5e-2, above that measured floor; the 3-layer
+    tests above hold the 2e-2 bar."""
+    shape = dict(hidden=2560, inter=9728, layers=36, n_heads=32, n_kv_heads=8, head_dim=128, vocab=151936)
+    print("building 4B models", flush=True)
+    gm = gpu.Qwen3(gpu.qwen3_config(**shape), 42, 0.02, max_tokens=16)
+    om = orc.Qwen3(orc.make_config(**shape), 42, 0.02)
+    print("built", flush=True)
+    prompt = orc.fill_tokens(15, 9, shape["vocab"])
+    gc, oc = gm.new_cache(64), om.new_cache(64)
+    agree = [_check_logits(gm.forward(gc, prompt, all_logits=True), om.forward(oc, prompt, all_logits=True), 5e-2)]
+    for t in orc.fill_tokens(16, 3, shape["vocab"]):
+        nxt, g = gm.decode_step(gc, int(t), want_logits=True)
+        agree.append(_check_logits(g, om.forward(oc, [t])[None], 5e-2))
+    assert np.mean(agree) >= 0.75
+    print("done", flush=True)

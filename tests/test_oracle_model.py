@@ -1,0 +1,139 @@
+"""Pins the oracle's Qwen3 forward / cache / decoding loops:
+
+* against HF transformers' Qwen3ForCausalLM (a third-party implementation
+  of the same architecture) running in float32 on the dequantized weights;
+* exact invariants of the reference's semantics: forward_multi rows equal
+  token-by-token forwards over the cache (causal_mask_offset, RoPE offset,
+  slice_update, qwen3.rs:314-563); truncate + replay reproduces logits
+  (qwen3.rs:150-161); KV overflow is an error (qwen3.rs:423-428);
+  greedy speculative decoding emits exactly the target's greedy tokens
+  (speculative.rs:1-24 "exact, no quality loss").
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import bf16_to_f32, max_rel_err
+
+TINY = dict(hidden=256, inter=512, layers=2, n_heads=4, n_kv_heads=2, head_dim=128, vocab=512)
+
+
+def tiny(orc, seed=1, **kw):
+    cfg = orc.make_config(**{**TINY, **kw})
+    return orc.Qwen3(cfg, seed, sigma=0.02)
+
+
+def test_forward_multi_rows_equal_sequential_forwards(orc):
+    m = tiny(orc)
+    toks = orc.fill_tokens(9, 12, 512)
+    c1 = m.new_cache(64)
+    multi = m.forward(c1, toks[:7], all_logits=True)
+    more = m.forward(c1, toks[7:], all_logits=True)  # offset > 0, M > 1
+    c2 = m.new_cache(64)
+    seq = np.stack([m.forward(c2, toks[i:i + 1]) for i in range(12)])
+    np.testing.assert_array_equal(np.concatenate([multi, more]), seq)
+    assert c1.seq_len == c2.seq_len == 12
+    np.testing.assert_array_equal(c1.data(), c2.data())
+
+
+def test_truncate_then_replay_reproduces_logits(orc):
+    m = tiny(orc)
+    toks = orc.fill_tokens(10, 10, 512)
+    c = m.new_cache(32)
+    m.forward(c, toks[:6])
+    a = m.forward(c, toks[6:], all_logits=True)
+    c.truncate(6)
+    assert c.seq_len == 6
+    c.truncate(8)  # no-op when target >= seq_len
+    assert c.seq_len == 6
+    b = m.forward(c, toks[6:], all_logits=True)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_kv_capacity_error_leaves_cache(orc):
+    m = tiny(orc)
+    c = m.new_cache(8)
+    m.forward(c, orc.fill_tokens(1, 6, 512))
+    snap = c.data().copy()
+    with pytest.raises(RuntimeError):
+        m.forward(c, orc.fill_tokens(2, 3, 512))
+    assert c.seq_len == 6
+    np.testing.assert_array_equal(c.data(), snap)
+
+
+def _hf_model(orc, m, cfg):
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+
+    hc = Qwen3Config(vocab_size=cfg.vocab, hidden_size=cfg.hidden, intermediate_size=cfg.inter,
+                     num_hidden_layers=cfg.layers, num_attention_heads=cfg.n_heads,
+                     num_key_value_heads=cfg.n_kv_heads, head_dim=cfg.head_dim, rope_theta=cfg.rope_theta,
+                     rms_norm_eps=cfg.eps, tie_word_embeddings=True, max_position_embeddings=4096,
+                     attention_bias=False)
+    hf = Qwen3ForCausalLM(hc).float().eval()
+
+    def deq(layer, slot):
+        w, s, b = m.qlinear(layer, slot)
+        return torch.from_numpy(bf16_to_f32(orc.dequantize(w, s, b)))
+
+    sd = {"model.embed_tokens.weight": deq(-1, 0)}
+    names = ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+             "mlp.up_proj", "mlp.down_proj"]
+    for l in range(cfg.layers):
+        for sl, n in enumerate(names):
+            sd[f"model.layers.{l}.{n}.weight"] = deq(l, sl)
+    with torch.no_grad():
+        for k, p in hf.named_parameters():
+            if k in sd:
+                p.copy_(sd[k])
+            elif k.endswith("norm.weight"):
+                p.fill_(1.0)
+            elif k != "lm_head.weight":
+                raise AssertionError(f"unmapped parameter {k}")
+        hf.tie_weights()
+    return hf
+
+
+def test_forward_matches_transformers_qwen3(orc):
+    m = tiny(orc, seed=3)
+    cfg = m.cfg
+    hf = _hf_model(orc, m, cfg)
+    toks = orc.fill_tokens(11, 16, cfg.vocab)
+    with torch.no_grad():
+        ref = hf(torch.from_numpy(toks.astype(np.int64))[None]).logits[0].double().numpy()
+    c = m.new_cache(32)
+    got = bf16_to_f32(m.forward(c, toks, all_logits=True)).astype(np.float64)
+    for t in range(16):
+        assert max_rel_err(got[t], ref[t]) < 3e-2, t
+    agree = np.mean(np.argmax(got, 1) == np.argmax(ref, 1))
+    assert agree >= 0.8
+
+
+def test_greedy_generate_follows_forward(orc):
+    m = tiny(orc, seed=4)
+    prompt = orc.fill_tokens(12, 8, 512)
+    c = m.new_cache(64)
+    out = orc.generate_greedy(m, c, prompt, 10, eos=())
+    assert len(out) == 10
+    # replay: each emitted token is the argmax of the forward that preceded it
+    c2 = m.new_cache(64)
+    logits = m.forward(c2, prompt)
+    for t in out:
+        assert int(np.argmax(bf16_to_f32(logits))) == t
+        logits = m.forward(c2, [t])
+
+
+def test_speculative_emits_the_greedy_tokens(orc):
+    target = tiny(orc, seed=5)
+    draft = tiny(orc, seed=6, layers=1)
+    prompt = orc.fill_tokens(13, 8, 512)
+    greedy = orc.generate_greedy(target, target.new_cache(128), prompt, 24, eos=())
+    spec, stats = orc.speculative_generate(target, target.new_cache(128), draft, draft.new_cache(128), prompt, 24,
+                                           spec_k=5, eos=())
+    np.testing.assert_array_equal(spec, greedy)
+    assert stats[0] > 0 and stats[1] >= stats[2]
+    # a draft identical to the target is always accepted
+    twin = tiny(orc, seed=5)
+    spec2, stats2 = orc.speculative_generate(target, target.new_cache(128), twin, twin.new_cache(128), prompt, 24,
+                                             spec_k=5, eos=())
+    np.testing.assert_array_equal(spec2, greedy)
+    assert stats2[1] == stats2[2] and stats2[1] > 0
