@@ -44,7 +44,11 @@ struct AttnParams {
   float scale;
 };
 
-template <int W, int IT>
+// KP = true: the PV product splits the chunk's keys over the W waves (each
+// wave accumulates all R <= IT rows over its 64 keys, partials added across
+// waves at the end) -- the decode / verify shape.  KP = false: rows split
+// over waves, each wave walks all keys (prefill).
+template <int W, int IT, bool KP>
 __global__ void __launch_bounds__(W * 64) attn_kernel(const AttnParams p) {
   constexpr int CH = 64 * W;  // keys per chunk
   extern __shared__ __align__(16) unsigned char smem[];
@@ -78,7 +82,7 @@ __global__ void __launch_bounds__(W * 64) attn_kernel(const AttnParams p) {
     st[r * 3 + 0] = -INFINITY;
     st[r * 3 + 1] = 0.0f;
   }
-  // PV accumulators: thread owns dims (2*lane, 2*lane+1) of rows wave + W*it
+  // PV accumulators: dims (2*lane, 2*lane+1) of rows it (KP) or wave + W*it
   float acc[IT][2];
 #pragma unroll
   for (int it = 0; it < IT; it++) acc[it][0] = acc[it][1] = 0.0f;
@@ -136,28 +140,43 @@ __global__ void __launch_bounds__(W * 64) attn_kernel(const AttnParams p) {
       }
     }
     __syncthreads();
-    // ---- PV: thread = (row wave + W*it, dims 2*lane .. 2*lane+1) ----
+    // ---- PV ----
     {
-      const int nk = min(CH, kend - c0);
+      constexpr int UNR = 8;
 #pragma unroll
       for (int it = 0; it < IT; it++) {
-        const int r = wave + W * it;
+        const int r = KP ? it : wave + W * it;
         if (r < R) {
           const float alpha = st[r * 3 + 2];
           acc[it][0] *= alpha;
           acc[it][1] *= alpha;
         }
       }
-      for (int c = 0; c < nk; c++) {
-        const uint32_t vv = *reinterpret_cast<const uint32_t*>(vb + static_cast<int64_t>(c0 + c) * kD + 2 * lane);
-        const float v0 = bf2f(vv & 0xffffu), v1 = bf2f(vv >> 16);
+      // keys [kb0, kb1) of this wave; masked / out-of-range keys have p = 0
+      const int kb0 = KP ? c0 + wave * 64 : c0;
+      const int nk = KP ? max(0, min(64, kend - kb0)) : min(CH, kend - c0);
+      const int pc0 = KP ? wave * 64 : 0;
+      for (int c = 0; c < nk; c += UNR) {
+        float v0[UNR], v1[UNR];
 #pragma unroll
-        for (int it = 0; it < IT; it++) {
-          const int r = wave + W * it;
-          if (r < R) {
-            const float pv = ps[r * CH + c];
-            acc[it][0] += pv * v0;
-            acc[it][1] += pv * v1;
+        for (int u = 0; u < UNR; u++) {
+          const int key = kb0 + min(c + u, nk - 1);
+          const uint32_t vv = *reinterpret_cast<const uint32_t*>(vb + static_cast<int64_t>(key) * kD + 2 * lane);
+          v0[u] = bf2f(vv & 0xffffu);
+          v1[u] = bf2f(vv >> 16);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+          if (c + u < nk) {
+#pragma unroll
+            for (int it = 0; it < IT; it++) {
+              const int r = KP ? it : wave + W * it;
+              if (r < R) {
+                const float pv = ps[r * CH + pc0 + c + u];
+                acc[it][0] += pv * v0[u];
+                acc[it][1] += pv * v1[u];
+              }
+            }
           }
         }
       }
@@ -165,10 +184,31 @@ __global__ void __launch_bounds__(W * 64) attn_kernel(const AttnParams p) {
     __syncthreads();
   }
 
+  if (KP) {
+    // add the W waves' partials: wave 0 ends up with the totals
+    float* red = st + R * 3;  // [W][IT][128], its own region after the softmax state
+    if (wave > 0) {
+#pragma unroll
+      for (int it = 0; it < IT; it++) {
+        red[((wave * IT + it) * kD) + 2 * lane] = acc[it][0];
+        red[((wave * IT + it) * kD) + 2 * lane + 1] = acc[it][1];
+      }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int w2 = 1; w2 < W; w2++) {
+#pragma unroll
+      for (int it = 0; it < IT; it++) {
+        acc[it][0] += red[((w2 * IT + it) * kD) + 2 * lane];
+        acc[it][1] += red[((w2 * IT + it) * kD) + 2 * lane + 1];
+      }
+    }
+  }
+
   // ---- write ----
 #pragma unroll
   for (int it = 0; it < IT; it++) {
-    const int r = wave + W * it;
+    const int r = KP ? it : wave + W * it;
     if (r >= R) continue;
     const int j = r / tn, i = r - j * tn;
     const int h = kvh * rep + j, t = t0 + i;
@@ -191,23 +231,209 @@ __global__ void __launch_bounds__(W * 64) attn_kernel(const AttnParams p) {
   }
 }
 
-// merge NS partials of each (head, token); one wave per pair
+// Decode / short verify (R = tokens x heads-per-kv-head <= RMAX <= 8).  A
+// workgroup of 4 waves owns one kv head and 256 keys, 64 per wave.  Every
+// K, V and q load of the wave is issued up front, before any arithmetic:
+//   QK on MFMA (v_mfma_f32_16x16x32_bf16): A = the R query rows (padded to
+//     16; lane l holds row l%16, dims 32*ks + 8*(l/16), 4 fragments read
+//     straight from global: the R rows of one kv head are contiguous in
+//     [Hq, M, 128]), B = K^T (lane l holds key l%16 of each 16-key tile,
+//     same dims).  The result tile puts key l%16 and rows 4*(l/16)+i in
+//     lane l; scores are scaled after the exact bf16 x bf16 products.
+//   softmax over the wave's 64 keys: registers + xor shuffles in 16-lane
+//     groups; p goes to LDS.
+//   PV on VALU: lane = (8 dims li, 16-key quarter g), fp32 FMAs, quarters
+//     added with xor shuffles.
+// The 4 waves' (o, m, l) are merged in LDS and one unnormalised partial per
+// workgroup goes to the split workspace (NS = ceil(L / 256)).
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+constexpr int kDecWaves = 4, kDecKeys = 64 * kDecWaves;
+
+template <int RMAX>
+__global__ void __launch_bounds__(256) attn_decode_kernel(const AttnParams p) {
+  __shared__ float ps[kDecWaves][RMAX][64];
+  __shared__ __align__(16) float os[kDecWaves][RMAX][kD];
+  __shared__ float ms[kDecWaves][RMAX], ls[kDecWaves][RMAX];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int li = lane & 15, g = lane >> 4;
+  const int tn = p.M;
+  const int R = tn * (p.Hq / p.Hkv);  // row r = j * tn + i: head kvh*rep + j, token i
+  const int kvh = blockIdx.x, split = blockIdx.y;
+  const int offset = p.offset_dev ? *p.offset_dev : p.offset;
+  const int L = offset + p.M;
+  const int c0 = split * kDecKeys + wave * 64;
+  const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
+  // ---- issue loads: q fragments, K fragments, V rows ----
+  uint4 qa[4];
+  {
+    const uint16_t* qrow = p.q + (static_cast<int64_t>(kvh) * R + min(li, R - 1)) * kD + g * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) qa[ks] = *reinterpret_cast<const uint4*>(qrow + ks * 32);
+  }
+  uint4 kb[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int key = max(min(c0 + t * 16 + li, L - 1), 0);
+    const uint16_t* krow = p.k + hbase + static_cast<int64_t>(key) * kD + g * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) kb[t][ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
+  }
+  uint4 vr[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int key = max(min(c0 + g * 16 + i, L - 1), 0);
+    vr[i] = *reinterpret_cast<const uint4*>(p.v + hbase + static_cast<int64_t>(key) * kD + li * 8);
+  }
+  if (li >= R) qa[0] = qa[1] = qa[2] = qa[3] = make_uint4(0, 0, 0, 0);
+  // ---- S = q K^T on MFMA ----
+  f32x4_t sc[4];
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    sc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+      sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[ks]),
+                                                      __builtin_bit_cast(bf16x8_t, kb[t][ks]), sc[t], 0, 0, 0);
+  }
+  // ---- softmax of the wave's 64 keys; lane holds rows 4g + i ----
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = 4 * g + i;
+    const int ti = r - (r / tn) * tn;
+    const int lim = p.causal ? min(L, offset + ti + 1) : L;  // keys < lim are visible
+    float s[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      s[t] = (c0 + t * 16 + li < lim) ? sc[t][i] * p.scale : -INFINITY;
+      mx = fmaxf(mx, s[t]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+    float l = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const float e = (mx == -INFINITY) ? 0.0f : expf(s[t] - mx);
+      l += e;
+      if (r < R) ps[wave][r][t * 16 + li] = e;
+    }
+    l += __shfl_xor(l, 1, 64);
+    l += __shfl_xor(l, 2, 64);
+    l += __shfl_xor(l, 4, 64);
+    l += __shfl_xor(l, 8, 64);
+    if (r < R && li == 0) {
+      ms[wave][r] = mx;
+      ls[wave][r] = l;
+    }
+  }
+  __syncthreads();
+  // ---- PV: lane = (dims 8 li .. 8 li + 7, keys 16 g .. 16 g + 15 of the wave) ----
+  float acc[RMAX][8];
+#pragma unroll
+  for (int r = 0; r < RMAX; r++)
+#pragma unroll
+    for (int d = 0; d < 8; d++) acc[r][d] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const uint32_t v4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+    float vf[8];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      vf[2 * d] = bf2f(v4[d] & 0xffffu);
+      vf[2 * d + 1] = bf2f(v4[d] >> 16);
+    }
+#pragma unroll
+    for (int r = 0; r < RMAX; r++) {
+      if (r >= R) break;
+      const float pv = ps[wave][r][g * 16 + i];
+#pragma unroll
+      for (int d = 0; d < 8; d++) acc[r][d] += pv * vf[d];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RMAX; r++) {
+    if (r >= R) break;
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+      acc[r][d] += __shfl_xor(acc[r][d], 16, 64);
+      acc[r][d] += __shfl_xor(acc[r][d], 32, 64);
+    }
+    if (g == 0) {
+      float4* o = reinterpret_cast<float4*>(&os[wave][r][li * 8]);
+      o[0] = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+      o[1] = make_float4(acc[r][4], acc[r][5], acc[r][6], acc[r][7]);
+    }
+  }
+  __syncthreads();
+  // ---- merge the 4 waves; thread = (row, 4 dims) ----
+  for (int e = threadIdx.x; e < R * (kD / 4); e += 256) {
+    const int r = e / (kD / 4), d4 = e - r * (kD / 4);
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; w++) m = fmaxf(m, ms[w][r]);
+    float l = 0.0f;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (m != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kDecWaves; w++) {
+        if (ms[w][r] == -INFINITY) continue;
+        const float a = expf(ms[w][r] - m);
+        const float4 ow = *reinterpret_cast<const float4*>(&os[w][r][d4 * 4]);
+        l += a * ls[w][r];
+        o.x += a * ow.x;
+        o.y += a * ow.y;
+        o.z += a * ow.z;
+        o.w += a * ow.w;
+      }
+    }
+    const int64_t base = (static_cast<int64_t>(kvh) * R + r) * p.ns + split;  // (h * M + token) * ns + split
+    *reinterpret_cast<float4*>(p.part_o + base * kD + d4 * 4) = o;
+    if (d4 == 0) *reinterpret_cast<float2*>(p.part_ml + base * 2) = make_float2(m, l);
+  }
+}
+
+// Merges the NS partials (o, m, l) of each (head, token); one wave per pair,
+// lane = 2 dims.  Up to 32 splits are read per batch (all loads in flight),
+// batches folded with an online rescale.
 __global__ void __launch_bounds__(256) attn_combine_kernel(const AttnParams p) {
   const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (wid >= p.Hq * p.M) return;
   const int h = wid / p.M, t = wid - h * p.M;
   const int64_t base = static_cast<int64_t>(wid) * p.ns;
-  float mx = -INFINITY;
-  for (int s = 0; s < p.ns; s++) mx = fmaxf(mx, p.part_ml[(base + s) * 2]);
-  float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (int s = 0; s < p.ns; s++) {
-    const float m = p.part_ml[(base + s) * 2];
-    if (m == -INFINITY) continue;
-    const float w = expf(m - mx);
-    l += w * p.part_ml[(base + s) * 2 + 1];
-    o0 += w * p.part_o[(base + s) * kD + 2 * lane];
-    o1 += w * p.part_o[(base + s) * kD + 2 * lane + 1];
+  constexpr int B = 32;
+  float mx = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  for (int s0 = 0; s0 < p.ns; s0 += B) {
+    float2 ml[B], ov[B];
+#pragma unroll
+    for (int u = 0; u < B; u++) {
+      const int s = min(s0 + u, p.ns - 1);
+      ml[u] = *reinterpret_cast<const float2*>(p.part_ml + (base + s) * 2);
+      ov[u] = *reinterpret_cast<const float2*>(p.part_o + (base + s) * kD + 2 * lane);
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < B; u++)
+      if (s0 + u < p.ns) bm = fmaxf(bm, ml[u].x);
+    const float nm = fmaxf(mx, bm);
+    if (nm == -INFINITY) continue;
+    const float a = (mx == -INFINITY) ? 0.0f : expf(mx - nm);
+    l *= a;
+    o0 *= a;
+    o1 *= a;
+#pragma unroll
+    for (int u = 0; u < B; u++) {
+      if (s0 + u >= p.ns || ml[u].x == -INFINITY) continue;
+      const float w = expf(ml[u].x - nm);
+      l += w * ml[u].y;
+      o0 += w * ov[u].x;
+      o1 += w * ov[u].y;
+    }
+    mx = nm;
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   uint16_t* o = p.out + static_cast<int64_t>(t) * p.Hq * kD + h * kD + 2 * lane;
@@ -217,13 +443,18 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const AttnParams p) {
 
 template <int W>
 int launch_w(const AttnParams& p, dim3 grid, int R, hipStream_t st) {
+  // q rows, scores of one chunk, softmax state; plus the cross-wave partials
+  // [W][IT][128] of the key-split variant
   const size_t lds = static_cast<size_t>(R) * (kD + 64 * W + 3) * 4;
-  const int it = (R + W - 1) / W;
+  const size_t red4 = static_cast<size_t>(W) * 4 * kD * 4, red8 = static_cast<size_t>(W) * 8 * kD * 4;
   if (R > 32 || R < 1) return set_error(BMX_E_SHAPE, "attention: %d query rows per workgroup", R);
-  if (it <= 1) hipLaunchKernelGGL((attn_kernel<W, 1>), grid, dim3(W * 64), lds, st, p);
-  else if (it <= 2) hipLaunchKernelGGL((attn_kernel<W, 2>), grid, dim3(W * 64), lds, st, p);
-  else if (it <= 4) hipLaunchKernelGGL((attn_kernel<W, 4>), grid, dim3(W * 64), lds, st, p);
-  else hipLaunchKernelGGL((attn_kernel<W, 8>), grid, dim3(W * 64), lds, st, p);
+  if (R <= 4) hipLaunchKernelGGL((attn_kernel<W, 4, true>), grid, dim3(W * 64), lds + red4, st, p);
+  else if (R <= 8) hipLaunchKernelGGL((attn_kernel<W, 8, true>), grid, dim3(W * 64), lds + red8, st, p);
+  else {
+    const int it = (R + W - 1) / W;
+    if (it <= 4) hipLaunchKernelGGL((attn_kernel<W, 4, false>), grid, dim3(W * 64), lds, st, p);
+    else hipLaunchKernelGGL((attn_kernel<W, 8, false>), grid, dim3(W * 64), lds, st, p);
+  }
   return check_launch("attention");
 }
 
@@ -258,12 +489,24 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || M <= 0) return set_error(BMX_E_SHAPE, "attention: bad head counts");
   if (!offset_dev && (offset < 0 || offset + M > cap))
     return set_error(BMX_E_KV_CAPACITY, "attention: %d positions exceed capacity %d", offset + M, cap);
-  int tq, ns, w;
   const int max_ns = ws ? static_cast<int>(ws_floats / (static_cast<size_t>(Hq) * M * (kD + 2))) : 1;
+  const int rep = Hq / Hkv;
+  const int chunks = (L_max + kDecKeys - 1) / kDecKeys;
+  if (ws && M * rep <= 8 && chunks <= max_ns) {
+    // 256 keys per workgroup, splits merged by the combine kernel
+    AttnParams p{q, k, v, out, ws, ws + static_cast<size_t>(Hq) * M * chunks * kD, offset_dev, offset,
+                 Hq, Hkv, M, cap, M, chunks, M > 1 ? 1 : 0, scale};
+    const dim3 grid(Hkv, chunks);
+    if (M * rep <= 4) hipLaunchKernelGGL((attn_decode_kernel<4>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((attn_decode_kernel<8>), grid, dim3(256), 0, stream, p);
+    if (int rc = check_launch("attention_decode")) return rc;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((Hq * M + 3) / 4), dim3(256), 0, stream, p);
+    return check_launch("attention_combine");
+  }
+  int tq, ns, w;
   attention_shape(Hq, Hkv, M, L_max, max_ns, &tq, &ns, &w);
   AttnParams p{q, k, v, out, ws, ws ? ws + static_cast<size_t>(Hq) * M * ns * kD : nullptr, offset_dev, offset,
                Hq, Hkv, M, cap, tq, ns, M > 1 ? 1 : 0, scale};
-  const int rep = Hq / Hkv;
   const dim3 grid(Hkv, (M + tq - 1) / tq, ns);
   if (int rc = launch_w<4>(p, grid, tq * rep, stream)) return rc;
   if (ns > 1) {
@@ -278,8 +521,8 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
 using namespace bmx;
 
 extern "C" size_t bmx_attention_workspace_bytes(int n_heads, int M) {
-  // splits are bounded by 64 for any call
-  return attention_workspace_floats(n_heads, M, 64) * sizeof(float);
+  // enough for one split per 64 keys of a 16384-position cache
+  return attention_workspace_floats(n_heads, M, 256) * sizeof(float);
 }
 
 extern "C" int bmx_attention_gqa(const bmx_bf16* q, const bmx_bf16* k_cache, const bmx_bf16* v_cache, bmx_bf16* out,

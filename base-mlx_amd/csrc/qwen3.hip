@@ -368,7 +368,10 @@ extern "C" int bmx_qwen3_create_random(const bmx_qwen3_config* cfg, uint64_t see
   if (!rc) rc = dalloc_t(m, &m->u, T * I);
   if (!rc) rc = dalloc_t(m, &m->a, T * I);
   if (!rc) rc = dalloc_t(m, &m->logits1, static_cast<size_t>(cfg->vocab));
-  m->attn_ws_floats = attention_workspace_floats(cfg->n_heads, 16, 64);
+  // split partials: one split per 64 keys for decode (up to 16384 cached
+  // positions), 64 splits for short verify forwards
+  m->attn_ws_floats = std::max(attention_workspace_floats(cfg->n_heads, 1, 256),
+                               attention_workspace_floats(cfg->n_heads, 16, 64));
   if (!rc) rc = dalloc_t(m, &m->attn_ws, m->attn_ws_floats);
   if (!rc) rc = dalloc_t(m, &m->ids, T);
   if (!rc) rc = dalloc_t(m, &m->tok_u, T < 64 ? 64 : T);

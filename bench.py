@@ -1,0 +1,204 @@
+"""Benchmark: Qwen3-4B-shaped 4-bit decode at batch 1 on one MI355X, plus the
+qmv sweep over the Qwen3-4B projection shapes.
+
+Workload (the headline `value`): a random-init Qwen3-4B-shaped model
+(hidden 2560, intermediate 9728, 36 layers, 32 q / 8 kv heads, head_dim 128,
+vocab 151936, MLX 4-bit gs64), KV cache [36, 2, 8, 4352, 128] bf16, a
+4096-token seeded random prompt prefilled untimed, then greedy decode.  One
+step = one decode token: a graph launch of the whole forward (36 layers +
+lm_head + argmax) and the 4-byte readback of the token, as the reference's
+generate loop syncs once per token.  `value` = decode tokens / s.
+
+`roofline`: the qmv GEMV at the gate/up projection shape (9728 x 2560),
+timed with HIP events around a graph of launches on the benchmark stream,
+rotating over >= 1 GiB of distinct weights so no launch reads from the
+256 MB Infinity Cache; algorithmic bytes per launch = 0.5625 N K + 2 K + 2 N.
+
+`cpu_baseline`: the C restatement of the same decode step (oracle/, OpenMP)
+on this host's cores, timed over a bounded sample of decode tokens at context
+4096 (KV positions filled synthetically instead of a CPU prefill).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "base-mlx_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+HBM_PEAK_GBS = 8000.0
+SHAPE_4B = dict(hidden=2560, inter=9728, layers=36, n_heads=32, n_kv_heads=8, head_dim=128, vocab=151936)
+QMV_SHAPES = [(4096, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (2560, 9728), (151936, 2560)]
+ROOF_SHAPE = (9728, 2560)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def qmv_bytes(N, K, M=1):
+    return int(0.5625 * N * K + 2 * M * K + 2 * M * N)
+
+
+def time_qmv(bmx, torch, N, K, reps=200, M=1):
+    """Average duration (us) of one qmv launch, graph-captured, rotating over
+    >= 1 GiB of distinct weights; HIP events on the capturing stream."""
+    nbytes = qmv_bytes(N, K, M)
+    copies = max(2, -(-(1 << 30) // nbytes))
+    ws = [bmx.init_qlinear(5000 + i, N, K) for i in range(copies)]
+    x = bmx.fill_normal_bf16(77, (M, K))
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    reps = max(reps, copies)
+    st = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        for i in range(4):
+            bmx.quantized_matmul(x, *ws[i % copies], out=y)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=st):
+            for i in range(reps):
+                bmx.quantized_matmul(x, *ws[i % copies], out=y)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        g.replay()
+        g.replay()
+        e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / (2 * reps)
+    del g, ws
+    torch.cuda.empty_cache()
+    return us, nbytes
+
+
+def cpu_baseline(tokens, ctx=4096, seed=42):
+    """Oracle decode of `tokens` tokens at context `ctx` on the host cores."""
+    import numpy as np
+
+    import oracle
+
+    cfg = oracle.make_config(**SHAPE_4B)
+    t0 = time.time()
+    m = oracle.Qwen3(cfg, seed, 0.02)
+    cache = m.new_cache(ctx + tokens + 1)
+    cache.fill_synthetic(1234, ctx)
+    log(f"cpu baseline: model + cache ready in {time.time() - t0:.1f}s")
+    tok = np.array([1], np.uint32)
+    m.forward(cache, tok)  # first step untimed (page-in)
+    t0 = time.time()
+    for _ in range(tokens):
+        logits = m.forward(cache, tok)
+        tok = np.array([int(np.argmax(oracle.bf16_to_f32(logits)))], np.uint32)
+    dt = time.time() - t0
+    m.close()
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return tokens / dt, cores
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="timed decode tokens")
+    ap.add_argument("--warmup", type=int, default=16, help="untimed decode tokens (rewound afterwards)")
+    ap.add_argument("--prompt", type=int, default=4096)
+    ap.add_argument("--cpu-tokens", type=int, default=8, help="decode tokens in the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs on one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import bmx
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    cap = args.prompt + args.steps
+    assert args.prompt + max(args.steps, args.warmup) <= cap
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        log("building Qwen3-4B-shaped model")
+        model = bmx.Qwen3(bmx.qwen3_config(**SHAPE_4B), 42, 0.02, max_tokens=min(args.prompt, 4096))
+        cache = model.new_cache(max(cap, 4352))
+        prompt = np.array([int(v) for v in np.random.default_rng(11).integers(0, 151936, args.prompt)], np.uint32)
+        torch.cuda.synchronize()
+        t0 = time.time()
+        logits = model.forward(cache, prompt)
+        tok = int(torch.argmax(logits.float()).item())
+        torch.cuda.synchronize()
+        prefill_s = time.time() - t0
+        log(f"prefill {args.prompt} tokens: {prefill_s * 1000:.1f} ms")
+        # warmup (captures the decode graph), then rewind to the prompt
+        t = tok
+        for _ in range(args.warmup):
+            t = model.decode_step(cache, t)
+        cache.truncate(args.prompt)
+        torch.cuda.synchronize()
+        # timed region: exactly `steps` decode tokens from position 4096
+        t = tok
+        toks = []
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            t = model.decode_step(cache, t)
+            toks.append(t)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+    tok_s = args.steps / dt
+    log(f"decode {args.steps} tokens at ctx {args.prompt}: {dt * 1000 / args.steps:.3f} ms/token, {tok_s:.1f} tok/s")
+    model.close()
+    del cache
+    torch.cuda.empty_cache()
+
+    sweep = []
+    roof = None
+    if not args.no_sweep:
+        for (N, K) in QMV_SHAPES:
+            us, nb = time_qmv(bmx, torch, N, K)
+            gbs = nb / us / 1e3
+            sweep.append({"N": N, "K": K, "us": round(us, 3), "GB/s": round(gbs, 1),
+                          "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            log(f"qmv N={N} K={K}: {us:.2f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
+            if (N, K) == ROOF_SHAPE:
+                roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "kernel": f"qmv M=1 N={N} K={K}", "avg_launch_us": round(us, 3), "bytes_per_launch": nb}
+
+    cpu = None
+    if not args.no_cpu:
+        v, cores = cpu_baseline(args.cpu_tokens)
+        cpu = {"value": round(v, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+               "sample": f"{args.cpu_tokens} greedy decode tokens of the same Qwen3-4B shape at context 4096 "
+                         f"(KV positions 0..4095 filled synthetically), oracle/ C restatement, OpenMP"}
+        log(f"cpu baseline: {v:.3f} tok/s on {cores} threads")
+
+    out = {
+        "metric": "decode tok/s Qwen3-4B-shape 4-bit bs1; qmv GB/s as % of HBM peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1000 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 activations, u4 weights (MLX affine gs64), fp32 accumulate",
+        "data": "synthetic: seeded random-init weights N(0,0.02) quantized 4-bit, seeded random token ids",
+        "config": {"workload": "Qwen3-4B-shape 4-bit greedy decode, batch 1, after a 4096-token prefill",
+                   "prompt_tokens": args.prompt, "kv_cache": [36, 2, 8, max(cap, 4352), 128],
+                   "prefill_ms": round(prefill_s * 1000, 1), "qmv_sweep": sweep},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -164,5 +164,9 @@ def test_qwen3_4b_shape_prefill_and_decode(gpu, orc):
     for t in orc.fill_tokens(16, 3, shape["vocab"]):
         nxt, g = gm.decode_step(gc, int(t), want_logits=True)
         agree.append(_check_logits(g, om.forward(oc, [t])[None], 5e-2))
+    # an 8-token verify forward: the M = 8 GEMV path with the fused norm
+    # taking its separate pass over x (8 x 2560 values)
+    v = orc.fill_tokens(17, 8, shape["vocab"])
+    agree.append(_check_logits(gm.forward(gc, v, all_logits=True), om.forward(oc, v, all_logits=True), 5e-2))
     assert np.mean(agree) >= 0.75
     print("done", flush=True)
