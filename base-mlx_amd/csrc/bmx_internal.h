@@ -30,6 +30,7 @@ struct QmvSegment {
   uint16_t* y;        // [M, rows] (row stride = rows)
   int rows;
   int row0;  // first global output row of this segment
+  int blk0;  // first workgroup of this segment (set by launch_qmv)
 };
 
 struct QmvParams {

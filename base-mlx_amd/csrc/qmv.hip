@@ -52,6 +52,14 @@ __device__ __forceinline__ uint4 permute_pairs(uint4 d) {
   return r;
 }
 
+// floor(a / b) for 0 <= a < 2^20 and b >= 1, from rcp_b = 1.0f / b (correctly
+// rounded): (a + 0.5) / b lies at least 0.5 / b from an integer, while the
+// product's relative error is below 2^-22, i.e. below (a + 0.5) / b * 2^-22
+// < 0.5 / b whenever a + 0.5 < 2^21.
+__device__ __forceinline__ int udiv_small(int a, float rcp_b) {
+  return static_cast<int>((static_cast<float>(a) + 0.5f) * rcp_b);
+}
+
 // Dot of one packed word (8 nibbles) with its permuted x pairs, +128 bias.
 __device__ __forceinline__ float word_dot(uint32_t w, uint4 xp, float acc) {
   const uint32_t magic = 0x43004300u;
@@ -82,31 +90,25 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
   uint32_t* sbs = reinterpret_cast<uint32_t*>(sxs + MT * CP);               // [NH][RB][GP]
   float* red = reinterpret_cast<float*>(sbs + NH * RB * GP);                // [4][MT]
 
-  const int row0 = blockIdx.x * RB;
-  const int rl = wave * SLOTS + slot;  // row within the workgroup
-  const int row = row0 + rl;
-  const bool valid = row < p.N;
-
-  // segment + local row of a global output row
-  auto seg_of = [&](int r) {
-    int sg = 0;
-    if (EPI != QMV_SWIGLU) {
-      if (p.nseg > 1 && r >= p.seg[1].row0) sg = 1;
-      if (p.nseg > 2 && r >= p.seg[2].row0) sg = 2;
-    }
-    return sg;
-  };
-  const uint32_t* wrow[NH];
+  // Segments start on workgroup boundaries, so the segment (and every
+  // kernel-argument field read through it) is uniform across the workgroup
+  // and is read with scalar loads.
   int seg = 0;
+  if constexpr (EPI != QMV_SWIGLU) {
+    if (p.nseg > 1 && static_cast<int>(blockIdx.x) >= p.seg[1].blk0) seg = 1;
+    if (p.nseg > 2 && static_cast<int>(blockIdx.x) >= p.seg[2].blk0) seg = 2;
+  }
+  const int rows = p.seg[seg].rows;
+  const int row0 = (static_cast<int>(blockIdx.x) - p.seg[seg].blk0) * RB;  // first row of the workgroup
+  const int rl = wave * SLOTS + slot;  // row within the workgroup
+  const int row = row0 + rl;           // row within the segment
+  const bool valid = row < rows;
+
+  const uint32_t* wrow[NH];
   {
-    const int rr = valid ? row : 0;
-    if constexpr (EPI == QMV_SWIGLU) {
+    const int64_t rr = min(row, rows - 1);
 #pragma unroll
-      for (int h = 0; h < NH; h++) wrow[h] = p.seg[h].w + static_cast<int64_t>(rr) * (K / 8);
-    } else {
-      seg = seg_of(rr);
-      wrow[0] = p.seg[seg].w + static_cast<int64_t>(rr - p.seg[seg].row0) * (K / 8);
-    }
+    for (int h = 0; h < NH; h++) wrow[h] = p.seg[EPI == QMV_SWIGLU ? h : seg].w + rr * (K / 8);
   }
 
   // Register ring of U chunks (see header).
@@ -189,34 +191,33 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
     //      workgroup's s|b words.  Each batch issues all of its loads before
     //      consuming any, so their latencies overlap (and overlap W). ----
     const int gunits = gpp / 8;  // 16-byte s/b units per row
-    const int sb_units = p.sb_vec ? NH * RB * gunits : NH * RB * gpp;
+    const int sb_units = p.sb_vec ? RB * gunits : RB * gpp;  // per weight matrix
+    const float rcp_words = 1.0f / static_cast<float>(words);
+    const float rcp_gu = 1.0f / static_cast<float>(p.sb_vec ? gunits : gpp);
     for (int b0x = 0, b0s = 0; b0x < total || b0s < sb_units; b0x += kThreads * XU, b0s += kThreads * SU) {
       uint4 xr[XU];
-      uint4 sr[SU], br[SU];
+      uint4 sr[NH][SU], br[NH][SU];
 #pragma unroll
       for (int i = 0; i < XU; i++) {
         const int idx = b0x + i * kThreads + threadIdx.x;
         xr[i] = make_uint4(0, 0, 0, 0);
         if (idx < total) {
-          const int m = idx / words;
+          const int m = (MT == 1) ? 0 : udiv_small(idx, rcp_words);
           if (m < M) xr[i] = *reinterpret_cast<const uint4*>(p.x + m * p.ldx + k0 + (idx - m * words) * 8);
         }
       }
       if (p.sb_vec) {
 #pragma unroll
-        for (int i = 0; i < SU; i++) {
-          const int e = b0s + i * kThreads + threadIdx.x;
-          if (e < sb_units) {
-            const int h = e / (RB * gunits);
-            const int rem = e - h * (RB * gunits);
-            const int r = rem / gunits;
-            const int gr = row0 + r;
-            if (gr < p.N) {
-              const int sg = (EPI == QMV_SWIGLU) ? h : seg_of(gr);
-              const int64_t off = static_cast<int64_t>(gr - (EPI == QMV_SWIGLU ? 0 : p.seg[sg].row0)) * G +
-                                  gbase + (rem - r * gunits) * 8;
-              sr[i] = *reinterpret_cast<const uint4*>(p.seg[sg].s + off);
-              br[i] = *reinterpret_cast<const uint4*>(p.seg[sg].b + off);
+        for (int h = 0; h < NH; h++) {
+          const QmvSegment& sgm = p.seg[EPI == QMV_SWIGLU ? h : seg];
+#pragma unroll
+          for (int i = 0; i < SU; i++) {
+            const int e = b0s + i * kThreads + threadIdx.x;
+            const int r = udiv_small(e, rcp_gu);
+            if (e < sb_units && row0 + r < rows) {
+              const int64_t off = static_cast<int64_t>(row0 + r) * G + gbase + (e - r * gunits) * 8;
+              sr[h][i] = *reinterpret_cast<const uint4*>(sgm.s + off);
+              br[h][i] = *reinterpret_cast<const uint4*>(sgm.b + off);
             }
           }
         }
@@ -226,7 +227,7 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
       for (int i = 0; i < XU; i++) {
         const int idx = b0x + i * kThreads + threadIdx.x;
         const bool act = idx < total;
-        const int m = act ? idx / words : 0;
+        const int m = (MT == 1 || !act) ? 0 : udiv_small(idx, rcp_words);
         const int j = act ? idx - m * words : 0;
         uint4 d = xr[i];
         float part = 0.0f;
@@ -255,42 +256,27 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
         }
       }
       // consume s|b
-      if (p.sb_vec) {
+#pragma unroll
+      for (int h = 0; h < NH; h++) {
+        const QmvSegment& sgm = p.seg[EPI == QMV_SWIGLU ? h : seg];
 #pragma unroll
         for (int i = 0; i < SU; i++) {
           const int e = b0s + i * kThreads + threadIdx.x;
-          if (e < sb_units) {
-            const int h = e / (RB * gunits);
-            const int rem = e - h * (RB * gunits);
-            const int r = rem / gunits;
-            if (row0 + r < p.N) {
-              const uint32_t s4[4] = {sr[i].x, sr[i].y, sr[i].z, sr[i].w};
-              const uint32_t b4[4] = {br[i].x, br[i].y, br[i].z, br[i].w};
-              uint32_t* dst = sbs + (h * RB + r) * GP + (rem - r * gunits) * 8;
+          const int r = udiv_small(e, rcp_gu);
+          if (e >= sb_units || row0 + r >= rows) continue;
+          if (p.sb_vec) {
+            const uint32_t s4[4] = {sr[h][i].x, sr[h][i].y, sr[h][i].z, sr[h][i].w};
+            const uint32_t b4[4] = {br[h][i].x, br[h][i].y, br[h][i].z, br[h][i].w};
+            uint32_t* dst = sbs + (h * RB + r) * GP + (e - r * gunits) * 8;
 #pragma unroll
-              for (int q = 0; q < 4; q++) {
-                dst[2 * q] = (s4[q] & 0xffffu) | (b4[q] << 16);
-                dst[2 * q + 1] = (s4[q] >> 16) | (b4[q] & 0xffff0000u);
-              }
+            for (int q = 0; q < 4; q++) {
+              dst[2 * q] = (s4[q] & 0xffffu) | (b4[q] << 16);
+              dst[2 * q + 1] = (s4[q] >> 16) | (b4[q] & 0xffff0000u);
             }
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < SU; i++) {
-          const int e = b0s + i * kThreads + threadIdx.x;
-          if (e < sb_units) {
-            const int h = e / (RB * gpp);
-            const int rem = e - h * (RB * gpp);
-            const int r = rem / gpp;
-            const int g = rem - r * gpp;
-            const int gr = row0 + r;
-            if (gr < p.N) {
-              const int sg = (EPI == QMV_SWIGLU) ? h : seg_of(gr);
-              const int64_t off = static_cast<int64_t>(gr - (EPI == QMV_SWIGLU ? 0 : p.seg[sg].row0)) * G + gbase + g;
-              sbs[(h * RB + r) * GP + g] = static_cast<uint32_t>(p.seg[sg].s[off]) |
-                                           (static_cast<uint32_t>(p.seg[sg].b[off]) << 16);
-            }
+          } else {
+            const int g = e - r * gpp;
+            const int64_t off = static_cast<int64_t>(row0 + r) * G + gbase + g;
+            sbs[(h * RB + r) * GP + g] = static_cast<uint32_t>(sgm.s[off]) | (static_cast<uint32_t>(sgm.b[off]) << 16);
           }
         }
       }
@@ -346,8 +332,7 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
     for (int m = 0; m < MT; m++) {
       if (m >= M) break;
       if constexpr (EPI == QMV_STORE) {
-        const QmvSegment& sg = p.seg[seg];
-        sg.y[static_cast<int64_t>(m) * sg.rows + (row - sg.row0)] = f2bf(acc[0][m]);
+        p.seg[seg].y[static_cast<int64_t>(m) * rows + row] = f2bf(acc[0][m]);
       } else if constexpr (EPI == QMV_RESIDUAL) {
         // x = x + o_proj(attn) in bf16 (qwen3.rs:520-521, 541)
         const int64_t o = static_cast<int64_t>(m) * p.N + row;
@@ -447,7 +432,18 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   const int CP = p.kp / 32, GP = p.kp / 64;
   const size_t lds = static_cast<size_t>(mt) * CP * (kChunkBytes + 4) +
                      static_cast<size_t>(nh) * rows_per_block * GP * 4 + 4 * static_cast<size_t>(mt) * 4;
-  const int blocks = (p.N + rows_per_block - 1) / rows_per_block;
+  // every segment starts on a workgroup boundary (the kernel reads its
+  // segment's fields with scalar loads)
+  int blocks = 0;
+  if (epi == QMV_SWIGLU) {
+    blocks = (p.N + rows_per_block - 1) / rows_per_block;
+    for (int i = 0; i < p.nseg; i++) p.seg[i].blk0 = 0;
+  } else {
+    for (int i = 0; i < p.nseg; i++) {
+      p.seg[i].blk0 = blocks;
+      blocks += (p.seg[i].rows + rows_per_block - 1) / rows_per_block;
+    }
+  }
   // 16-byte staging of s/b needs whole 8-group units at 16-byte alignment
   p.sb_vec = (p.K % 512) == 0;
   for (int i = 0; i < p.nseg; i++)
