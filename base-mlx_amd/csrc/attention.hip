@@ -232,28 +232,28 @@ __global__ void __launch_bounds__(W * 64) attn_kernel(const AttnParams p) {
 }
 
 // Decode / short verify (R = tokens x heads-per-kv-head <= RMAX <= 8).  A
-// workgroup of 4 waves owns one kv head and 256 keys, 64 per wave.  Every
-// K, V and q load of the wave is issued up front, before any arithmetic:
+// workgroup of 8 waves owns one kv head and 256 keys, 32 per wave.  Every
+// K, V and q load of a wave is issued before any arithmetic:
 //   QK on MFMA (v_mfma_f32_16x16x32_bf16): A = the R query rows (padded to
 //     16; lane l holds row l%16, dims 32*ks + 8*(l/16), 4 fragments read
 //     straight from global: the R rows of one kv head are contiguous in
 //     [Hq, M, 128]), B = K^T (lane l holds key l%16 of each 16-key tile,
 //     same dims).  The result tile puts key l%16 and rows 4*(l/16)+i in
 //     lane l; scores are scaled after the exact bf16 x bf16 products.
-//   softmax over the wave's 64 keys: registers + xor shuffles in 16-lane
-//     groups; p goes to LDS.
-//   PV on VALU: lane = (8 dims li, 16-key quarter g), fp32 FMAs, quarters
-//     added with xor shuffles.
-// The 4 waves' (o, m, l) are merged in LDS and one unnormalised partial per
+//   softmax over the wave's 32 keys: registers + DPP reductions inside
+//     16-lane rows; p goes to LDS as [key][row].
+//   PV on VALU: lane = 2 dims over all 32 keys (V read one 256-byte key row
+//     per load instruction), so no cross-lane reduction is needed.
+// The 8 waves' (o, m, l) are merged in LDS and one unnormalised partial per
 // workgroup goes to the split workspace (NS = ceil(L / 256)).
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
-constexpr int kDecWaves = 4, kDecKeys = 64 * kDecWaves;
+constexpr int kDecWaves = 8, kDecWaveKeys = 32, kDecKeys = kDecWaveKeys * kDecWaves;
 
 template <int RMAX>
-__global__ void __launch_bounds__(256) attn_decode_kernel(const AttnParams p) {
-  __shared__ float ps[kDecWaves][RMAX][64];
+__global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnParams p) {
+  __shared__ __align__(16) float ps[kDecWaves][kDecWaveKeys][RMAX];
   __shared__ __align__(16) float os[kDecWaves][RMAX][kD];
   __shared__ float ms[kDecWaves][RMAX], ls[kDecWaves][RMAX];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -263,7 +263,7 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const AttnParams p) {
   const int kvh = blockIdx.x, split = blockIdx.y;
   const int offset = p.offset_dev ? *p.offset_dev : p.offset;
   const int L = offset + p.M;
-  const int c0 = split * kDecKeys + wave * 64;
+  const int c0 = split * kDecKeys + wave * kDecWaveKeys;
   const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
   // ---- issue loads: q fragments, K fragments, V rows ----
   uint4 qa[4];
@@ -272,105 +272,82 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const AttnParams p) {
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) qa[ks] = *reinterpret_cast<const uint4*>(qrow + ks * 32);
   }
-  uint4 kb[4][4];
+  uint4 kb[2][4];
 #pragma unroll
-  for (int t = 0; t < 4; t++) {
+  for (int t = 0; t < 2; t++) {
     const int key = max(min(c0 + t * 16 + li, L - 1), 0);
     const uint16_t* krow = p.k + hbase + static_cast<int64_t>(key) * kD + g * 8;
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) kb[t][ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
   }
-  uint4 vr[16];
+  uint32_t vr[kDecWaveKeys];
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const int key = max(min(c0 + g * 16 + i, L - 1), 0);
-    vr[i] = *reinterpret_cast<const uint4*>(p.v + hbase + static_cast<int64_t>(key) * kD + li * 8);
+  for (int k = 0; k < kDecWaveKeys; k++) {
+    const int key = max(min(c0 + k, L - 1), 0);
+    vr[k] = *reinterpret_cast<const uint32_t*>(p.v + hbase + static_cast<int64_t>(key) * kD + 2 * lane);
   }
   if (li >= R) qa[0] = qa[1] = qa[2] = qa[3] = make_uint4(0, 0, 0, 0);
   // ---- S = q K^T on MFMA ----
-  f32x4_t sc[4];
+  f32x4_t sc[2];
 #pragma unroll
-  for (int t = 0; t < 4; t++) {
+  for (int t = 0; t < 2; t++) {
     sc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int ks = 0; ks < 4; ks++)
       sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[ks]),
                                                       __builtin_bit_cast(bf16x8_t, kb[t][ks]), sc[t], 0, 0, 0);
   }
-  // ---- softmax of the wave's 64 keys; lane holds rows 4g + i ----
+  // ---- softmax of the wave's 32 keys; lane holds rows 4g + i ----
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int r = 4 * g + i;
     const int ti = r - (r / tn) * tn;
     const int lim = p.causal ? min(L, offset + ti + 1) : L;  // keys < lim are visible
-    float s[4];
-    float mx = -INFINITY;
+    float s[2];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      s[t] = (c0 + t * 16 + li < lim) ? sc[t][i] * p.scale : -INFINITY;
-      mx = fmaxf(mx, s[t]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
-    float l = 0.0f;
+    for (int t = 0; t < 2; t++) s[t] = (c0 + t * 16 + li < lim) ? sc[t][i] * p.scale : -INFINITY;
+    const float mx = row16_max(fmaxf(s[0], s[1]));
+    float e[2];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const float e = (mx == -INFINITY) ? 0.0f : expf(s[t] - mx);
-      l += e;
-      if (r < R) ps[wave][r][t * 16 + li] = e;
-    }
-    l += __shfl_xor(l, 1, 64);
-    l += __shfl_xor(l, 2, 64);
-    l += __shfl_xor(l, 4, 64);
-    l += __shfl_xor(l, 8, 64);
-    if (r < R && li == 0) {
-      ms[wave][r] = mx;
-      ls[wave][r] = l;
+    for (int t = 0; t < 2; t++) e[t] = (mx == -INFINITY) ? 0.0f : expf(s[t] - mx);
+    const float l = row16_sum(e[0] + e[1]);
+    if (r < R) {
+#pragma unroll
+      for (int t = 0; t < 2; t++) ps[wave][t * 16 + li][r] = e[t];
+      if (li == 0) {
+        ms[wave][r] = mx;
+        ls[wave][r] = l;
+      }
     }
   }
   __syncthreads();
-  // ---- PV: lane = (dims 8 li .. 8 li + 7, keys 16 g .. 16 g + 15 of the wave) ----
-  float acc[RMAX][8];
+  // ---- PV: lane = dims 2 lane, 2 lane + 1 over the wave's 32 keys ----
+  float acc[RMAX][2];
 #pragma unroll
-  for (int r = 0; r < RMAX; r++)
+  for (int r = 0; r < RMAX; r++) acc[r][0] = acc[r][1] = 0.0f;
 #pragma unroll
-    for (int d = 0; d < 8; d++) acc[r][d] = 0.0f;
+  for (int k = 0; k < kDecWaveKeys; k++) {
+    const float v0 = bf2f(vr[k] & 0xffffu), v1 = bf2f(vr[k] >> 16);
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const uint32_t v4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
-    float vf[8];
+    for (int r4 = 0; r4 < RMAX; r4 += 4) {
+      if (r4 >= R) break;
+      const float4 pv = *reinterpret_cast<const float4*>(&ps[wave][k][r4]);
+      const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
-    for (int d = 0; d < 4; d++) {
-      vf[2 * d] = bf2f(v4[d] & 0xffffu);
-      vf[2 * d + 1] = bf2f(v4[d] >> 16);
-    }
-#pragma unroll
-    for (int r = 0; r < RMAX; r++) {
-      if (r >= R) break;
-      const float pv = ps[wave][r][g * 16 + i];
-#pragma unroll
-      for (int d = 0; d < 8; d++) acc[r][d] += pv * vf[d];
+      for (int q = 0; q < 4; q++) {
+        acc[r4 + q][0] += pr[q] * v0;
+        acc[r4 + q][1] += pr[q] * v1;
+      }
     }
   }
 #pragma unroll
   for (int r = 0; r < RMAX; r++) {
     if (r >= R) break;
-#pragma unroll
-    for (int d = 0; d < 8; d++) {
-      acc[r][d] += __shfl_xor(acc[r][d], 16, 64);
-      acc[r][d] += __shfl_xor(acc[r][d], 32, 64);
-    }
-    if (g == 0) {
-      float4* o = reinterpret_cast<float4*>(&os[wave][r][li * 8]);
-      o[0] = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
-      o[1] = make_float4(acc[r][4], acc[r][5], acc[r][6], acc[r][7]);
-    }
+    *reinterpret_cast<float2*>(&os[wave][r][2 * lane]) = make_float2(acc[r][0], acc[r][1]);
   }
   __syncthreads();
-  // ---- merge the 4 waves; thread = (row, 4 dims) ----
-  for (int e = threadIdx.x; e < R * (kD / 4); e += 256) {
+  // ---- merge the waves; thread = (row, 4 dims) ----
+  for (int e = threadIdx.x; e < R * (kD / 4); e += 64 * kDecWaves) {
     const int r = e / (kD / 4), d4 = e - r * (kD / 4);
     float m = -INFINITY;
 #pragma unroll
@@ -497,8 +474,8 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
     AttnParams p{q, k, v, out, ws, ws + static_cast<size_t>(Hq) * M * chunks * kD, offset_dev, offset,
                  Hq, Hkv, M, cap, M, chunks, M > 1 ? 1 : 0, scale};
     const dim3 grid(Hkv, chunks);
-    if (M * rep <= 4) hipLaunchKernelGGL((attn_decode_kernel<4>), grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((attn_decode_kernel<8>), grid, dim3(256), 0, stream, p);
+    if (M * rep <= 4) hipLaunchKernelGGL((attn_decode_kernel<4>), grid, dim3(64 * kDecWaves), 0, stream, p);
+    else hipLaunchKernelGGL((attn_decode_kernel<8>), grid, dim3(64 * kDecWaves), 0, stream, p);
     if (int rc = check_launch("attention_decode")) return rc;
     hipLaunchKernelGGL(attn_combine_kernel, dim3((Hq * M + 3) / 4), dim3(256), 0, stream, p);
     return check_launch("attention_combine");

@@ -36,6 +36,30 @@ __device__ __forceinline__ T wave_sum_xor(T v, int width) {
   return v;
 }
 
+// DPP lane moves within 16-lane rows (gfx9 dpp_ctrl encodings):
+// quad_perm [1,0,3,2] = 0xB1 (lane ^ 1), quad_perm [2,3,0,1] = 0x4E
+// (lane ^ 2), row_ror:4 = 0x124 and row_ror:8 = 0x128 (rotations by 4 and 8
+// inside the row; the reductions below do not depend on the direction).
+// Every source lane lies inside its row, so no lane reads a disabled or
+// out-of-row source.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// max / sum over each 16-lane row; every lane of the row gets the result
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x124>(v));
+  return fmaxf(v, dpp_f32<0x128>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x124>(v);
+  return v + dpp_f32<0x128>(v);
+}
+
 // Same counter-based generator as the oracle (splitmix64 finalizer).
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {
   z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
