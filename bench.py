@@ -34,6 +34,20 @@ QMV_SHAPES = [(4096, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (2560, 972
 ROOF_SHAPE = (9728, 2560)
 
 
+def measured_traffic():
+    """HBM bytes per launch of the roofline GEMV, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE scaled by a copy of
+    known size); None when that summary is absent."""
+    path = os.path.join(ROOT, "profiles", "qmv_9728x2560_pmc.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -75,6 +89,29 @@ def time_qmv(bmx, torch, N, K, reps=200, M=1):
     return us, nbytes
 
 
+def profile_roofline(bmx, torch, launches=200):
+    """Counter-collection workload: the roofline GEMV shape launched eagerly
+    (rotating over >= 1 GiB of weights), then a plain 256 MiB device copy as
+    the calibration kernel whose FETCH_SIZE / WRITE_SIZE must read 256 MiB."""
+    N, K = ROOF_SHAPE
+    nbytes = qmv_bytes(N, K)
+    copies = max(2, -(-(1 << 30) // nbytes))
+    ws = [bmx.init_qlinear(5000 + i, N, K) for i in range(copies)]
+    x = bmx.fill_normal_bf16(77, (1, K))
+    y = torch.empty(1, N, dtype=torch.bfloat16, device="cuda")
+    for i in range(launches):
+        bmx.quantized_matmul(x, *ws[i % copies], out=y)
+    torch.cuda.synchronize()
+    del ws
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"profile-roofline: {launches} qmv launches N={N} K={K} ({nbytes} algorithmic bytes each), "
+        f"10 copies of {256 << 20} bytes")
+
+
 def cpu_baseline(tokens, ctx=4096, seed=42):
     """Oracle decode of `tokens` tokens at context `ctx` on the host cores."""
     import numpy as np
@@ -108,6 +145,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=8, help="decode tokens in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--profile-roofline", action="store_true",
+                    help="only run the roofline GEMV and a copy of known size (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)", file=sys.stderr)
@@ -119,6 +158,9 @@ def main():
     import bmx
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.profile_roofline:
+        profile_roofline(bmx, torch)
+        return
     cap = args.prompt + args.steps
     assert args.prompt + max(args.steps, args.warmup) <= cap
     stream = torch.cuda.Stream()
@@ -167,7 +209,7 @@ def main():
             log(f"qmv N={N} K={K}: {us:.2f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
             if (N, K) == ROOF_SHAPE:
                 roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                         "kernel": f"qmv M=1 N={N} K={K}", "avg_launch_us": round(us, 3), "bytes_per_launch": nb}
 
     cpu = None
