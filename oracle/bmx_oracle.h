@@ -15,6 +15,18 @@
  * Conventions: bf16 values are passed as raw uint16_t bit patterns; all
  * arrays are row-major and contiguous; fp32 accumulation, bf16 outputs
  * rounded to nearest-even, as the reference's bf16 models produce.
+ *
+ * Pinning.  The reference holds no tests or golden vectors for this path
+ * and cannot be built or imported here (Rust over mlx-rs; MLX's kernels are
+ * Metal), so each function is checked against closed forms, library
+ * routines and invariants (tests/test_oracle_*.py) and against the
+ * closed-form fixtures of tests/golden/ (tests/test_golden.py).  Parity
+ * unpinned -- only an MLX import could pin these bits: the exact output of
+ * MLX's own quantizer (orc_quantize_affine follows the documented formula;
+ * op parity does not depend on it since both sides consume the same packed
+ * tensors), the accumulation order inside MLX's quantized_matmul, the
+ * internal precision of MLX's fast::rms_norm / rope / SDPA, MLX's
+ * end-to-end logits and its argmax tie-break.
  */
 #ifndef BMX_ORACLE_H
 #define BMX_ORACLE_H
