@@ -46,10 +46,16 @@ struct QmvParams {
   float eps;
   int kp;      // K columns staged in LDS per phase (set by launch_qmv)
   int sb_vec;  // s/b staged with 16-byte loads (set by launch_qmv)
+  // QMV_STORE with one segment: optional per-workgroup argmax partials of
+  // the bf16 outputs, (value bits, row) at [m * qmv_blocks(...) + workgroup]
+  uint2* amax;
 };
 
 // Validates shapes/alignment and launches the qmv kernel family.
 int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream);
+// Workgroups launch_qmv uses for these parameters (the count of argmax
+// partials per x row).
+int qmv_blocks(const QmvParams& p, QmvEpilogue epi);
 
 // ---- other kernels (one launch each, errors recorded) --------------------
 int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M,
@@ -69,10 +75,11 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
                      size_t ws_floats, int Hq, int Hkv, int M, int D, int cap, int offset, const int* offset_dev,
                      int L_max, float scale, hipStream_t stream);
 int launch_argmax(const uint16_t* x, int64_t rows, int64_t n, uint32_t* out, hipStream_t stream);
+// Reduces `nblk` argmax partials per row (from the qmv epilogue) to out[rows].
+int launch_argmax_partials(const uint2* part, int rows, int nblk, uint32_t* out, hipStream_t stream);
 int launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* y, int64_t n, hipStream_t stream);
 int launch_add(const uint16_t* a, const uint16_t* b, uint16_t* y, int64_t n, hipStream_t stream);
 int launch_tokens_to_ids(const uint32_t* src, int32_t* dst, int n, hipStream_t stream);
-int launch_add_scalar(int* v, int d, hipStream_t stream);
 int launch_dequant_gather(const int32_t* ids, int64_t M, int64_t rows, const uint32_t* w, const uint16_t* s,
                           const uint16_t* b, uint16_t* out, int64_t K, hipStream_t stream);
 int launch_init_qlinear(uint64_t seed, int64_t N, int64_t K, float c, uint32_t* w, uint16_t* s, uint16_t* b,

@@ -20,21 +20,11 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
   return v > bv || (v == bv && i < bi);
 }
 
-// one workgroup per row
-__global__ void __launch_bounds__(kArgThreads)
-    argmax_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t* __restrict__ out) {
+// (value, index) reduction across a workgroup of kArgThreads; the result is
+// valid in thread 0.
+__device__ __forceinline__ void block_best(float& bv, uint32_t& bi) {
   __shared__ float sv[kArgThreads / 64];
   __shared__ uint32_t si[kArgThreads / 64];
-  const uint16_t* xr = x + static_cast<int64_t>(blockIdx.x) * n;
-  float bv = -INFINITY;
-  uint32_t bi = 0xffffffffu;
-  for (int64_t i = threadIdx.x; i < n; i += kArgThreads) {
-    const float v = bf2f(xr[i]);
-    if (better(v, static_cast<uint32_t>(i), bv, bi)) {
-      bv = v;
-      bi = static_cast<uint32_t>(i);
-    }
-  }
   for (int off = 32; off > 0; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
     const uint32_t oi = __shfl_xor(bi, off, 64);
@@ -55,9 +45,81 @@ __global__ void __launch_bounds__(kArgThreads)
         bv = sv[w];
         bi = si[w];
       }
-    // all -inf / NaN rows: index 0
-    out[blockIdx.x] = bi == 0xffffffffu ? 0u : bi;
   }
+}
+
+// one workgroup per row; rows of a multiple of 8 values at 16-byte
+// alignment are read 8 values per load, 8 loads in flight per thread
+__global__ void __launch_bounds__(kArgThreads)
+    argmax_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t* __restrict__ out) {
+  const uint16_t* xr = x + static_cast<int64_t>(blockIdx.x) * n;
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  if (n % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    const uint4* xv = reinterpret_cast<const uint4*>(xr);
+    const int64_t nv = n / 8;
+    constexpr int B = 8;
+    for (int64_t j0 = threadIdx.x; j0 < nv; j0 += static_cast<int64_t>(kArgThreads) * B) {
+      uint4 d[B];
+#pragma unroll
+      for (int u = 0; u < B; u++) {
+        const int64_t j = j0 + static_cast<int64_t>(u) * kArgThreads;
+        d[u] = j < nv ? xv[j] : make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u);  // -inf
+      }
+#pragma unroll
+      for (int u = 0; u < B; u++) {
+        const uint32_t w[4] = {d[u].x, d[u].y, d[u].z, d[u].w};
+        const uint32_t base = static_cast<uint32_t>((j0 + static_cast<int64_t>(u) * kArgThreads) * 8);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float v = bf2f((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+          if (better(v, base + e, bv, bi)) {
+            bv = v;
+            bi = base + e;
+          }
+        }
+      }
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < n; i += kArgThreads) {
+      const float v = bf2f(xr[i]);
+      if (better(v, static_cast<uint32_t>(i), bv, bi)) {
+        bv = v;
+        bi = static_cast<uint32_t>(i);
+      }
+    }
+  }
+  block_best(bv, bi);
+  // all -inf / NaN rows: index 0
+  if (threadIdx.x == 0) out[blockIdx.x] = bi == 0xffffffffu ? 0u : bi;
+}
+
+// one workgroup per row over the per-workgroup partials (value bits, index)
+// of the GEMV epilogue
+__global__ void __launch_bounds__(kArgThreads)
+    argmax_partials_kernel(const uint2* __restrict__ part, int nblk, uint32_t* __restrict__ out) {
+  const uint2* pr = part + static_cast<int64_t>(blockIdx.x) * nblk;
+  float bv = -INFINITY;
+  uint32_t bi = 0xffffffffu;
+  constexpr int B = 8;
+  for (int j0 = threadIdx.x; j0 < nblk; j0 += kArgThreads * B) {
+    uint2 d[B];
+#pragma unroll
+    for (int u = 0; u < B; u++) {
+      const int j = j0 + u * kArgThreads;
+      d[u] = j < nblk ? pr[j] : make_uint2(0xff800000u, 0xffffffffu);
+    }
+#pragma unroll
+    for (int u = 0; u < B; u++) {
+      const float v = __uint_as_float(d[u].x);
+      if (better(v, d[u].y, bv, bi)) {
+        bv = v;
+        bi = d[u].y;
+      }
+    }
+  }
+  block_best(bv, bi);
+  if (threadIdx.x == 0) out[blockIdx.x] = bi == 0xffffffffu ? 0u : bi;
 }
 
 __global__ void __launch_bounds__(256)
@@ -83,10 +145,6 @@ __global__ void tokens_to_ids_kernel(const uint32_t* __restrict__ src, int32_t* 
   if (i < n) dst[i] = static_cast<int32_t>(src[i]);
 }
 
-__global__ void add_scalar_kernel(int* v, int d) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) *v += d;
-}
-
 }  // namespace
 
 int launch_argmax(const uint16_t* x, int64_t rows, int64_t n, uint32_t* out, hipStream_t stream) {
@@ -95,6 +153,13 @@ int launch_argmax(const uint16_t* x, int64_t rows, int64_t n, uint32_t* out, hip
   if (rows > INT32_MAX) return set_error(BMX_E_SHAPE, "argmax: rows=%lld", (long long)rows);
   hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(rows)), dim3(kArgThreads), 0, stream, x, n, out);
   return check_launch("argmax");
+}
+
+int launch_argmax_partials(const uint2* part, int rows, int nblk, uint32_t* out, hipStream_t stream) {
+  if (rows <= 0) return BMX_OK;
+  if (nblk <= 0) return set_error(BMX_E_SHAPE, "argmax partials: %d per row", nblk);
+  hipLaunchKernelGGL(argmax_partials_kernel, dim3(rows), dim3(kArgThreads), 0, stream, part, nblk, out);
+  return check_launch("argmax_partials");
 }
 
 int launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* y, int64_t n, hipStream_t stream) {
@@ -113,11 +178,6 @@ int launch_tokens_to_ids(const uint32_t* src, int32_t* dst, int n, hipStream_t s
   if (n <= 0) return BMX_OK;
   hipLaunchKernelGGL(tokens_to_ids_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, src, dst, n);
   return check_launch("tokens_to_ids");
-}
-
-int launch_add_scalar(int* v, int d, hipStream_t stream) {
-  hipLaunchKernelGGL(add_scalar_kernel, dim3(1), dim3(64), 0, stream, v, d);
-  return check_launch("add_scalar");
 }
 
 }  // namespace bmx

@@ -89,6 +89,8 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
   float* sxs = reinterpret_cast<float*>(smem + MT * CP * kChunkBytes);      // [MT][CP]
   uint32_t* sbs = reinterpret_cast<uint32_t*>(sxs + MT * CP);               // [NH][RB][GP]
   float* red = reinterpret_cast<float*>(sbs + NH * RB * GP);                // [4][MT]
+  float* amv = red + 4 * MT;                                                 // [MT][RB] (argmax partials)
+  uint32_t* ami = reinterpret_cast<uint32_t*>(amv + MT * RB);                // [MT][RB]
 
   // Segments start on workgroup boundaries, so the segment (and every
   // kernel-argument field read through it) is uniform across the workgroup
@@ -348,6 +350,34 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
       }
     }
   }
+  if constexpr (EPI == QMV_STORE) {
+    if (p.amax != nullptr) {
+      // argmax partial of the workgroup's rows (first index on ties)
+      if (sl == 0) {
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+          const bool ok = valid && m < M;
+          amv[m * RB + rl] = ok ? bf2f(f2bf(acc[0][m])) : -INFINITY;
+          ami[m * RB + rl] = ok ? static_cast<uint32_t>(row) : 0xffffffffu;
+        }
+      }
+      __syncthreads();
+      if (static_cast<int>(threadIdx.x) < M) {
+        const int m = threadIdx.x;
+        float bv = -INFINITY;
+        uint32_t bi = 0xffffffffu;
+        for (int r = 0; r < RB; r++) {
+          const float v = amv[m * RB + r];
+          const uint32_t i = ami[m * RB + r];
+          if (v > bv || (v == bv && i < bi)) {
+            bv = v;
+            bi = i;
+          }
+        }
+        p.amax[static_cast<int64_t>(m) * gridDim.x + blockIdx.x] = make_uint2(__float_as_uint(bv), bi);
+      }
+    }
+  }
 }
 
 template <int MT, int EPI>
@@ -400,7 +430,38 @@ int pick_lanes_per_row(int N, int K) {
   return best;
 }
 
+struct QmvGrid {
+  int mt, S, rows_per_block, blocks;
+  int blk0[3];
+};
+
+// Tile shape and grid of one launch: lanes per row S (tuning override
+// BMX_QMV_LANES = 8/16/32/64), rows per workgroup, and the first workgroup of
+// each segment (segments start on workgroup boundaries; SWIGLU's two
+// matrices share every workgroup).
+QmvGrid qmv_grid(const QmvParams& p, QmvEpilogue epi) {
+  QmvGrid g{};
+  g.mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : p.m <= 5 ? 5 : 8;
+  g.S = (g.mt == 1) ? pick_lanes_per_row(p.N, p.K) : (p.K / 32 >= 64 ? 64 : 16);
+  if (const char* e = getenv("BMX_QMV_LANES")) {
+    const int v = atoi(e);
+    if (v == 16 || v == 64 || (g.mt == 1 && (v == 8 || v == 32))) g.S = v;
+  }
+  g.rows_per_block = (kThreads / 64) * (64 / g.S);
+  if (epi == QMV_SWIGLU) {
+    g.blocks = (p.N + g.rows_per_block - 1) / g.rows_per_block;
+  } else {
+    for (int i = 0; i < p.nseg && i < 3; i++) {
+      g.blk0[i] = g.blocks;
+      g.blocks += (p.seg[i].rows + g.rows_per_block - 1) / g.rows_per_block;
+    }
+  }
+  return g;
+}
+
 }  // namespace
+
+int qmv_blocks(const QmvParams& p, QmvEpilogue epi) { return qmv_grid(p, epi).blocks; }
 
 int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   if (p.m < 1 || p.m > 8) return set_error(BMX_E_SHAPE, "qmv: M=%d outside 1..8", p.m);
@@ -414,15 +475,12 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
       return set_error(BMX_E_ARG, "qmv: null pointer in segment %d", i);
     if (!aligned(p.seg[i].w, 16)) return set_error(BMX_E_ALIGN, "qmv: W must be 16-byte aligned");
   }
-  int mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : p.m <= 5 ? 5 : 8;
-  int S = (mt == 1) ? pick_lanes_per_row(p.N, p.K) : (p.K / 32 >= 64 ? 64 : 16);
-  // Tuning override: BMX_QMV_LANES = lanes per output row (8/16/32/64).
-  if (const char* e = getenv("BMX_QMV_LANES")) {
-    const int v = atoi(e);
-    if (v == 16 || v == 64 || (mt == 1 && (v == 8 || v == 32))) S = v;
-  }
+  if (p.amax && (epi != QMV_STORE || p.nseg != 1))
+    return set_error(BMX_E_ARG, "qmv: argmax partials need the store epilogue and one segment");
+  const QmvGrid gr = qmv_grid(p, epi);
+  const int mt = gr.mt, S = gr.S;
   const int nh = epi == QMV_SWIGLU ? 2 : 1;
-  const int rows_per_block = (kThreads / 64) * (64 / S);
+  const int rows_per_block = gr.rows_per_block;
   // LDS per phase: x chunks (80 B + 4 B sum per 32 columns per x row) and
   // the workgroup's s|b words (4 B per 64 columns per weight row).
   const double per_col = mt * (kChunkBytes + 4) / 32.0 + nh * rows_per_block * 4 / 64.0;
@@ -431,19 +489,12 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   p.kp = std::min(kp, p.K);
   const int CP = p.kp / 32, GP = p.kp / 64;
   const size_t lds = static_cast<size_t>(mt) * CP * (kChunkBytes + 4) +
-                     static_cast<size_t>(nh) * rows_per_block * GP * 4 + 4 * static_cast<size_t>(mt) * 4;
+                     static_cast<size_t>(nh) * rows_per_block * GP * 4 + 4 * static_cast<size_t>(mt) * 4 +
+                     (p.amax ? static_cast<size_t>(mt) * rows_per_block * 8 : 0);
   // every segment starts on a workgroup boundary (the kernel reads its
   // segment's fields with scalar loads)
-  int blocks = 0;
-  if (epi == QMV_SWIGLU) {
-    blocks = (p.N + rows_per_block - 1) / rows_per_block;
-    for (int i = 0; i < p.nseg; i++) p.seg[i].blk0 = 0;
-  } else {
-    for (int i = 0; i < p.nseg; i++) {
-      p.seg[i].blk0 = blocks;
-      blocks += (p.seg[i].rows + rows_per_block - 1) / rows_per_block;
-    }
-  }
+  const int blocks = gr.blocks;
+  for (int i = 0; i < p.nseg; i++) p.seg[i].blk0 = gr.blk0[i];
   // 16-byte staging of s/b needs whole 8-group units at 16-byte alignment
   p.sb_vec = (p.K % 512) == 0;
   for (int i = 0; i < p.nseg; i++)

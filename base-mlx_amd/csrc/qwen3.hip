@@ -93,7 +93,9 @@ struct bmx_qwen3 {
   int32_t* ids = nullptr;     // [max_tokens] token ids for the embedding gather
   uint32_t* tok_u = nullptr;  // [max(max_tokens, 64)] token staging
   uint32_t* next_tok = nullptr;  // argmax output of the decode step
-  int* pos = nullptr;            // decode position (device)
+  int* step_io = nullptr;        // decode graph: [token, position, next token] (device)
+  uint2* amax = nullptr;         // lm_head argmax partials of the decode graph
+  int amax_cap = 0;
   uint32_t* host_tok = nullptr;    // pinned [64]: token / position / argmax exchange
   uint32_t* host_stage = nullptr;  // pinned [max_tokens]: prompt upload staging
   hipEvent_t stage_done = nullptr; // host_stage may be rewritten once this fired
@@ -134,7 +136,7 @@ int ones(bmx_qwen3* m, uint16_t** p, int n, hipStream_t st) {
 }
 
 int qmv(const bmx_qwen3* m, const uint16_t* x, int M, const QLin& w, uint16_t* y, hipStream_t st,
-        const uint16_t* norm = nullptr) {
+        const uint16_t* norm = nullptr, uint2* amax = nullptr, int* amax_nblk = nullptr) {
   QmvParams p{};
   p.x = x;
   p.ldx = w.K;
@@ -145,6 +147,12 @@ int qmv(const bmx_qwen3* m, const uint16_t* x, int M, const QLin& w, uint16_t* y
   p.K = w.K;
   p.norm_w = norm;
   p.eps = m->cfg.eps;
+  p.amax = amax;
+  if (amax) {
+    const int nblk = qmv_blocks(p, QMV_STORE);
+    if (nblk > m->amax_cap) return set_error(BMX_E_SHAPE, "argmax partials: %d workgroups", nblk);
+    if (amax_nblk) *amax_nblk = nblk;
+  }
   return launch_qmv(p, QMV_STORE, st);
 }
 
@@ -153,15 +161,19 @@ const QLin& head_of(const bmx_qwen3* m) { return m->cfg.tied ? m->embed : m->lm_
 // One forward over M tokens whose ids are already in m->ids, at position
 // cache->seq_len (or *pos_dev when graph-captured).  logits: [rows, vocab]
 // (rows = M if all_logits else 1).
+// ids: token ids on device (m->ids when null).  amax (one logits row only):
+// the head GEMV also writes its argmax partials there, *amax_nblk of them.
 int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* pos_dev, bool all_logits,
-                   uint16_t* logits, hipStream_t st) {
+                   uint16_t* logits, hipStream_t st, const int32_t* ids = nullptr, uint2* amax = nullptr,
+                   int* amax_nblk = nullptr) {
   const bmx_qwen3_config& cf = m->cfg;
   const int H = cf.hidden, I = cf.inter, nq = cf.n_heads, nkv = cf.n_kv_heads, hd = cf.head_dim;
   const int qd = nq * hd, kvd = nkv * hd;
   const float scale = 1.0f / sqrtf(static_cast<float>(hd));  // qwen3.rs:324
   const int L_max = pos_dev ? c->cap : offset + M;
   // x = embed.lookup(tokens)  (qwen3.rs:328-333)
-  if (int rc = launch_dequant_gather(m->ids, M, cf.vocab, m->embed.w, m->embed.s, m->embed.b, m->x, H, st)) return rc;
+  if (int rc = launch_dequant_gather(ids ? ids : m->ids, M, cf.vocab, m->embed.w, m->embed.s, m->embed.b, m->x, H, st))
+    return rc;
   for (int l = 0; l < cf.layers; l++) {
     const Layer& L = m->layers[l];
     // ---- qkv_block: rms_norm + q/k/v projections (kernels.rs:28-46) ----
@@ -246,19 +258,21 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
   const QLin& head = head_of(m);
   const int rows = all_logits ? M : 1;
   const uint16_t* xin = all_logits ? m->x : m->x + static_cast<size_t>(M - 1) * H;
-  if (rows <= 8) return qmv(m, xin, rows, head, logits, st, m->final_norm);
+  if (rows <= 8) return qmv(m, xin, rows, head, logits, st, m->final_norm, rows == 1 ? amax : nullptr, amax_nblk);
   if (int rc = launch_rms_norm(xin, m->final_norm, m->h, rows, H, cf.eps, st)) return rc;
   return launch_qmm(m->h, head.w, head.s, head.b, logits, rows, cf.vocab, H, st);
 }
 
-// Decode step with token and position in device memory: ids <- tok_u[0],
-// forward, argmax -> next_tok, pos += 1.  Captured into a graph.
+// Decode step with token and position in device memory (step_io[0], [1]):
+// forward, with the lm_head GEMV writing per-workgroup argmax partials, then
+// the reduction of the partials -> step_io[2].  Captured into a graph.  The
+// token is read as the embedding id directly: tokens are below the
+// vocabulary size (checked on the host, or produced by the argmax).
 int decode_step_device(bmx_qwen3* m, bmx_kv_cache* c, hipStream_t st) {
-  if (int rc = launch_tokens_to_ids(m->tok_u, m->ids, 1, st)) return rc;
-  if (int rc = forward_device(m, c, 1, 0, m->pos, false, m->logits1, st)) return rc;
-  if (int rc = launch_argmax(m->logits1, 1, m->cfg.vocab, m->next_tok, st)) return rc;
-  if (int rc = check_hip(hipMemcpyAsync(m->tok_u, m->next_tok, 4, hipMemcpyDeviceToDevice, st), "copy token")) return rc;
-  return launch_add_scalar(m->pos, 1, st);
+  int nblk = 0;
+  if (int rc = forward_device(m, c, 1, 0, m->step_io + 1, false, m->logits1, st, m->step_io, m->amax, &nblk))
+    return rc;
+  return launch_argmax_partials(m->amax, 1, nblk, reinterpret_cast<uint32_t*>(m->step_io + 2), st);
 }
 
 void drop_graph(bmx_qwen3* m) {
@@ -376,7 +390,9 @@ extern "C" int bmx_qwen3_create_random(const bmx_qwen3_config* cfg, uint64_t see
   if (!rc) rc = dalloc_t(m, &m->ids, T);
   if (!rc) rc = dalloc_t(m, &m->tok_u, T < 64 ? 64 : T);
   if (!rc) rc = dalloc_t(m, &m->next_tok, 64);
-  if (!rc) rc = dalloc_t(m, &m->pos, 16);
+  if (!rc) rc = dalloc_t(m, &m->step_io, 4);
+  m->amax_cap = cfg->vocab / 4 + 64;  // workgroups of the lm_head GEMV (>= 4 rows each)
+  if (!rc) rc = dalloc_t(m, &m->amax, static_cast<size_t>(m->amax_cap));
   if (!rc) rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&m->host_tok), 64 * sizeof(uint32_t), hipHostMallocDefault), "hipHostMalloc");
   if (!rc) rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&m->host_stage), T * sizeof(uint32_t), hipHostMallocDefault), "hipHostMalloc");
   if (!rc) rc = check_hip(hipEventCreateWithFlags(&m->stage_done, hipEventDisableTiming), "event create");
@@ -500,10 +516,10 @@ static int graph_step(bmx_qwen3* m, bmx_kv_cache* c, hipStream_t st, uint32_t to
   if (int rc = ensure_graph(m, c, st)) return rc;
   m->host_tok[0] = tok;
   m->host_tok[1] = static_cast<uint32_t>(c->seq_len);
-  if (int rc = check_hip(hipMemcpyAsync(m->tok_u, &m->host_tok[0], 4, hipMemcpyHostToDevice, st), "set token")) return rc;
-  if (int rc = check_hip(hipMemcpyAsync(m->pos, &m->host_tok[1], 4, hipMemcpyHostToDevice, st), "set pos")) return rc;
+  if (int rc = check_hip(hipMemcpyAsync(m->step_io, &m->host_tok[0], 8, hipMemcpyHostToDevice, st), "set token"))
+    return rc;
   if (int rc = check_hip(hipGraphLaunch(m->graph, st), "graph launch")) return rc;
-  if (int rc = check_hip(hipMemcpyAsync(&m->host_tok[2], m->next_tok, 4, hipMemcpyDeviceToHost, st), "read token"))
+  if (int rc = check_hip(hipMemcpyAsync(&m->host_tok[2], m->step_io + 2, 4, hipMemcpyDeviceToHost, st), "read token"))
     return rc;
   if (int rc = check_hip(hipStreamSynchronize(st), "decode sync")) return rc;
   c->seq_len += 1;

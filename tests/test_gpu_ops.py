@@ -92,14 +92,17 @@ def test_attention(gpu, orc, Hq, Hkv, M, offset):
         assert _close(yb, ref, ulps=2, floor=2e-3) > 0.999
 
 
-def test_argmax(gpu, orc):
-    x = gpu.fill_normal_bf16(14, (6, 151936))
+@pytest.mark.parametrize("n", [151936, 1001])
+def test_argmax(gpu, orc, n):
+    """16-byte vector path (rows of a multiple of 8) and the scalar path."""
+    x = gpu.fill_normal_bf16(14, (6, n))
     xb = torch_bf16_bits(x).copy()
-    xb[1, 7] = xb[1, 151000] = orc.f32_to_bf16(np.array([30.0], np.float32))[0]
+    xb[1, 7] = xb[1, n - 936] = orc.f32_to_bf16(np.array([30.0], np.float32))[0]
     xb[2, :] = 0x3F80
+    xb[3, :] = 0xFF80  # -inf row: index 0
     got = gpu.argmax_rows(to_torch_bf16(xb)).cpu().numpy()
     np.testing.assert_array_equal(got.view(np.uint32), orc.argmax_rows(xb))
-    assert got[1] == 7 and got[2] == 0
+    assert got[1] == 7 and got[2] == 0 and got[3] == 0
 
 
 def test_silu_mul_and_add(gpu, orc):
