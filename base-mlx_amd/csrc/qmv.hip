@@ -380,6 +380,273 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
   }
 }
 
+// Sum over groups of S consecutive lanes (S = 8, 16, 32 or 64); every lane
+// of a group gets the group's sum.  Inside 16-lane rows with DPP: quad_perm
+// [1,0,3,2] (0xB1), quad_perm [2,3,0,1] (0x4E), row_half_mirror (0x141:
+// lane i <-> 7 - i within 8), row_mirror (0x140: lane i <-> 15 - i).
+__device__ __forceinline__ float lanes_sum(float v, int S) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);
+  if (S >= 16) v += dpp_f32<0x140>(v);
+  if (S >= 32) v += __shfl_xor(v, 16, 64);
+  if (S >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// M = 1 with the whole K in one LDS phase (the decode shapes).  Every load
+// of the workgroup is issued up front and unconditionally (indices are
+// clamped; duplicate addresses coalesce inside an instruction): first x, the
+// norm weight and s|b, then all NI 16-byte W chunks of each lane.  With the
+// count of loads in flight fixed, the compiler waits for each W chunk on its
+// own, so the dot products of chunk u overlap the arrival of the later ones.
+// S (lanes per row) is a launch parameter; NI = ceil(K/32 / S) rounded up to
+// an instantiated value.
+constexpr int kXU1 = 5;  // x units (8 values) per thread: K <= 256 * 8 * 5
+
+template <int NI, int EPI>
+__global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const int S) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NH = (EPI == QMV_SWIGLU) ? 2 : 1;
+  const int lshift = __builtin_ctz(S);
+  const int SLOTS = 64 >> lshift;
+  const int RB = 4 * SLOTS;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int slot = lane >> lshift;
+  const int sl = lane & (S - 1);
+  const int K = p.K;
+  const int G = K / 64, C = K / 32, W8 = K / 8, GU = G / 8;
+  unsigned char* xs = smem;                                        // [C] x 80 B
+  float* sxs = reinterpret_cast<float*>(smem + C * kChunkBytes);   // [C]
+  uint32_t* sbs = reinterpret_cast<uint32_t*>(sxs + C);            // [NH][RB][G]
+  float* red = reinterpret_cast<float*>(sbs + NH * RB * G);        // [4]
+  float* amv = red + 4;                                            // [RB]
+  uint32_t* ami = reinterpret_cast<uint32_t*>(amv + RB);           // [RB]
+
+  int seg = 0;
+  if constexpr (EPI != QMV_SWIGLU) {
+    if (p.nseg > 1 && static_cast<int>(blockIdx.x) >= p.seg[1].blk0) seg = 1;
+    if (p.nseg > 2 && static_cast<int>(blockIdx.x) >= p.seg[2].blk0) seg = 2;
+  }
+  const int rows = p.seg[seg].rows;
+  const int row0 = (static_cast<int>(blockIdx.x) - p.seg[seg].blk0) * RB;
+  const int rl = wave * SLOTS + slot;
+  const int row = row0 + rl;
+  const bool valid = row < rows;
+  const bool has_norm = p.norm_w != nullptr;
+  const uint16_t* nw = has_norm ? p.norm_w : p.x;  // a readable address either way
+
+  // ---- 1. staging loads (unconditional, clamped) ----
+  uint4 xr[kXU1], nr[kXU1];
+#pragma unroll
+  for (int i = 0; i < kXU1; i++) {
+    const int idx = min(i * kThreads + static_cast<int>(threadIdx.x), W8 - 1);
+    xr[i] = *reinterpret_cast<const uint4*>(p.x + idx * 8);
+    nr[i] = *reinterpret_cast<const uint4*>(nw + idx * 8);
+  }
+  uint4 sr[NH], br[NH];
+  const int sb_units = RB * GU;
+  const float rcp_gu = 1.0f / static_cast<float>(GU);
+  const int e_sb = min(static_cast<int>(threadIdx.x), sb_units - 1);
+  const int r_sb = udiv_small(e_sb, rcp_gu);
+#pragma unroll
+  for (int h = 0; h < NH; h++) {
+    const QmvSegment& sgm = p.seg[EPI == QMV_SWIGLU ? h : seg];
+    const int64_t off = static_cast<int64_t>(min(row0 + r_sb, rows - 1)) * G + (e_sb - r_sb * GU) * 8;
+    sr[h] = *reinterpret_cast<const uint4*>(sgm.s + off);
+    br[h] = *reinterpret_cast<const uint4*>(sgm.b + off);
+  }
+  // keep the staging loads ahead of the W stream in issue order
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- 2. every W chunk of this lane ----
+  // in the order they are consumed: chunk by chunk, both matrices of a chunk
+  // together
+  uint4 wv[NI][NH];
+  {
+    const int64_t rr = min(row, rows - 1);
+    const uint32_t* wrow[NH];
+#pragma unroll
+    for (int h = 0; h < NH; h++) wrow[h] = p.seg[EPI == QMV_SWIGLU ? h : seg].w + rr * (K / 8);
+#pragma unroll
+    for (int u = 0; u < NI; u++) {
+      const int c = min(sl + (u << lshift), C - 1);
+#pragma unroll
+      for (int h = 0; h < NH; h++) {
+        const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[h] + c * 4));
+        wv[u][h] = make_uint4(t.x, t.y, t.z, t.w);
+      }
+    }
+  }
+  // ---- 3. fused RMSNorm (fast::rms_norm, qwen3.rs:50-55) from the staged x:
+  //      h = w * bf16(x * rsqrt(mean(x^2) + eps)) ----
+  float inv = 1.0f;
+  if (has_norm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kXU1; i++) {
+      if (i * kThreads + static_cast<int>(threadIdx.x) < W8) {
+        const uint32_t v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float lo = bf2f(v[q] & 0xffffu), hi = bf2f(v[q] >> 16);
+          ss += lo * lo + hi * hi;
+        }
+      }
+    }
+    ss = lanes_sum(ss, 64);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / static_cast<float>(K) + p.eps);
+  }
+  // ---- 4. x (pair-permuted, chunk sums) and s|b into LDS ----
+#pragma unroll
+  for (int i = 0; i < kXU1; i++) {
+    const int idx = i * kThreads + static_cast<int>(threadIdx.x);
+    const bool act = idx < W8;
+    uint4 d = xr[i];
+    if (has_norm) {
+      uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+      const uint32_t wq[4] = {nr[i].x, nr[i].y, nr[i].z, nr[i].w};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float lo = bf2f(wq[q] & 0xffffu) * round_bf(bf2f(dv[q] & 0xffffu) * inv);
+        const float hi = bf2f(wq[q] >> 16) * round_bf(bf2f(dv[q] >> 16) * inv);
+        dv[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+      }
+      d = make_uint4(dv[0], dv[1], dv[2], dv[3]);
+    }
+    const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+    float part = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) part += bf2f(dv[q] & 0xffffu) + bf2f(dv[q] >> 16);
+    // a chunk of 32 values = 4 consecutive words = 4 consecutive lanes
+    part += dpp_f32<0xB1>(part);
+    part += dpp_f32<0x4E>(part);
+    if (act) {
+      *reinterpret_cast<uint4*>(xs + (idx >> 2) * kChunkBytes + (idx & 3) * 16) = permute_pairs(d);
+      if ((idx & 3) == 0) sxs[idx >> 2] = part;
+    }
+  }
+  if (static_cast<int>(threadIdx.x) < sb_units && row0 + r_sb < rows) {
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      const uint32_t s4[4] = {sr[h].x, sr[h].y, sr[h].z, sr[h].w};
+      const uint32_t b4[4] = {br[h].x, br[h].y, br[h].z, br[h].w};
+      uint32_t* dst = sbs + (h * RB + r_sb) * G + (e_sb - r_sb * GU) * 8;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        dst[2 * q] = (s4[q] & 0xffffu) | (b4[q] << 16);
+        dst[2 * q + 1] = (s4[q] >> 16) | (b4[q] & 0xffff0000u);
+      }
+    }
+  }
+  __syncthreads();
+  // ---- 5. dot products, chunk by chunk as the W stream arrives ----
+  float acc[NH];
+#pragma unroll
+  for (int h = 0; h < NH; h++) acc[h] = 0.0f;
+#pragma unroll
+  for (int u = 0; u < NI; u++) {
+    const int c = sl + (u << lshift);
+    if (c < C) {
+      const uint4* xp = reinterpret_cast<const uint4*>(xs + c * kChunkBytes);
+      const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+      const float sx = sxs[c];
+#pragma unroll
+      for (int h = 0; h < NH; h++) {
+        const uint32_t sb = sbs[(h * RB + rl) * G + (c >> 1)];
+        const float sv = bf2f(sb & 0xffffu);
+        const float bb = bf2f(sb >> 16) - 128.0f * sv;
+        float d0 = 0.0f, d1 = 0.0f;  // two independent dot2 chains
+        d0 = word_dot(wv[u][h].x, x0, d0);
+        d1 = word_dot(wv[u][h].y, x1, d1);
+        d0 = word_dot(wv[u][h].z, x2, d0);
+        d1 = word_dot(wv[u][h].w, x3, d1);
+        acc[h] += sv * (d0 + d1);
+        acc[h] += bb * sx;
+      }
+    }
+    // consume the chunks in issue order (each waits only for its own loads)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // ---- 6. reduce the S lanes of each row, epilogue ----
+#pragma unroll
+  for (int h = 0; h < NH; h++) acc[h] = lanes_sum(acc[h], S);
+  if (sl == 0 && valid) {
+    if constexpr (EPI == QMV_STORE) {
+      p.seg[seg].y[row] = f2bf(acc[0]);
+    } else if constexpr (EPI == QMV_RESIDUAL) {
+      // x = x + o_proj(attn) in bf16 (qwen3.rs:520-521, 541)
+      const float r = bf2f(p.res[row]);
+      p.seg[0].y[row] = f2bf(r + round_bf(acc[0]));
+    } else {
+      // silu(gate) * up, each MLX op rounding to bf16 (kernels.rs:73-74)
+      const float g = round_bf(acc[0]);
+      const float u = round_bf(acc[NH - 1]);
+      const float sg = round_bf(1.0f / (1.0f + expf(-g)));
+      const float a = round_bf(g * sg);
+      p.seg[0].y[row] = f2bf(a * u);
+    }
+  }
+  if constexpr (EPI == QMV_STORE) {
+    if (p.amax != nullptr) {
+      // argmax partial of the workgroup's rows (first index on ties)
+      if (sl == 0) {
+        amv[rl] = valid ? bf2f(f2bf(acc[0])) : -INFINITY;
+        ami[rl] = valid ? static_cast<uint32_t>(row) : 0xffffffffu;
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        float bv = -INFINITY;
+        uint32_t bi = 0xffffffffu;
+        for (int r = 0; r < RB; r++)
+          if (amv[r] > bv || (amv[r] == bv && ami[r] < bi)) {
+            bv = amv[r];
+            bi = ami[r];
+          }
+        p.amax[blockIdx.x] = make_uint2(__float_as_uint(bv), bi);
+      }
+    }
+  }
+}
+
+template <int NI>
+int launch_qmv1_ni(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
+  switch (epi) {
+    case QMV_STORE:
+      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_STORE>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      break;
+    case QMV_RESIDUAL:
+      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_RESIDUAL>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      break;
+    default:
+      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_SWIGLU>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+  }
+  return check_launch("qmv1");
+}
+
+// Launches qmv1 when it applies (M = 1, one phase, 16-byte s|b staging, x
+// within kXU1 units per thread, s|b within one unit per thread); returns -1
+// otherwise.
+int try_launch_qmv1(QmvEpilogue epi, int S, const QmvParams& p, int blocks, hipStream_t st) {
+  if (p.m != 1 || p.kp < p.K || !p.sb_vec || p.K / 8 > kThreads * kXU1) return -1;
+  const int C = p.K / 32, G = p.K / 64;
+  const int RB = 4 * (64 / S);
+  if (RB * (G / 8) > kThreads) return -1;
+  const int ni = (C + S - 1) / S;
+  const int nh = epi == QMV_SWIGLU ? 2 : 1;
+  const size_t lds = static_cast<size_t>(C) * (kChunkBytes + 4) + static_cast<size_t>(nh) * RB * G * 4 + 16 +
+                     static_cast<size_t>(RB) * 8;
+  if (ni <= 2) return launch_qmv1_ni<2>(epi, S, p, blocks, lds, st);
+  if (ni <= 3) return launch_qmv1_ni<3>(epi, S, p, blocks, lds, st);
+  if (ni <= 5) return launch_qmv1_ni<5>(epi, S, p, blocks, lds, st);
+  if (ni <= 8) return launch_qmv1_ni<8>(epi, S, p, blocks, lds, st);
+  if (nh == 1 && ni <= 10) return launch_qmv1_ni<10>(epi, S, p, blocks, lds, st);
+  if (nh == 1 && ni <= 16) return launch_qmv1_ni<16>(epi, S, p, blocks, lds, st);
+  return -1;
+}
+
 template <int MT, int EPI>
 int launch_s(int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
   if constexpr (MT == 1) {
@@ -499,6 +766,10 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   p.sb_vec = (p.K % 512) == 0;
   for (int i = 0; i < p.nseg; i++)
     p.sb_vec = p.sb_vec && aligned(p.seg[i].s, 16) && aligned(p.seg[i].b, 16);
+  if (mt == 1) {
+    const int rc = try_launch_qmv1(epi, S, p, blocks, stream);
+    if (rc >= 0) return rc;
+  }
   switch (mt) {
     case 1: return launch_epi<1>(epi, S, p, blocks, lds, stream);
     case 2: return launch_epi<2>(epi, S, p, blocks, lds, stream);
