@@ -485,6 +485,7 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < kXU1; i++) {
+      if (i * kThreads >= W8) break;  // uniform: the remaining units are clamped copies
       if (i * kThreads + static_cast<int>(threadIdx.x) < W8) {
         const uint32_t v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
 #pragma unroll
@@ -502,24 +503,27 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   // ---- 4. x (pair-permuted, chunk sums) and s|b into LDS ----
 #pragma unroll
   for (int i = 0; i < kXU1; i++) {
+    if (i * kThreads >= W8) break;  // uniform: the remaining units are clamped copies
     const int idx = i * kThreads + static_cast<int>(threadIdx.x);
     const bool act = idx < W8;
     uint4 d = xr[i];
-    if (has_norm) {
-      uint32_t dv[4] = {d.x, d.y, d.z, d.w};
-      const uint32_t wq[4] = {nr[i].x, nr[i].y, nr[i].z, nr[i].w};
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float lo = bf2f(wq[q] & 0xffffu) * round_bf(bf2f(dv[q] & 0xffffu) * inv);
-        const float hi = bf2f(wq[q] >> 16) * round_bf(bf2f(dv[q] >> 16) * inv);
-        dv[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
-      }
-      d = make_uint4(dv[0], dv[1], dv[2], dv[3]);
-    }
-    const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
     float part = 0.0f;
+    if (act) {
+      if (has_norm) {
+        uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+        const uint32_t wq[4] = {nr[i].x, nr[i].y, nr[i].z, nr[i].w};
 #pragma unroll
-    for (int q = 0; q < 4; q++) part += bf2f(dv[q] & 0xffffu) + bf2f(dv[q] >> 16);
+        for (int q = 0; q < 4; q++) {
+          const float lo = bf2f(wq[q] & 0xffffu) * round_bf(bf2f(dv[q] & 0xffffu) * inv);
+          const float hi = bf2f(wq[q] >> 16) * round_bf(bf2f(dv[q] >> 16) * inv);
+          dv[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+        }
+        d = make_uint4(dv[0], dv[1], dv[2], dv[3]);
+      }
+      const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+      for (int q = 0; q < 4; q++) part += bf2f(dv[q] & 0xffffu) + bf2f(dv[q] >> 16);
+    }
     // a chunk of 32 values = 4 consecutive words = 4 consecutive lanes
     part += dpp_f32<0xB1>(part);
     part += dpp_f32<0x4E>(part);
@@ -591,19 +595,29 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   }
   if constexpr (EPI == QMV_STORE) {
     if (p.amax != nullptr) {
-      // argmax partial of the workgroup's rows (first index on ties)
-      if (sl == 0) {
-        amv[rl] = valid ? bf2f(f2bf(acc[0])) : -INFINITY;
-        ami[rl] = valid ? static_cast<uint32_t>(row) : 0xffffffffu;
+      // argmax partial of the workgroup's rows (first index on ties): across
+      // the row slots of each wave with shuffles, then the 4 waves in LDS
+      float bv = valid ? bf2f(f2bf(acc[0])) : -INFINITY;
+      uint32_t bi = valid ? static_cast<uint32_t>(row) : 0xffffffffu;
+      for (int off = S; off < 64; off <<= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const uint32_t oi = __shfl_xor(bi, off, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (lane == 0) {
+        amv[wave] = bv;
+        ami[wave] = bi;
       }
       __syncthreads();
       if (threadIdx.x == 0) {
-        float bv = -INFINITY;
-        uint32_t bi = 0xffffffffu;
-        for (int r = 0; r < RB; r++)
-          if (amv[r] > bv || (amv[r] == bv && ami[r] < bi)) {
-            bv = amv[r];
-            bi = ami[r];
+#pragma unroll
+        for (int w = 1; w < 4; w++)
+          if (amv[w] > bv || (amv[w] == bv && ami[w] < bi)) {
+            bv = amv[w];
+            bi = ami[w];
           }
         p.amax[blockIdx.x] = make_uint2(__float_as_uint(bv), bi);
       }
