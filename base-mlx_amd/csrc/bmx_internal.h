@@ -51,8 +51,23 @@ struct QmvParams {
   uint2* amax;
 };
 
+// Raises a kernel's dynamic-LDS limit to `bytes` once (launches above 64 KB
+// need it); returns a BMX code.
+template <class F>
+int allow_lds(F* kernel, size_t bytes) {
+  static size_t allowed = 64 * 1024;
+  if (bytes <= allowed) return BMX_OK;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(bytes)) != hipSuccess)
+    return set_error(BMX_E_UNSUPPORTED, "kernel needs %zu bytes of LDS", bytes);
+  allowed = bytes;
+  return BMX_OK;
+}
+
 // Validates shapes/alignment and launches the qmv kernel family.
 int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream);
+// 2..8 rows of x on the matrix cores; -1 when the shape does not fit.
+int try_launch_qmvx(QmvParams p, QmvEpilogue epi, hipStream_t stream);
 // Workgroups launch_qmv uses for these parameters (the count of argmax
 // partials per x row).
 int qmv_blocks(const QmvParams& p, QmvEpilogue epi);

@@ -29,6 +29,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "bmx_device.h"
 
@@ -661,6 +662,413 @@ int try_launch_qmv1(QmvEpilogue epi, int S, const QmvParams& p, int blocks, hipS
   return -1;
 }
 
+// Persistent GEMV for M <= 8 rows of x with the whole K in LDS.  About two
+// workgroups per CU stage x once (with the fused RMSNorm for M = 1) and then
+// stream their share of row tiles (RB rows each; a tile is what one
+// workgroup of qmv1 handles): while a tile's dot products run, the next
+// tile's W and s|b are already in flight in a second register buffer.  All
+// loads are unconditional (clamped), so every wait is for one specific load.
+template <int MT, int NI, int NH>
+struct QmvTileRegs {
+  uint4 w[NI][NH];
+  uint4 s[NH];
+  uint4 b[NH];
+};
+
+template <int MT, int NI, int EPI>
+__global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const int S, const int ntiles) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NH = (EPI == QMV_SWIGLU) ? 2 : 1;
+  constexpr int XU = (MT == 1) ? 5 : 8;  // x units (8 values) per thread per staging batch
+  const int lshift = __builtin_ctz(S);
+  const int SLOTS = 64 >> lshift;
+  const int RB = 4 * SLOTS;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int slot = lane >> lshift;
+  const int sl = lane & (S - 1);
+  const int rl = wave * SLOTS + slot;
+  const int M = p.m;
+  const int K = p.K;
+  const int G = K / 64, C = K / 32, W8 = K / 8, GU = G / 8;
+  unsigned char* xs = smem;                                            // [MT][C] x 80 B
+  float* sxs = reinterpret_cast<float*>(smem + MT * C * kChunkBytes);  // [MT][C]
+  uint32_t* sbs = reinterpret_cast<uint32_t*>(sxs + MT * C);           // [2][NH][RB][G]
+  float* red = reinterpret_cast<float*>(sbs + 2 * NH * RB * G);        // [4][MT]
+  float* amv = red + 4 * MT;                                           // [4]
+  uint32_t* ami = reinterpret_cast<uint32_t*>(amv + 4);                // [4]
+  const bool has_norm = p.norm_w != nullptr;
+  const int sb_units = RB * GU;
+  const float rcp_gu = 1.0f / static_cast<float>(GU);
+  const int e_sb = min(static_cast<int>(threadIdx.x), sb_units - 1);
+  const int r_sb = udiv_small(e_sb, rcp_gu);
+
+  auto seg_of = [&](int t) {
+    int sg = 0;
+    if constexpr (EPI != QMV_SWIGLU) {
+      if (p.nseg > 1 && t >= p.seg[1].blk0) sg = 1;
+      if (p.nseg > 2 && t >= p.seg[2].blk0) sg = 2;
+    }
+    return sg;
+  };
+  // loads of tile t (clamped to the last tile: the prefetch past the end is
+  // never consumed): s|b units of the workgroup's rows, then W
+  auto issue_tile = [&](int t, QmvTileRegs<MT, NI, NH>& R) {
+    t = min(t, ntiles - 1);
+    const int sg = seg_of(t);
+    const int rows = p.seg[sg].rows;
+    const int row0 = (t - p.seg[sg].blk0) * RB;
+    const int64_t rs = min(row0 + r_sb, rows - 1);
+    const int64_t rr = min(row0 + rl, rows - 1);
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      const QmvSegment& sgm = p.seg[EPI == QMV_SWIGLU ? h : sg];
+      const int64_t off = rs * G + (e_sb - r_sb * GU) * 8;
+      R.s[h] = *reinterpret_cast<const uint4*>(sgm.s + off);
+      R.b[h] = *reinterpret_cast<const uint4*>(sgm.b + off);
+    }
+    const uint32_t* wrow[NH];
+#pragma unroll
+    for (int h = 0; h < NH; h++) wrow[h] = p.seg[EPI == QMV_SWIGLU ? h : sg].w + rr * (K / 8);
+#pragma unroll
+    for (int u = 0; u < NI; u++) {
+      const int c = min(sl + (u << lshift), C - 1);
+#pragma unroll
+      for (int h = 0; h < NH; h++) {
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[h] + c * 4));
+        R.w[u][h] = make_uint4(v.x, v.y, v.z, v.w);
+      }
+    }
+  };
+
+  QmvTileRegs<MT, NI, NH> A, B;
+  int t = blockIdx.x;
+
+  // ---- x into LDS once: pair-permuted, chunk sums; RMSNorm fused for M = 1 ----
+  // 1 / rms of x row m from the per-wave sums of squares in red [4][MT]
+  auto inv_of = [&](int m) {
+    const float t = red[m] + red[MT + m] + red[2 * MT + m] + red[3 * MT + m];
+    return 1.0f / sqrtf(t / static_cast<float>(K) + p.eps);
+  };
+  auto stage_unit = [&](int idx, uint4 d, const uint4& wn, float inv) {
+    const bool act = idx < MT * W8;
+    float part = 0.0f;
+    int m = 0, j = 0;
+    if (act) {
+      m = (MT == 1) ? 0 : idx / W8;
+      j = idx - m * W8;
+      if (MT > 1 && has_norm) inv = inv_of(m);
+      if (has_norm) {
+        uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+        const uint32_t wq[4] = {wn.x, wn.y, wn.z, wn.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float lo = bf2f(wq[q] & 0xffffu) * round_bf(bf2f(dv[q] & 0xffffu) * inv);
+          const float hi = bf2f(wq[q] >> 16) * round_bf(bf2f(dv[q] >> 16) * inv);
+          dv[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+        }
+        d = make_uint4(dv[0], dv[1], dv[2], dv[3]);
+      }
+      const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+      for (int q = 0; q < 4; q++) part += bf2f(dv[q] & 0xffffu) + bf2f(dv[q] >> 16);
+    }
+    // a chunk of 32 values = 4 consecutive words = 4 consecutive lanes
+    part += dpp_f32<0xB1>(part);
+    part += dpp_f32<0x4E>(part);
+    if (act) {
+      *reinterpret_cast<uint4*>(xs + (m * C + (j >> 2)) * kChunkBytes + (j & 3) * 16) = permute_pairs(d);
+      if ((j & 3) == 0) sxs[m * C + (j >> 2)] = part;
+    }
+  };
+  if constexpr (MT == 1) {
+    const uint16_t* nw = has_norm ? p.norm_w : p.x;  // a readable address either way
+    uint4 xr[XU], nr[XU];
+#pragma unroll
+    for (int i = 0; i < XU; i++) {
+      const int idx = min(i * kThreads + static_cast<int>(threadIdx.x), W8 - 1);
+      xr[i] = *reinterpret_cast<const uint4*>(p.x + idx * 8);
+      nr[i] = *reinterpret_cast<const uint4*>(nw + idx * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    issue_tile(t, A);  // the first tile's loads stream in behind x
+    __builtin_amdgcn_sched_barrier(0);
+    float inv = 1.0f;
+    if (has_norm) {
+      // fast::rms_norm (qwen3.rs:50-55): h = w * bf16(x * rsqrt(mean(x^2) + eps))
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < XU; i++) {
+        if (i * kThreads >= W8) break;
+        if (i * kThreads + static_cast<int>(threadIdx.x) < W8) {
+          const uint32_t v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const float lo = bf2f(v[q] & 0xffffu), hi = bf2f(v[q] >> 16);
+            ss += lo * lo + hi * hi;
+          }
+        }
+      }
+      ss = lanes_sum(ss, 64);
+      if (lane == 0) red[wave] = ss;
+      __syncthreads();
+      inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / static_cast<float>(K) + p.eps);
+    }
+#pragma unroll
+    for (int i = 0; i < XU; i++) {
+      if (i * kThreads >= W8) break;
+      stage_unit(i * kThreads + static_cast<int>(threadIdx.x), xr[i], nr[i], inv);
+    }
+  } else {
+    if (has_norm) {
+      // fast::rms_norm (qwen3.rs:50-55) of each x row: a first pass for the
+      // sums of squares, then the staging pass normalises
+      float ss[MT];
+#pragma unroll
+      for (int m = 0; m < MT; m++) ss[m] = 0.0f;
+      for (int b0 = 0; b0 < MT * W8; b0 += kThreads * XU) {
+        uint4 xr[XU];
+#pragma unroll
+        for (int i = 0; i < XU; i++) {
+          const int idx = min(b0 + i * kThreads + static_cast<int>(threadIdx.x), MT * W8 - 1);
+          const int m = idx / W8;
+          xr[i] = *reinterpret_cast<const uint4*>(p.x + min(m, M - 1) * p.ldx + (idx - m * W8) * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < XU; i++) {
+          const int idx = b0 + i * kThreads + static_cast<int>(threadIdx.x);
+          if (idx < MT * W8) {
+            const int m = idx / W8;
+            const uint32_t v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+            float q2 = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const float lo = bf2f(v[q] & 0xffffu), hi = bf2f(v[q] >> 16);
+              q2 += lo * lo + hi * hi;
+            }
+#pragma unroll
+            for (int mm = 0; mm < MT; mm++)
+              if (m == mm) ss[mm] += q2;
+          }
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        const float v = lanes_sum(ss[m], 64);
+        if (lane == 0) red[wave * MT + m] = v;
+      }
+      __syncthreads();
+    }
+    for (int b0 = 0; b0 < MT * W8; b0 += kThreads * XU) {
+      uint4 xr[XU], nr[XU];
+#pragma unroll
+      for (int i = 0; i < XU; i++) {
+        const int idx = min(b0 + i * kThreads + static_cast<int>(threadIdx.x), MT * W8 - 1);
+        const int m = idx / W8;
+        const int j = idx - m * W8;
+        xr[i] = *reinterpret_cast<const uint4*>(p.x + min(m, M - 1) * p.ldx + j * 8);
+        nr[i] = *reinterpret_cast<const uint4*>((has_norm ? p.norm_w : p.x) + j * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < XU; i++) stage_unit(b0 + i * kThreads + static_cast<int>(threadIdx.x), xr[i], nr[i], 1.0f);
+    }
+    issue_tile(t, A);
+  }
+  __syncthreads();
+
+  // ---- one tile: s|b to LDS, prefetch the next tile, dot products, epilogue ----
+  // pf: whether a next tile exists (its loads are issued before the dot
+  // products of this one); the last tile of the workgroup issues none
+  auto step = [&](auto pf, int tt, QmvTileRegs<MT, NI, NH>& cur, QmvTileRegs<MT, NI, NH>& nxt, int par) {
+    const int sg = seg_of(tt);
+    const int rows = p.seg[sg].rows;
+    const int row0 = (tt - p.seg[sg].blk0) * RB;
+    uint32_t* sb = sbs + par * NH * RB * G;
+    if (static_cast<int>(threadIdx.x) < sb_units && row0 + r_sb < rows) {
+#pragma unroll
+      for (int h = 0; h < NH; h++) {
+        const uint32_t s4[4] = {cur.s[h].x, cur.s[h].y, cur.s[h].z, cur.s[h].w};
+        const uint32_t b4[4] = {cur.b[h].x, cur.b[h].y, cur.b[h].z, cur.b[h].w};
+        uint32_t* dst = sb + (h * RB + r_sb) * G + (e_sb - r_sb * GU) * 8;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          dst[2 * q] = (s4[q] & 0xffffu) | (b4[q] << 16);
+          dst[2 * q + 1] = (s4[q] >> 16) | (b4[q] & 0xffff0000u);
+        }
+      }
+    }
+    __syncthreads();
+    if constexpr (decltype(pf)::value) issue_tile(tt + static_cast<int>(gridDim.x), nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    float acc[NH][MT];
+#pragma unroll
+    for (int h = 0; h < NH; h++)
+#pragma unroll
+      for (int m = 0; m < MT; m++) acc[h][m] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NI; u++) {
+      const int c = sl + (u << lshift);
+      if (c < C) {
+        float sv[NH], bb[NH];
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+          const uint32_t w = sb[(h * RB + rl) * G + (c >> 1)];
+          sv[h] = bf2f(w & 0xffffu);
+          bb[h] = bf2f(w >> 16) - 128.0f * sv[h];
+        }
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+          if (m >= M) break;
+          const uint4* xp = reinterpret_cast<const uint4*>(xs + (m * C + c) * kChunkBytes);
+          const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+          const float sx = sxs[m * C + c];
+#pragma unroll
+          for (int h = 0; h < NH; h++) {
+            float d0 = 0.0f, d1 = 0.0f;
+            d0 = word_dot(cur.w[u][h].x, x0, d0);
+            d1 = word_dot(cur.w[u][h].y, x1, d1);
+            d0 = word_dot(cur.w[u][h].z, x2, d0);
+            d1 = word_dot(cur.w[u][h].w, x3, d1);
+            acc[h][m] += sv[h] * (d0 + d1);
+            acc[h][m] += bb[h] * sx;
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const int row = row0 + rl;
+    const bool valid = row < rows;
+#pragma unroll
+    for (int h = 0; h < NH; h++)
+#pragma unroll
+      for (int m = 0; m < MT; m++) acc[h][m] = lanes_sum(acc[h][m], S);
+    if (sl == 0 && valid) {
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        if (m >= M) break;
+        if constexpr (EPI == QMV_STORE) {
+          p.seg[sg].y[static_cast<int64_t>(m) * rows + row] = f2bf(acc[0][m]);
+        } else if constexpr (EPI == QMV_RESIDUAL) {
+          // x = x + o_proj(attn) in bf16 (qwen3.rs:520-521, 541)
+          const int64_t o = static_cast<int64_t>(m) * p.N + row;
+          p.seg[0].y[o] = f2bf(bf2f(p.res[o]) + round_bf(acc[0][m]));
+        } else {
+          // silu(gate) * up, each MLX op rounding to bf16 (kernels.rs:73-74)
+          const float g = round_bf(acc[0][m]);
+          const float u = round_bf(acc[NH - 1][m]);
+          const float sgm = round_bf(1.0f / (1.0f + expf(-g)));
+          p.seg[0].y[static_cast<int64_t>(m) * p.N + row] = f2bf(round_bf(g * sgm) * u);
+        }
+      }
+    }
+    if constexpr (EPI == QMV_STORE && MT == 1) {
+      if (p.amax != nullptr) {
+        // argmax partial of the tile (first index on ties): across row slots
+        // with shuffles, then the 4 waves in LDS
+        float bv = valid ? bf2f(f2bf(acc[0][0])) : -INFINITY;
+        uint32_t bi = valid ? static_cast<uint32_t>(row) : 0xffffffffu;
+        for (int off = S; off < 64; off <<= 1) {
+          const float ov = __shfl_xor(bv, off, 64);
+          const uint32_t oi = __shfl_xor(bi, off, 64);
+          if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+          }
+        }
+        if (lane == 0) {
+          amv[wave] = bv;
+          ami[wave] = bi;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+#pragma unroll
+          for (int w = 1; w < 4; w++)
+            if (amv[w] > bv || (amv[w] == bv && ami[w] < bi)) {
+              bv = amv[w];
+              bi = ami[w];
+            }
+          p.amax[tt] = make_uint2(__float_as_uint(bv), bi);
+        }
+      }
+    }
+  };
+  using more = std::integral_constant<bool, true>;
+  using last = std::integral_constant<bool, false>;
+  const int g = static_cast<int>(gridDim.x);
+  for (;;) {
+    if (t + g >= ntiles) {
+      step(last{}, t, A, B, 0);
+      break;
+    }
+    step(more{}, t, A, B, 0);
+    t += g;
+    if (t + g >= ntiles) {
+      step(last{}, t, B, A, 1);
+      break;
+    }
+    step(more{}, t, B, A, 1);
+    t += g;
+  }
+}
+
+template <int MT, int NI>
+int launch_qmvp_epi(QmvEpilogue epi, int S, const QmvParams& p, int ntiles, int grid, size_t lds, hipStream_t st) {
+  switch (epi) {
+    case QMV_STORE:
+      if (int rc = allow_lds(qmvp_kernel<MT, NI, QMV_STORE>, lds)) return rc;
+      hipLaunchKernelGGL((qmvp_kernel<MT, NI, QMV_STORE>), dim3(grid), dim3(kThreads), lds, st, p, S, ntiles);
+      break;
+    case QMV_RESIDUAL:
+      if (int rc = allow_lds(qmvp_kernel<MT, NI, QMV_RESIDUAL>, lds)) return rc;
+      hipLaunchKernelGGL((qmvp_kernel<MT, NI, QMV_RESIDUAL>), dim3(grid), dim3(kThreads), lds, st, p, S, ntiles);
+      break;
+    default:
+      if (int rc = allow_lds(qmvp_kernel<MT, NI, QMV_SWIGLU>, lds)) return rc;
+      hipLaunchKernelGGL((qmvp_kernel<MT, NI, QMV_SWIGLU>), dim3(grid), dim3(kThreads), lds, st, p, S, ntiles);
+  }
+  return check_launch("qmvp");
+}
+
+template <int MT>
+int launch_qmvp_ni(int ni, int nh, QmvEpilogue epi, int S, const QmvParams& p, int ntiles, int grid, size_t lds,
+                   hipStream_t st) {
+  if (ni <= 2) return launch_qmvp_epi<MT, 2>(epi, S, p, ntiles, grid, lds, st);
+  if (ni <= 3) return launch_qmvp_epi<MT, 3>(epi, S, p, ntiles, grid, lds, st);
+  if (ni <= 5) return launch_qmvp_epi<MT, 5>(epi, S, p, ntiles, grid, lds, st);
+  if (nh == 1 && ni <= 10) return launch_qmvp_epi<MT, 10>(epi, S, p, ntiles, grid, lds, st);
+  return -1;
+}
+
+// Launches the persistent GEMV when it applies (whole K in LDS, 16-byte s|b
+// staging, the workgroup's s|b in one unit per thread, norm only with one x
+// row); returns -1 otherwise.
+// one-row GEMVs with at least this many weight rows (the vocabulary
+// projection) go to the persistent kernel
+constexpr int kPersistentRows = 65536;
+
+int try_launch_qmvp(QmvEpilogue epi, int mt, int S, const QmvParams& p, int ntiles, hipStream_t st) {
+  if (!p.sb_vec) return -1;
+  if (mt == 1 && p.K / 8 > kThreads * 5) return -1;
+  const int C = p.K / 32, G = p.K / 64;
+  const int RB = 4 * (64 / S);
+  if (RB * (G / 8) > kThreads) return -1;
+  const int ni = (C + S - 1) / S;
+  const int nh = epi == QMV_SWIGLU ? 2 : 1;
+  const size_t lds = static_cast<size_t>(mt) * C * (kChunkBytes + 4) + 2ull * nh * RB * G * 4 +
+                     4ull * mt * 4 + 32;
+  if (lds > 150 * 1024) return -1;
+  static const int env_grid = getenv("BMX_QMV_GRID") ? std::max(1, atoi(getenv("BMX_QMV_GRID"))) : 0;
+  int grid = env_grid ? env_grid : (mt == 1 ? 512 : 256);
+  grid = std::min(grid, ntiles);
+  switch (mt) {
+    case 1: return launch_qmvp_ni<1>(ni, nh, epi, S, p, ntiles, grid, lds, st);
+    case 2: return launch_qmvp_ni<2>(ni, nh, epi, S, p, ntiles, grid, lds, st);
+    case 4: return launch_qmvp_ni<4>(ni, nh, epi, S, p, ntiles, grid, lds, st);
+    case 5: return launch_qmvp_ni<5>(ni, nh, epi, S, p, ntiles, grid, lds, st);
+    default: return launch_qmvp_ni<8>(ni, nh, epi, S, p, ntiles, grid, lds, st);
+  }
+}
+
 template <int MT, int EPI>
 int launch_s(int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
   if constexpr (MT == 1) {
@@ -724,8 +1132,9 @@ QmvGrid qmv_grid(const QmvParams& p, QmvEpilogue epi) {
   QmvGrid g{};
   g.mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : p.m <= 5 ? 5 : 8;
   g.S = (g.mt == 1) ? pick_lanes_per_row(p.N, p.K) : (p.K / 32 >= 64 ? 64 : 16);
-  if (const char* e = getenv("BMX_QMV_LANES")) {
-    const int v = atoi(e);
+  static const int env_lanes = getenv("BMX_QMV_LANES") ? atoi(getenv("BMX_QMV_LANES")) : 0;
+  {
+    const int v = env_lanes;
     if (v == 16 || v == 64 || (g.mt == 1 && (v == 8 || v == 32))) g.S = v;
   }
   g.rows_per_block = (kThreads / 64) * (64 / g.S);
@@ -780,6 +1189,22 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   p.sb_vec = (p.K % 512) == 0;
   for (int i = 0; i < p.nseg; i++)
     p.sb_vec = p.sb_vec && aligned(p.seg[i].s, 16) && aligned(p.seg[i].b, 16);
+  // kernel choice: matrix cores for 2..8 rows of x; for one row the
+  // persistent kernel on the vocabulary-sized projection, the single-phase
+  // GEMV elsewhere (BMX_QMV_NO_MFMA / BMX_QMV_NO_PERSISTENT switch the first
+  // two off for comparison)
+  static const bool no_mfma = getenv("BMX_QMV_NO_MFMA") != nullptr;
+  static const bool no_persistent = getenv("BMX_QMV_NO_PERSISTENT") != nullptr;
+  if (mt >= 2 && !no_mfma) {
+    const int rc = try_launch_qmvx(p, epi, stream);
+    if (rc >= 0) return rc;
+  }
+  int rows_total = 0;
+  for (int i = 0; i < p.nseg; i++) rows_total += p.seg[i].rows;
+  if (mt == 1 && !no_persistent && rows_total >= kPersistentRows) {
+    const int rc = try_launch_qmvp(epi, mt, S, p, blocks, stream);
+    if (rc >= 0) return rc;
+  }
   if (mt == 1) {
     const int rc = try_launch_qmv1(epi, S, p, blocks, stream);
     if (rc >= 0) return rc;

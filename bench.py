@@ -32,6 +32,9 @@ HBM_PEAK_GBS = 8000.0
 SHAPE_4B = dict(hidden=2560, inter=9728, layers=36, n_heads=32, n_kv_heads=8, head_dim=128, vocab=151936)
 QMV_SHAPES = [(4096, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (2560, 9728), (151936, 2560)]
 ROOF_SHAPE = (9728, 2560)
+QMM_SHAPES = QMV_SHAPES + [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288), (151936, 4096)]
+QMM_M = [5, 128, 512, 2048]
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def measured_traffic():
@@ -87,6 +90,106 @@ def time_qmv(bmx, torch, N, K, reps=200, M=1):
     del g, ws
     torch.cuda.empty_cache()
     return us, nbytes
+
+
+def time_qmm(bmx, torch, M, N, K):
+    """Average duration (us) of one quantized matmul of M rows, graph-captured,
+    rotating over >= 1 GiB of distinct weights (at least 2 copies)."""
+    nbytes = qmv_bytes(N, K, M)
+    copies = max(2, -(-(1 << 30) // int(0.5625 * N * K)))
+    flops = 2.0 * M * N * K
+    reps = max(copies, min(200, int(2e12 / flops) + 2))
+    ws = [bmx.init_qlinear(6000 + i, N, K) for i in range(copies)]
+    x = bmx.fill_normal_bf16(78, (M, K))
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    st = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        bmx.quantized_matmul(x, *ws[0], out=y)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=st):
+            for i in range(reps):
+                bmx.quantized_matmul(x, *ws[i % copies], out=y)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        g.replay()
+        e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / reps
+    del g, ws
+    torch.cuda.empty_cache()
+    return us, nbytes, flops
+
+
+def qmm_sweep(bmx, torch):
+    out = []
+    for M in QMM_M:
+        for (N, K) in QMM_SHAPES:
+            us, nb, fl = time_qmm(bmx, torch, M, N, K)
+            tf = fl / us / 1e6
+            out.append({"M": M, "N": N, "K": K, "us": round(us, 2), "TFLOP/s": round(tf, 1),
+                        "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "GB/s": round(nb / us / 1e3, 1)})
+            log(f"qmm M={M} N={N} K={K}: {us:.1f} us, {tf:.1f} TFLOP/s ({100 * tf / MFMA_BF16_PEAK_TFLOPS:.1f}% of "
+                f"2.5 PF bf16), {nb / us / 1e3:.0f} GB/s")
+    return out
+
+
+def speculative_bench(bmx, torch, new_tokens=512, prompt_len=2048, spec_k=5):
+    """Greedy speculative decoding: a Qwen3-32B-shaped 4-bit target (64 layers,
+    untied head) verifying 4 drafted tokens + 1 per step (M = 5) from a
+    Qwen3-0.6B-shaped draft, after a seeded prompt.  With independent random
+    models almost no draft is accepted, so this measures the verify-step cost.
+    Returns accepted tokens/s of the generation phase, the verify-step and
+    draft-step costs and the acceptance counts."""
+    import numpy as np
+
+    t0 = time.time()
+    target = bmx.Qwen3(bmx.qwen3_config(**bmx.QWEN3_32B), 42, 0.02, max_tokens=prompt_len)
+    draft = bmx.Qwen3(bmx.qwen3_config(**bmx.QWEN3_0_6B), 43, 0.02, max_tokens=prompt_len)
+    cap = prompt_len + new_tokens + 2 * spec_k + 8
+    tc, dc = target.new_cache(cap), draft.new_cache(cap)
+    prompt = np.array([int(v) for v in np.random.default_rng(13).integers(0, 151936, prompt_len)], np.uint32)
+    torch.cuda.synchronize()
+    log(f"speculative: 32B target + 0.6B draft ready in {time.time() - t0:.1f}s")
+    # prefill cost alone (both models), then reset
+    t0 = time.perf_counter()
+    target.forward(tc, prompt)
+    draft.forward(dc, prompt)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    tc.reset()
+    dc.reset()
+    t0 = time.perf_counter()
+    toks, stats = bmx.speculative_generate(target, tc, draft, dc, prompt, new_tokens, spec_k=spec_k, eos=())
+    torch.cuda.synchronize()
+    total_s = time.perf_counter() - t0
+    gen_s = max(total_s - prefill_s, 1e-9)
+    # verify step: one M = 5 target forward at the final context, rewound
+    seq = tc.seq_len
+    v = np.array(toks[:spec_k], np.uint32)
+    target.forward(tc, v)
+    tc.truncate(seq)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        target.forward(tc, v)
+        tc.truncate(seq)
+    torch.cuda.synchronize()
+    verify_ms = (time.perf_counter() - t0) * 100.0
+    res = {"accepted_tokens_per_s": round(len(toks) / gen_s, 2), "tokens": int(len(toks)),
+           "iterations": int(stats[0]), "drafted": int(stats[1]), "accepted": int(stats[2]),
+           "verify_step_ms": round(verify_ms, 3), "prefill_ms_both_models": round(prefill_s * 1000, 1),
+           "wall_s": round(total_s, 2), "prompt_tokens": prompt_len, "spec_k": spec_k,
+           "workload": "Qwen3-32B-shape 4-bit target + Qwen3-0.6B-shape draft, greedy speculative, batch 1"}
+    log(f"speculative: {res}")
+    target.close()
+    draft.close()
+    del tc, dc
+    torch.cuda.empty_cache()
+    return res
 
 
 def profile_roofline(bmx, torch, launches=200):
@@ -145,6 +248,10 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=8, help="decode tokens in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--qmm-sweep", action="store_true",
+                    help="also time the quantized GEMM at M = 5, 128, 512, 2048 (4B and 8B projection shapes)")
+    ap.add_argument("--speculative", action="store_true",
+                    help="also run 32B-target / 0.6B-draft greedy speculative decoding (M = 5 verify)")
     ap.add_argument("--profile-roofline", action="store_true",
                     help="only run the roofline GEMV and a copy of known size (for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -212,6 +319,9 @@ def main():
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                         "kernel": f"qmv M=1 N={N} K={K}", "avg_launch_us": round(us, 3), "bytes_per_launch": nb}
 
+    qmm = qmm_sweep(bmx, torch) if args.qmm_sweep else []
+    spec = speculative_bench(bmx, torch) if args.speculative else None
+
     cpu = None
     if not args.no_cpu:
         v, cores = cpu_baseline(args.cpu_tokens)
@@ -235,7 +345,8 @@ def main():
         "data": "synthetic: seeded random-init weights N(0,0.02) quantized 4-bit, seeded random token ids",
         "config": {"workload": "Qwen3-4B-shape 4-bit greedy decode, batch 1, after a 4096-token prefill",
                    "prompt_tokens": args.prompt, "kv_cache": [36, 2, 8, max(cap, 4352), 128],
-                   "prefill_ms": round(prefill_s * 1000, 1), "qmv_sweep": sweep},
+                   "prefill_ms": round(prefill_s * 1000, 1), "qmv_sweep": sweep, "qmm_sweep": qmm,
+                   "speculative": spec},
         "roofline": roof,
         "cpu_baseline": cpu,
     }
