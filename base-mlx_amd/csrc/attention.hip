@@ -231,11 +231,12 @@ __global__ void __launch_bounds__(W * 64) attn_kernel(const AttnParams p) {
   }
 }
 
-// Decode / short verify (R = tokens x heads-per-kv-head <= RMAX <= 8).  A
-// workgroup of 8 waves owns one kv head and 256 keys, 32 per wave.  Every
-// K, V and q load of a wave is issued before any arithmetic:
-//   QK on MFMA (v_mfma_f32_16x16x32_bf16): A = the R query rows (padded to
-//     16; lane l holds row l%16, dims 32*ks + 8*(l/16), 4 fragments read
+// Decode / short verify (R = tokens x heads-per-kv-head query rows of one kv
+// head, up to 64).  A workgroup of 8 waves owns one kv head, one tile of
+// RMAX <= 16 of those rows and 256 keys, 32 per wave.  Every K, V and q load
+// of a wave is issued before any arithmetic:
+//   QK on MFMA (v_mfma_f32_16x16x32_bf16): A = the tile's query rows (padded
+//     to 16; lane l holds row l%16, dims 32*ks + 8*(l/16), 4 fragments read
 //     straight from global: the R rows of one kv head are contiguous in
 //     [Hq, M, 128]), B = K^T (lane l holds key l%16 of each 16-key tile,
 //     same dims).  The result tile puts key l%16 and rows 4*(l/16)+i in
@@ -244,23 +245,28 @@ __global__ void __launch_bounds__(W * 64) attn_kernel(const AttnParams p) {
 //     16-lane rows; p goes to LDS as [key][row].
 //   PV on VALU: lane = 2 dims over all 32 keys (V read one 256-byte key row
 //     per load instruction), so no cross-lane reduction is needed.
-// The 8 waves' (o, m, l) are merged in LDS and one unnormalised partial per
-// workgroup goes to the split workspace (NS = ceil(L / 256)).
+// The 8 waves' (o, m, l) are merged in LDS, 8 rows at a time, and one
+// unnormalised partial per row and workgroup goes to the split workspace
+// (NS = ceil(L / 256)).
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 constexpr int kDecWaves = 8, kDecWaveKeys = 32, kDecKeys = kDecWaveKeys * kDecWaves;
+constexpr int kDecMaxRows = 64;  // query rows per kv head on this path
+constexpr int kMergeRows = 8;    // rows merged per LDS pass
 
 template <int RMAX>
 __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnParams p) {
   __shared__ __align__(16) float ps[kDecWaves][kDecWaveKeys][RMAX];
-  __shared__ __align__(16) float os[kDecWaves][RMAX][kD];
+  __shared__ __align__(16) float os[kDecWaves][kMergeRows][kD];
   __shared__ float ms[kDecWaves][RMAX], ls[kDecWaves][RMAX];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int li = lane & 15, g = lane >> 4;
   const int tn = p.M;
   const int R = tn * (p.Hq / p.Hkv);  // row r = j * tn + i: head kvh*rep + j, token i
   const int kvh = blockIdx.x, split = blockIdx.y;
+  const int r0 = blockIdx.z * RMAX;   // first row of this workgroup's tile
+  const int RT = min(RMAX, R - r0);   // rows in the tile
   const int offset = p.offset_dev ? *p.offset_dev : p.offset;
   const int L = offset + p.M;
   const int c0 = split * kDecKeys + wave * kDecWaveKeys;
@@ -268,7 +274,7 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   // ---- issue loads: q fragments, K fragments, V rows ----
   uint4 qa[4];
   {
-    const uint16_t* qrow = p.q + (static_cast<int64_t>(kvh) * R + min(li, R - 1)) * kD + g * 8;
+    const uint16_t* qrow = p.q + (static_cast<int64_t>(kvh) * R + r0 + min(li, RT - 1)) * kD + g * 8;
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) qa[ks] = *reinterpret_cast<const uint4*>(qrow + ks * 32);
   }
@@ -286,7 +292,7 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
     const int key = max(min(c0 + k, L - 1), 0);
     vr[k] = *reinterpret_cast<const uint32_t*>(p.v + hbase + static_cast<int64_t>(key) * kD + 2 * lane);
   }
-  if (li >= R) qa[0] = qa[1] = qa[2] = qa[3] = make_uint4(0, 0, 0, 0);
+  if (li >= RT) qa[0] = qa[1] = qa[2] = qa[3] = make_uint4(0, 0, 0, 0);
   // ---- S = q K^T on MFMA ----
   f32x4_t sc[2];
 #pragma unroll
@@ -297,11 +303,13 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
       sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[ks]),
                                                       __builtin_bit_cast(bf16x8_t, kb[t][ks]), sc[t], 0, 0, 0);
   }
-  // ---- softmax of the wave's 32 keys; lane holds rows 4g + i ----
+  // ---- softmax of the wave's 32 keys; lane holds tile rows 4g + i ----
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int r = 4 * g + i;
-    const int ti = r - (r / tn) * tn;
+    if (r >= RMAX) break;
+    const int rg = r0 + r;
+    const int ti = rg - (rg / tn) * tn;
     const int lim = p.causal ? min(L, offset + ti + 1) : L;  // keys < lim are visible
     float s[2];
 #pragma unroll
@@ -311,7 +319,7 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
 #pragma unroll
     for (int t = 0; t < 2; t++) e[t] = (mx == -INFINITY) ? 0.0f : expf(s[t] - mx);
     const float l = row16_sum(e[0] + e[1]);
-    if (r < R) {
+    if (r < RT) {
 #pragma unroll
       for (int t = 0; t < 2; t++) ps[wave][t * 16 + li][r] = e[t];
       if (li == 0) {
@@ -330,7 +338,7 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
     const float v0 = bf2f(vr[k] & 0xffffu), v1 = bf2f(vr[k] >> 16);
 #pragma unroll
     for (int r4 = 0; r4 < RMAX; r4 += 4) {
-      if (r4 >= R) break;
+      if (r4 >= RT) break;
       const float4 pv = *reinterpret_cast<const float4*>(&ps[wave][k][r4]);
       const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
@@ -340,36 +348,44 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
       }
     }
   }
+  // ---- merge the waves kMergeRows rows at a time; thread = (row, 4 dims) ----
 #pragma unroll
-  for (int r = 0; r < RMAX; r++) {
-    if (r >= R) break;
-    *reinterpret_cast<float2*>(&os[wave][r][2 * lane]) = make_float2(acc[r][0], acc[r][1]);
-  }
-  __syncthreads();
-  // ---- merge the waves; thread = (row, 4 dims) ----
-  for (int e = threadIdx.x; e < R * (kD / 4); e += 64 * kDecWaves) {
-    const int r = e / (kD / 4), d4 = e - r * (kD / 4);
-    float m = -INFINITY;
+  for (int h0 = 0; h0 < RMAX; h0 += kMergeRows) {
+    if (h0 >= RT) break;
+    if (h0 > 0) __syncthreads();  // the previous pass has read os
 #pragma unroll
-    for (int w = 0; w < kDecWaves; w++) m = fmaxf(m, ms[w][r]);
-    float l = 0.0f;
-    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (m != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < kDecWaves; w++) {
-        if (ms[w][r] == -INFINITY) continue;
-        const float a = expf(ms[w][r] - m);
-        const float4 ow = *reinterpret_cast<const float4*>(&os[w][r][d4 * 4]);
-        l += a * ls[w][r];
-        o.x += a * ow.x;
-        o.y += a * ow.y;
-        o.z += a * ow.z;
-        o.w += a * ow.w;
-      }
+    for (int r = 0; r < kMergeRows && r < RMAX; r++) {
+      if (h0 + r >= RT) break;
+      *reinterpret_cast<float2*>(&os[wave][r][2 * lane]) = make_float2(acc[h0 + r][0], acc[h0 + r][1]);
     }
-    const int64_t base = (static_cast<int64_t>(kvh) * R + r) * p.ns + split;  // (h * M + token) * ns + split
-    *reinterpret_cast<float4*>(p.part_o + base * kD + d4 * 4) = o;
-    if (d4 == 0) *reinterpret_cast<float2*>(p.part_ml + base * 2) = make_float2(m, l);
+    __syncthreads();
+    const int nr = min(kMergeRows, RT - h0);
+    for (int e = threadIdx.x; e < nr * (kD / 4); e += 64 * kDecWaves) {
+      const int rr = e / (kD / 4), d4 = e - rr * (kD / 4);
+      const int r = h0 + rr;
+      float m = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kDecWaves; w++) m = fmaxf(m, ms[w][r]);
+      float l = 0.0f;
+      float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (m != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < kDecWaves; w++) {
+          if (ms[w][r] == -INFINITY) continue;
+          const float a = expf(ms[w][r] - m);
+          const float4 ow = *reinterpret_cast<const float4*>(&os[w][rr][d4 * 4]);
+          l += a * ls[w][r];
+          o.x += a * ow.x;
+          o.y += a * ow.y;
+          o.z += a * ow.z;
+          o.w += a * ow.w;
+        }
+      }
+      // (h * M + token) * ns + split
+      const int64_t base = (static_cast<int64_t>(kvh) * R + r0 + r) * p.ns + split;
+      *reinterpret_cast<float4*>(p.part_o + base * kD + d4 * 4) = o;
+      if (d4 == 0) *reinterpret_cast<float2*>(p.part_ml + base * 2) = make_float2(m, l);
+    }
   }
 }
 
@@ -469,13 +485,20 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
   const int max_ns = ws ? static_cast<int>(ws_floats / (static_cast<size_t>(Hq) * M * (kD + 2))) : 1;
   const int rep = Hq / Hkv;
   const int chunks = (L_max + kDecKeys - 1) / kDecKeys;
-  if (ws && M * rep <= 8 && chunks <= max_ns) {
-    // 256 keys per workgroup, splits merged by the combine kernel
+  if (ws && M * rep <= kDecMaxRows && chunks <= max_ns) {
+    // 256 keys and up to 16 query rows per workgroup, splits merged by the
+    // combine kernel
     AttnParams p{q, k, v, out, ws, ws + static_cast<size_t>(Hq) * M * chunks * kD, offset_dev, offset,
                  Hq, Hkv, M, cap, M, chunks, M > 1 ? 1 : 0, scale};
-    const dim3 grid(Hkv, chunks);
-    if (M * rep <= 4) hipLaunchKernelGGL((attn_decode_kernel<4>), grid, dim3(64 * kDecWaves), 0, stream, p);
-    else hipLaunchKernelGGL((attn_decode_kernel<8>), grid, dim3(64 * kDecWaves), 0, stream, p);
+    const int R = M * rep;
+    if (R <= 4) {
+      hipLaunchKernelGGL((attn_decode_kernel<4>), dim3(Hkv, chunks, 1), dim3(64 * kDecWaves), 0, stream, p);
+    } else if (R <= 8) {
+      hipLaunchKernelGGL((attn_decode_kernel<8>), dim3(Hkv, chunks, 1), dim3(64 * kDecWaves), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((attn_decode_kernel<16>), dim3(Hkv, chunks, (R + 15) / 16), dim3(64 * kDecWaves), 0, stream,
+                         p);
+    }
     if (int rc = check_launch("attention_decode")) return rc;
     hipLaunchKernelGGL(attn_combine_kernel, dim3((Hq * M + 3) / 4), dim3(256), 0, stream, p);
     return check_launch("attention_combine");
