@@ -2,6 +2,10 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "bmx_device.h"
 
 namespace bmx {
@@ -24,6 +28,38 @@ int check_hip(hipError_t e, const char* what) {
 }
 
 int check_launch(const char* what) { return check_hip(hipGetLastError(), what); }
+
+int allow_lds_ptr(const void* kernel, size_t bytes) {
+  // (device, kernel) -> dynamic LDS limit already set
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, size_t> raised;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(BMX_E_ARG, "no current HIP device");
+  std::lock_guard<std::mutex> lock(mu);
+  size_t& have = raised[{dev, kernel}];
+  if (bytes <= have) return BMX_OK;
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)) != hipSuccess)
+    return set_error(BMX_E_UNSUPPORTED, "kernel needs %zu bytes of LDS", bytes);
+  have = bytes;
+  return BMX_OK;
+}
+
+int resident_blocks(const void* kernel, int threads, size_t lds) {
+  // (device, kernel, lds) -> workgroups resident on the whole device
+  static std::mutex mu;
+  static std::map<std::pair<std::pair<int, const void*>, size_t>, int> known;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  int& n = known[{{dev, kernel}, lds}];
+  if (n > 0) return n;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+  n = per_cu * cus;
+  return n;
+}
 
 }  // namespace bmx
 

@@ -51,17 +51,16 @@ struct QmvParams {
   uint2* amax;
 };
 
-// Raises a kernel's dynamic-LDS limit to `bytes` once (launches above 64 KB
-// need it); returns a BMX code.
+// Raises a kernel's dynamic-LDS limit to `bytes` (launches above 64 KB need
+// it); returns a BMX code.  Limits already raised are remembered per kernel.
+int allow_lds_ptr(const void* kernel, size_t bytes);
+// Workgroups of `threads` threads and `lds` bytes of dynamic LDS that the
+// current device holds at once (per-CU occupancy x CUs).
+int resident_blocks(const void* kernel, int threads, size_t lds);
 template <class F>
 int allow_lds(F* kernel, size_t bytes) {
-  static size_t allowed = 64 * 1024;
-  if (bytes <= allowed) return BMX_OK;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          static_cast<int>(bytes)) != hipSuccess)
-    return set_error(BMX_E_UNSUPPORTED, "kernel needs %zu bytes of LDS", bytes);
-  allowed = bytes;
-  return BMX_OK;
+  if (bytes <= 64 * 1024) return BMX_OK;
+  return allow_lds_ptr(reinterpret_cast<const void*>(kernel), bytes);
 }
 
 // Validates shapes/alignment and launches the qmv kernel family.

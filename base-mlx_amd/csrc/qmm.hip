@@ -30,15 +30,6 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 constexpr int BM = 64, BN = 128, PAD = 72;  // K step = one 64-wide group
 
-__device__ __forceinline__ uint4 permute_pairs(uint4 d) {
-  uint4 r;
-  r.x = (d.x & 0xffffu) | (d.z << 16);
-  r.y = (d.x >> 16) | (d.z & 0xffff0000u);
-  r.z = (d.y & 0xffffu) | (d.w << 16);
-  r.w = (d.y >> 16) | (d.w & 0xffff0000u);
-  return r;
-}
-
 __device__ __forceinline__ uint4 nibbles_bf16(uint32_t w) {
   const uint32_t magic = 0x43004300u;
   return make_uint4((w & 0x000f000fu) | magic, ((w >> 4) & 0x000f000fu) | magic, ((w >> 8) & 0x000f000fu) | magic,

@@ -42,25 +42,6 @@ constexpr int kThreads = 256;
 constexpr int kChunkBytes = 80;  // 64 data bytes + 16 pad per 32 x values
 constexpr int kLdsBudget = 40 * 1024;
 
-__device__ __forceinline__ uint4 permute_pairs(uint4 d) {
-  // bf16 e0..e7 in d.x=(e0,e1) d.y=(e2,e3) d.z=(e4,e5) d.w=(e6,e7)
-  // -> (e0,e4) (e1,e5) (e2,e6) (e3,e7)
-  uint4 r;
-  r.x = (d.x & 0xffffu) | (d.z << 16);
-  r.y = (d.x >> 16) | (d.z & 0xffff0000u);
-  r.z = (d.y & 0xffffu) | (d.w << 16);
-  r.w = (d.y >> 16) | (d.w & 0xffff0000u);
-  return r;
-}
-
-// floor(a / b) for 0 <= a < 2^20 and b >= 1, from rcp_b = 1.0f / b (correctly
-// rounded): (a + 0.5) / b lies at least 0.5 / b from an integer, while the
-// product's relative error is below 2^-22, i.e. below (a + 0.5) / b * 2^-22
-// < 0.5 / b whenever a + 0.5 < 2^21.
-__device__ __forceinline__ int udiv_small(int a, float rcp_b) {
-  return static_cast<int>((static_cast<float>(a) + 0.5f) * rcp_b);
-}
-
 // Dot of one packed word (8 nibbles) with its permuted x pairs, +128 bias.
 __device__ __forceinline__ float word_dot(uint32_t w, uint4 xp, float acc) {
   const uint32_t magic = 0x43004300u;
@@ -379,20 +360,6 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
       }
     }
   }
-}
-
-// Sum over groups of S consecutive lanes (S = 8, 16, 32 or 64); every lane
-// of a group gets the group's sum.  Inside 16-lane rows with DPP: quad_perm
-// [1,0,3,2] (0xB1), quad_perm [2,3,0,1] (0x4E), row_half_mirror (0x141:
-// lane i <-> 7 - i within 8), row_mirror (0x140: lane i <-> 15 - i).
-__device__ __forceinline__ float lanes_sum(float v, int S) {
-  v += dpp_f32<0xB1>(v);
-  v += dpp_f32<0x4E>(v);
-  v += dpp_f32<0x141>(v);
-  if (S >= 16) v += dpp_f32<0x140>(v);
-  if (S >= 32) v += __shfl_xor(v, 16, 64);
-  if (S >= 64) v += __shfl_xor(v, 32, 64);
-  return v;
 }
 
 // M = 1 with the whole K in one LDS phase (the decode shapes).  Every load
