@@ -389,6 +389,193 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   }
 }
 
+// Prefill / long verify: flash attention on MFMA.  A workgroup of 4 waves
+// owns one query head and 64 consecutive query tokens (16 per wave) and
+// walks the visible keys in blocks of 64 with an online softmax:
+//   S^T = K Q^T (v_mfma_f32_16x16x32_bf16; A = K rows from LDS, B = the
+//     wave's q rows, kept in registers) puts query l%16 and keys 4(l/16)+i
+//     of each 16-key tile in lane l.  The softmax runs per lane column
+//     (max / sum across the four lane quarters by shuffles), and the
+//     probabilities are already an A operand for P V: over a 32-key chunk
+//     lane l holds keys {4(l/16)+i} and {16+4(l/16)+i}, i < 4, which serve
+//     as its 8-wide k slice in that order;
+//   O += P V with B = V^T from LDS, staged transposed (4 keys x 8 dims per
+//     thread, transposed in registers) so that the same 8 keys are two
+//     8-byte reads.  p is rounded to bf16 for the product (and the row sums
+//     add the rounded values); O and the softmax statistics stay fp32.
+// The K and V^T tiles are double-buffered: the loads of key block j+1 are
+// issued before the products of block j.  Causal masking (query t sees keys
+// <= offset + t) stops at the block holding the diagonal and masks inside.
+constexpr int kFaQ = 64, kFaK = 64;  // queries per workgroup, keys per block
+constexpr int kFaKS = kD + 8;        // K tile row stride (elements)
+constexpr int kFaVS = kFaK + 8;      // V^T tile row stride (elements)
+constexpr size_t kFaLds = 2ull * (kFaK * kFaKS + kD * kFaVS) * sizeof(uint16_t);
+
+__global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnParams p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* kt_s = reinterpret_cast<uint16_t*>(smem);  // [2][kFaK][kFaKS]
+  uint16_t* vt_s = kt_s + 2 * kFaK * kFaKS;             // [2][kD][kFaVS]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y, kvh = h / (p.Hq / p.Hkv);
+  const int t0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * kFaQ;  // longest rows first
+  const int offset = p.offset_dev ? *p.offset_dev : p.offset;
+  const int L = offset + p.M;
+  const int kend = p.causal ? min(L, offset + min(t0 + kFaQ, p.M)) : L;
+  const int nkb = (kend + kFaK - 1) / kFaK;
+  const int t = t0 + 16 * wave + n;  // this lane's query (softmax column)
+  const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
+
+  // q fragments of the lane's query: dims 32 ks + 8 g .. + 7
+  uint4 qf[4];
+  {
+    const uint16_t* qrow = p.q + (static_cast<int64_t>(h) * p.M + min(t, p.M - 1)) * kD + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) qf[ks] = *reinterpret_cast<const uint4*>(qrow + 32 * ks);
+  }
+  // staging of one key block: K rows (4 x 16 bytes) and V (4 keys x 8 dims);
+  // plain registers (no arrays), so nothing is indexed at run time
+  uint4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
+  const int vdc = tid & 15, vkq = tid >> 4;  // V task: dims 8 vdc.., keys 4 vkq..
+  auto kaddr = [&](int k0, int i) {
+    const int e = tid + 256 * i, key = e >> 4, ch = e & 15;
+    return reinterpret_cast<const uint4*>(p.k + hbase + static_cast<int64_t>(min(k0 + key, L - 1)) * kD + ch * 8);
+  };
+  auto vaddr = [&](int k0, int j) {
+    return reinterpret_cast<const uint4*>(p.v + hbase + static_cast<int64_t>(min(k0 + 4 * vkq + j, L - 1)) * kD +
+                                          vdc * 8);
+  };
+  auto load_block = [&](int k0) {
+    kr0 = *kaddr(k0, 0);
+    kr1 = *kaddr(k0, 1);
+    kr2 = *kaddr(k0, 2);
+    kr3 = *kaddr(k0, 3);
+    vr0 = *vaddr(k0, 0);
+    vr1 = *vaddr(k0, 1);
+    vr2 = *vaddr(k0, 2);
+    vr3 = *vaddr(k0, 3);
+  };
+  auto store_block = [&](int buf) {
+    uint16_t* kb = kt_s + buf * kFaK * kFaKS;
+    auto kput = [&](int i, const uint4& v) {
+      const int e = tid + 256 * i, key = e >> 4, ch = e & 15;
+      *reinterpret_cast<uint4*>(kb + key * kFaKS + ch * 8) = v;
+    };
+    kput(0, kr0);
+    kput(1, kr1);
+    kput(2, kr2);
+    kput(3, kr3);
+    // V^T: dim 8 vdc + d gets keys 4 vkq .. + 3 (8 bytes)
+    uint16_t* vb = vt_s + buf * kD * kFaVS + 4 * vkq;
+    auto vput = [&](int c, uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
+      const uint2 lo = make_uint2((a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16));
+      const uint2 hi = make_uint2((a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u));
+      *reinterpret_cast<uint2*>(vb + (vdc * 8 + 2 * c) * kFaVS) = lo;
+      *reinterpret_cast<uint2*>(vb + (vdc * 8 + 2 * c + 1) * kFaVS) = hi;
+    };
+    vput(0, vr0.x, vr1.x, vr2.x, vr3.x);
+    vput(1, vr0.y, vr1.y, vr2.y, vr3.y);
+    vput(2, vr0.z, vr1.z, vr2.z, vr3.z);
+    vput(3, vr0.w, vr1.w, vr2.w, vr3.w);
+  };
+
+  f32x4_t o[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) o[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = -INFINITY, l_run = 0.0f;
+  const int lim = p.causal ? min(L, offset + t + 1) : L;  // keys < lim are visible to query t
+
+  load_block(0);
+  store_block(0);
+  __syncthreads();
+  for (int jb = 0; jb < nkb; jb++) {
+    const int buf = jb & 1, k0 = jb * kFaK;
+    const bool more = jb + 1 < nkb;
+    if (more) load_block(k0 + kFaK);
+    const uint16_t* kb = kt_s + buf * kFaK * kFaKS;
+    const uint16_t* vb = vt_s + buf * kD * kFaVS;
+    // ---- S^T = K Q^T: 4 key tiles of 16 ----
+    f32x4_t sc[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+      sc[kt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) {
+        const uint4 a = *reinterpret_cast<const uint4*>(kb + (kt * 16 + n) * kFaKS + 32 * ks + 8 * g);
+        sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                         __builtin_bit_cast(bf16x8_t, qf[ks]), sc[kt], 0, 0, 0);
+      }
+    }
+    // ---- online softmax of the lane's query over the block's 64 keys ----
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int key = k0 + kt * 16 + 4 * g + i;
+        sc[kt][i] = key < lim ? sc[kt][i] * p.scale : -INFINITY;
+        mx = fmaxf(mx, sc[kt][i]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = (m_run == -INFINITY) ? 0.0f : expf(m_run - m_new);
+    float sum = 0.0f;
+    bf16x8_t pa[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      uint32_t pw[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int kt = 2 * c + (u >> 1), i0 = 2 * (u & 1);
+        const float e0 = (sc[kt][i0] == -INFINITY) ? 0.0f : expf(sc[kt][i0] - m_new);
+        const float e1 = (sc[kt][i0 + 1] == -INFINITY) ? 0.0f : expf(sc[kt][i0 + 1] - m_new);
+        const uint16_t b0 = f2bf(e0), b1 = f2bf(e1);
+        sum += bf2f(b0) + bf2f(b1);
+        pw[u] = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
+      }
+      pa[c] = __builtin_bit_cast(bf16x8_t, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+    }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    l_run = l_run * alpha + sum;
+    m_run = m_new;
+    // ---- rescale O (rows = queries 4 g + i) and O += P V ----
+    float ar[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[j][i] *= ar[i];
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const uint16_t* vrow = vb + (j * 16 + n) * kFaVS + 32 * c + 4 * g;
+        const uint2 v0 = *reinterpret_cast<const uint2*>(vrow);
+        const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 16);
+        const bf16x8_t bv = __builtin_bit_cast(bf16x8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[c], bv, o[j], 0, 0, 0);
+      }
+    if (more) store_block(buf ^ 1);
+    __syncthreads();
+  }
+  // ---- normalise and write: lane holds dim 16 j + n of queries 4 g + i ----
+  float lr[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) lr[i] = __shfl(l_run, 4 * g + i, 64);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int tq = t0 + 16 * wave + 4 * g + i;
+    if (tq >= p.M) continue;
+    const float inv = lr[i] > 0.0f ? 1.0f / lr[i] : 0.0f;
+    uint16_t* orow = p.out + static_cast<int64_t>(tq) * p.Hq * kD + h * kD + n;
+#pragma unroll
+    for (int j = 0; j < 8; j++) orow[16 * j] = f2bf(o[j][i] * inv);
+  }
+}
+
 // Merges the NS partials (o, m, l) of each (head, token); one wave per pair,
 // lane = 2 dims.  Up to 32 splits are read per batch (all loads in flight),
 // batches folded with an online rescale.
@@ -502,6 +689,13 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
     if (int rc = check_launch("attention_decode")) return rc;
     hipLaunchKernelGGL(attn_combine_kernel, dim3((Hq * M + 3) / 4), dim3(256), 0, stream, p);
     return check_launch("attention_combine");
+  }
+  {
+    // flash attention: no split workspace
+    AttnParams p{q, k, v, out, nullptr, nullptr, offset_dev, offset, Hq, Hkv, M, cap, kFaQ, 1, M > 1 ? 1 : 0, scale};
+    if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(attn_prefill_kernel), kFaLds)) return rc;
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3((M + kFaQ - 1) / kFaQ, Hq), dim3(256), kFaLds, stream, p);
+    return check_launch("attention_prefill");
   }
   int tq, ns, w;
   attention_shape(Hq, Hkv, M, L_max, max_ns, &tq, &ns, &w);
