@@ -273,6 +273,60 @@ int orc_qmatmul(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
   return ORC_OK;
 }
 
+/* The matrix path of quantized_matmul (MLX runs its qmm kernel for
+ * matrices and its qmv kernel for a few rows; the HIP library takes this
+ * path for M > 8 rows): every weight row is dequantized to bf16 -- the bits
+ * orc_dequantize returns, s*q + b with one rounding -- and y = x w^T
+ * accumulates in fp32, rounded to bf16 [MLX upstream: the Metal qmm loader
+ * dequantizes each weight tile to the input dtype in threadgroup memory
+ * before its GEMM].  Parity unpinned at one bf16 ulp of w: MLX's loader
+ * rounds s*q and the sum separately. */
+int orc_qmm_dequant(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
+                    const uint16_t *b, uint16_t *y, int64_t M, int64_t N,
+                    int64_t K, int gs, int bits) {
+  if (bits != 4) return ORC_E_UNSUPPORTED;
+  if (gs != 64 || K % 64) return ORC_E_SHAPE;
+  const int64_t G = K / 64;
+  float *xf = (float *)malloc(sizeof(float) * (size_t)(M * K));
+  if (!xf) return ORC_E_ALLOC;
+  for (int64_t i = 0; i < M * K; i++) xf[i] = bf2f(x[i]);
+  int fail = 0;
+#pragma omp parallel
+  {
+    float *wrow = (float *)malloc(sizeof(float) * (size_t)K);
+    if (!wrow) {
+#pragma omp atomic write
+      fail = 1;
+    } else {
+#pragma omp for schedule(dynamic, 16)
+      for (int64_t n = 0; n < N; n++) {
+        for (int64_t k = 0; k < K; k++)
+          wrow[k] = bf2f(f2bf(dq_elem(wq + n * (K / 8), s + n * G, b + n * G, k, 64)));
+        for (int64_t m = 0; m < M; m++) {
+          const float *xp = xf + m * K;
+          float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+          for (int64_t k = 0; k < K; k += 8)
+            for (int j = 0; j < 8; j++) a[j] += wrow[k + j] * xp[k + j];
+          y[m * N + n] = f2bf(((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7])));
+        }
+      }
+      free(wrow);
+    }
+  }
+  free(xf);
+  return fail ? ORC_E_ALLOC : ORC_OK;
+}
+
+/* QLinear::forward (qwen3.rs:30-41) as the HIP library evaluates it: the
+ * group-decomposition GEMV for up to 8 rows of x, the dequantizing GEMM
+ * beyond. */
+int orc_qlinear(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
+                const uint16_t *b, uint16_t *y, int64_t M, int64_t N, int64_t K,
+                int gs, int bits) {
+  if (M <= 8) return orc_qmatmul(x, wq, s, b, y, M, N, K, gs, bits);
+  return orc_qmm_dequant(x, wq, s, b, y, M, N, K, gs, bits);
+}
+
 /* Same product evaluated in float64 on the dequantized weights
  * (s*q + b exact in double); the high-precision yardstick for tests. */
 int orc_qmatmul_f64(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
@@ -680,9 +734,9 @@ int orc_qwen3_forward(orc_qwen3 *m, orc_kv *kv, const uint32_t *tokens, int M,
     layer_t *L = &m->layers[l];
     /* qkv_block: rms_norm + q/k/v projections (kernels.rs:28-46) */
     orc_rms_norm(x, L->in_norm, h, M, H, c->eps);
-    orc_qmatmul(h, L->p[SLOT_Q].w, L->p[SLOT_Q].s, L->p[SLOT_Q].b, q, M, qd, H, 64, 4);
-    orc_qmatmul(h, L->p[SLOT_K].w, L->p[SLOT_K].s, L->p[SLOT_K].b, k, M, kvd, H, 64, 4);
-    orc_qmatmul(h, L->p[SLOT_V].w, L->p[SLOT_V].s, L->p[SLOT_V].b, v, M, kvd, H, 64, 4);
+    orc_qlinear(h, L->p[SLOT_Q].w, L->p[SLOT_Q].s, L->p[SLOT_Q].b, q, M, qd, H, 64, 4);
+    orc_qlinear(h, L->p[SLOT_K].w, L->p[SLOT_K].s, L->p[SLOT_K].b, k, M, kvd, H, 64, 4);
+    orc_qlinear(h, L->p[SLOT_V].w, L->p[SLOT_V].s, L->p[SLOT_V].b, v, M, kvd, H, 64, 4);
     /* per-head QK-norm before RoPE (qwen3.rs:392-399) */
     orc_rms_norm(q, L->q_norm, q, (int64_t)M * nq, hd, c->eps);
     orc_rms_norm(k, L->k_norm, k, (int64_t)M * nkv, hd, c->eps);
@@ -710,14 +764,14 @@ int orc_qwen3_forward(orc_qwen3 *m, orc_kv *kv, const uint32_t *tokens, int M,
      * (qwen3.rs:345-349, 491-518) */
     orc_sdpa(qt, kl, vl, att, nq, nkv, M, new_end, hd, kv->cap, offset, M > 1, scale);
     /* o_proj + residual (qwen3.rs:520-521) */
-    orc_qmatmul(att, L->p[SLOT_O].w, L->p[SLOT_O].s, L->p[SLOT_O].b, o, M, H, qd, 64, 4);
+    orc_qlinear(att, L->p[SLOT_O].w, L->p[SLOT_O].s, L->p[SLOT_O].b, o, M, H, qd, 64, 4);
     orc_add(x, o, x, (int64_t)MH);
     /* mlp_block + residual (kernels.rs:55-78; qwen3.rs:523-541) */
     orc_rms_norm(x, L->post_norm, h, M, H, c->eps);
-    orc_qmatmul(h, L->p[SLOT_GATE].w, L->p[SLOT_GATE].s, L->p[SLOT_GATE].b, g, M, I, H, 64, 4);
-    orc_qmatmul(h, L->p[SLOT_UP].w, L->p[SLOT_UP].s, L->p[SLOT_UP].b, u, M, I, H, 64, 4);
+    orc_qlinear(h, L->p[SLOT_GATE].w, L->p[SLOT_GATE].s, L->p[SLOT_GATE].b, g, M, I, H, 64, 4);
+    orc_qlinear(h, L->p[SLOT_UP].w, L->p[SLOT_UP].s, L->p[SLOT_UP].b, u, M, I, H, 64, 4);
     orc_silu_mul(g, u, a, (int64_t)M * I);
-    orc_qmatmul(a, L->p[SLOT_DOWN].w, L->p[SLOT_DOWN].s, L->p[SLOT_DOWN].b, o, M, H, I, 64, 4);
+    orc_qlinear(a, L->p[SLOT_DOWN].w, L->p[SLOT_DOWN].s, L->p[SLOT_DOWN].b, o, M, H, I, 64, 4);
     orc_add(x, o, x, (int64_t)MH);
   }
   /* final norm, last row unless all logits, tied head (qwen3.rs:545-555) */
@@ -725,9 +779,9 @@ int orc_qwen3_forward(orc_qwen3 *m, orc_kv *kv, const uint32_t *tokens, int M,
   {
     const qlin *head = c->tied ? &m->embed : &m->lm_head;
     if (all_logits)
-      orc_qmatmul(h, head->w, head->s, head->b, logits, M, c->vocab, H, 64, 4);
+      orc_qlinear(h, head->w, head->s, head->b, logits, M, c->vocab, H, 64, 4);
     else
-      orc_qmatmul(h + (size_t)(M - 1) * H, head->w, head->s, head->b, logits, 1, c->vocab, H, 64, 4);
+      orc_qlinear(h + (size_t)(M - 1) * H, head->w, head->s, head->b, logits, 1, c->vocab, H, 64, 4);
   }
   kv->seq_len += M; /* qwen3.rs:557 */
 done:

@@ -65,6 +65,12 @@ int orc_dequant_gather(const uint32_t *ids, int64_t M, int64_t rows,
 int orc_qmatmul(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
                 const uint16_t *b, uint16_t *y, int64_t M, int64_t N, int64_t K,
                 int gs, int bits);
+int orc_qmm_dequant(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
+                    const uint16_t *b, uint16_t *y, int64_t M, int64_t N,
+                    int64_t K, int gs, int bits);
+int orc_qlinear(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
+                const uint16_t *b, uint16_t *y, int64_t M, int64_t N, int64_t K,
+                int gs, int bits);
 int orc_qmatmul_f64(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
                     const uint16_t *b, double *y, int64_t M, int64_t N,
                     int64_t K, int gs, int bits);

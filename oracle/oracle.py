@@ -39,6 +39,8 @@ _SIGS = {
     "orc_dequant_gather": (INT, [P, I64, I64, P, P, P, I64, INT, INT, P]),
     "orc_qmatmul": (INT, [P, P, P, P, P, I64, I64, I64, INT, INT]),
     "orc_qmatmul_f64": (INT, [P, P, P, P, P, I64, I64, I64, INT, INT]),
+    "orc_qmm_dequant": (INT, [P, P, P, P, P, I64, I64, I64, INT, INT]),
+    "orc_qlinear": (INT, [P, P, P, P, P, I64, I64, I64, INT, INT]),
     "orc_rms_norm": (None, [P, P, P, I64, I64, F]),
     "orc_rope": (None, [P, P, I64, I64, I64, F, I64]),
     "orc_slice_update": (INT, [P, INT, P, P, P, P, P]),
@@ -167,6 +169,28 @@ def qmatmul(x, wq, s, b, gs=64, bits=4):
     N = wq.shape[0]
     y = np.empty((M, N), np.uint16)
     _chk(lib().orc_qmatmul(_p(x), _p(wq), _p(s), _p(b), _p(y), M, N, K, gs, bits))
+    return y
+
+
+def qmm_dequant(x, wq, s, b, gs=64, bits=4):
+    """Matrix path: bf16-dequantized weights, fp32-accumulated x w^T."""
+    x = np.ascontiguousarray(x, np.uint16)
+    K = x.shape[-1]
+    M = x.size // K
+    N = wq.shape[0]
+    y = np.empty((M, N), np.uint16)
+    _chk(lib().orc_qmm_dequant(_p(x), _p(wq), _p(s), _p(b), _p(y), M, N, K, gs, bits))
+    return y
+
+
+def qlinear(x, wq, s, b, gs=64, bits=4):
+    """The product's dispatch: qmatmul for M <= 8 rows, qmm_dequant beyond."""
+    x = np.ascontiguousarray(x, np.uint16)
+    K = x.shape[-1]
+    M = x.size // K
+    N = wq.shape[0]
+    y = np.empty((M, N), np.uint16)
+    _chk(lib().orc_qlinear(_p(x), _p(wq), _p(s), _p(b), _p(y), M, N, K, gs, bits))
     return y
 
 

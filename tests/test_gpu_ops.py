@@ -130,5 +130,6 @@ def test_qmm_vs_oracle(gpu, orc, M, N, K):
     ref64 = orc.qmatmul_f64(xb, wq, sb, bb)
     yb = torch_bf16_bits(y)
     assert max_rel_err(bf16_to_f32(yb), ref64) < 1e-2
-    # same group decomposition as the oracle: within 2 bf16 ulps of it
-    assert _close(yb, orc.qmatmul(xb, wq, sb, bb), ulps=2, floor=1e-4) == 1.0
+    # the matrix path of the oracle (bf16-dequantized weights, fp32
+    # accumulation): within 2 bf16 ulps of it
+    assert _close(yb, orc.qmm_dequant(xb, wq, sb, bb), ulps=2, floor=1e-4) == 1.0

@@ -170,3 +170,27 @@ def test_qmatmul_vs_float64_matmul(orc, M, N, K):
     assert np.all(np.abs(y - ref) <= tol)
     # the float64 yardstick of the oracle agrees with numpy
     np.testing.assert_allclose(orc.qmatmul_f64(x, wq, s, b), ref, rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 64, 512), (16, 96, 2560), (37, 40, 4096)])
+def test_qmm_dequant_vs_float64_on_dequantized_weights(orc, M, N, K):
+    """Matrix path: y = bf16(x w^T) with w the bf16 weights orc.dequantize
+    returns (pinned bit-exact separately); numpy float64 on those same bf16
+    weights is the yardstick, so a dropped scale / bias, a transposed operand
+    or a skipped weight rounding shows up well above the fp32 summation bar."""
+    wq, s, b = orc.init_qlinear(300 + M, N, K)
+    x = orc.fill_normal_bf16(400 + M, M * K).reshape(M, K)
+    y = bf16_to_f32(orc.qmm_dequant(x, wq, s, b))
+    w16 = bf16_to_f32(orc.dequantize(wq, s, b)).astype(np.float64)
+    ref = bf16_to_f32(x).astype(np.float64) @ w16.T
+    # bf16 output rounding (2^-9 relative) plus fp32 accumulation error
+    tol = np.abs(ref) * 2 ** -8 + 1e-5 * np.sqrt(K) * np.max(np.abs(ref))
+    assert np.all(np.abs(y - ref) <= tol)
+    # the unrounded weights (s*q + b in float64) give a measurably different
+    # product: the weight rounding is really there
+    nib = ((wq[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(N, K)
+    wx = np.repeat(bf16_to_f32(s), 64, 1).astype(np.float64) * nib + np.repeat(bf16_to_f32(b), 64, 1)
+    assert np.max(np.abs(w16 - wx)) > 0
+    # dispatch: qlinear is qmatmul up to 8 rows and qmm_dequant beyond
+    np.testing.assert_array_equal(orc.qlinear(x, wq, s, b), orc.qmm_dequant(x, wq, s, b))
+    np.testing.assert_array_equal(orc.qlinear(x[:8], wq, s, b), orc.qmatmul(x[:8], wq, s, b))
