@@ -276,6 +276,10 @@ def main():
         model = bmx.Qwen3(bmx.qwen3_config(**SHAPE_4B), 42, 0.02, max_tokens=min(args.prompt, 4096))
         cache = model.new_cache(max(cap, 4352))
         prompt = np.array([int(v) for v in np.random.default_rng(11).integers(0, 151936, args.prompt)], np.uint32)
+        # prefill twice: the first forward of the process also pays one-time
+        # setup (LDS limits, the split-K buffer); the second is timed
+        model.forward(cache, prompt)
+        cache.reset()
         torch.cuda.synchronize()
         t0 = time.time()
         logits = model.forward(cache, prompt)
