@@ -12,14 +12,21 @@ namespace bmx {
 __device__ __forceinline__ float bf2f(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
-// f32 -> bf16, round to nearest even; NaN stays a (quiet) NaN.
+// f32 -> bf16, round to nearest even; NaN stays a (quiet) NaN.  One
+// v_cvt_pk_bf16_f32 (gfx950), and conversions of neighbouring values pair up.
 __device__ __forceinline__ uint16_t f2bf(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+// The same rounding in integer arithmetic, for a float that must first exist
+// as a float: the compiler folds double -> float -> bf16 conversions into one
+// (single-rounding) conversion, which differs in rare ties.
+__device__ __forceinline__ uint16_t f2bf_int(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
   u += 0x7fffu + ((u >> 16) & 1u);
   return static_cast<uint16_t>(u >> 16);
 }
-__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 

@@ -57,7 +57,7 @@ __global__ void __launch_bounds__(256)
   uint4* wp = reinterpret_cast<uint4*>(w + n * (K / 8) + g * 8);
   wp[0] = make_uint4(words[0], words[1], words[2], words[3]);
   wp[1] = make_uint4(words[4], words[5], words[6], words[7]);
-  s[n * G + g] = f2bf(static_cast<float>(sd));
+  s[n * G + g] = f2bf_int(static_cast<float>(sd));  // double -> float -> bf16, two roundings
   b[n * G + g] = f2bf(__fmul_rn(static_cast<float>(lo), c));
 }
 
