@@ -9,16 +9,14 @@
 // (qwen3.rs:629-653) lets query t attend keys j <= offset + t, which is
 // applied here as a predicate (masked keys contribute exactly 0).
 //
-// Decomposition (flash-decoding).  A workgroup of W waves owns one kv head,
-// a tile of TQ query tokens (R = TQ * Hq/Hkv query rows, all sharing the kv
-// head) and one of NS splits of the key range.  It walks its split in chunks
-// of 64*W keys with an online softmax:
-//   QK: lane = key; the key row (128 bf16) sits in registers, query rows
-//       (pre-scaled, fp32) are broadcast from LDS;
-//   softmax: one wave per row updates the running max / sum;
-//   PV: thread = (row, pair of dims); V rows are read coalesced, p from LDS.
-// With NS > 1 the unnormalised partial (o, m, l) goes to a workspace and a
-// combine kernel merges the splits.
+// Two kernels, chosen by the number of query rows per kv head
+// (R = new tokens x q heads per kv head):
+//   R <= 64 (decode, speculative verify): attn_decode_kernel splits the key
+//     range over workgroups of 256 keys (flash-decoding) and
+//     attn_combine_kernel merges the unnormalised partials (o, m, l);
+//   otherwise (prefill): attn_prefill_kernel, flash attention with one
+//     workgroup per (query head, 64 query tokens) walking all visible keys.
+// Both run Q K^T and (prefill) P V on the matrix cores.
 #include <math.h>
 
 #include "bmx_device.h"
@@ -43,193 +41,6 @@ struct AttnParams {
   int causal;
   float scale;
 };
-
-// KP = true: the PV product splits the chunk's keys over the W waves (each
-// wave accumulates all R <= IT rows over its 64 keys, partials added across
-// waves at the end) -- the decode / verify shape.  KP = false: rows split
-// over waves, each wave walks all keys (prefill).
-template <int W, int IT, bool KP>
-__global__ void __launch_bounds__(W * 64) attn_kernel(const AttnParams p) {
-  constexpr int CH = 64 * W;  // keys per chunk
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int rep = p.Hq / p.Hkv;
-  const int kvh = blockIdx.x;
-  const int qt = blockIdx.y;
-  const int split = blockIdx.z;
-  const int t0 = qt * p.tq;
-  const int tn = min(p.tq, p.M - t0);
-  const int R = tn * rep;  // rows: r = j * tn + i  (head kvh*rep + j, token t0 + i)
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int offset = p.offset_dev ? *p.offset_dev : p.offset;
-  const int L = offset + p.M;  // keys in the cache view
-  // keys this tile can see: causal -> up to offset + t0 + tn - 1
-  const int Lt = p.causal ? offset + t0 + tn : L;
-  const int per = ((Lt + p.ns - 1) / p.ns + CH - 1) / CH * CH;
-  const int kbeg = split * per;
-  const int kend = min(Lt, kbeg + per);
-
-  float* qs = reinterpret_cast<float*>(smem);  // [R][128]
-  float* ps = qs + R * kD;                     // [R][CH]
-  float* st = ps + R * CH;                     // [R][3]: m, l, alpha
-
-  for (int e = threadIdx.x; e < R * kD; e += W * 64) {
-    const int r = e / kD, d = e - r * kD;
-    const int j = r / tn, i = r - j * tn;
-    qs[e] = bf2f(p.q[(static_cast<int64_t>(kvh * rep + j) * p.M + t0 + i) * kD + d]) * p.scale;
-  }
-  for (int r = threadIdx.x; r < R; r += W * 64) {
-    st[r * 3 + 0] = -INFINITY;
-    st[r * 3 + 1] = 0.0f;
-  }
-  // PV accumulators: dims (2*lane, 2*lane+1) of rows it (KP) or wave + W*it
-  float acc[IT][2];
-#pragma unroll
-  for (int it = 0; it < IT; it++) acc[it][0] = acc[it][1] = 0.0f;
-  __syncthreads();
-
-  const uint16_t* kb = p.k + static_cast<int64_t>(kvh) * p.cap * kD;
-  const uint16_t* vb = p.v + static_cast<int64_t>(kvh) * p.cap * kD;
-  for (int c0 = kbeg; c0 < kend; c0 += CH) {
-    // ---- QK: lane = key ----
-    {
-      const int j = c0 + wave * 64 + lane;
-      const bool kok = j < kend;
-      uint4 kr[16];
-      const uint4* kp = reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(kok ? j : c0) * kD);
-#pragma unroll
-      for (int c = 0; c < 16; c++) kr[c] = kp[c];
-      for (int r = 0; r < R; r++) {
-        const float* qr = qs + r * kD;
-        float s = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 16; c++) {
-          const uint32_t w4[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
-          const float4 qa = *reinterpret_cast<const float4*>(qr + c * 8);
-          const float4 qb = *reinterpret_cast<const float4*>(qr + c * 8 + 4);
-          s += qa.x * bf2f(w4[0] & 0xffffu) + qa.y * bf2f(w4[0] >> 16) + qa.z * bf2f(w4[1] & 0xffffu) +
-               qa.w * bf2f(w4[1] >> 16) + qb.x * bf2f(w4[2] & 0xffffu) + qb.y * bf2f(w4[2] >> 16) +
-               qb.z * bf2f(w4[3] & 0xffffu) + qb.w * bf2f(w4[3] >> 16);
-        }
-        const int t = t0 + (r % tn);
-        const bool vis = kok && (!p.causal || j <= offset + t);
-        ps[r * CH + wave * 64 + lane] = vis ? s : -INFINITY;
-      }
-    }
-    __syncthreads();
-    // ---- online softmax: one wave per row ----
-    for (int r = wave; r < R; r += W) {
-      float* pr = ps + r * CH;
-      float mx = -INFINITY;
-      for (int c = lane; c < CH; c += 64) mx = fmaxf(mx, pr[c]);
-      for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-      const float m_old = st[r * 3 + 0];
-      const float m_new = fmaxf(m_old, mx);
-      float sum = 0.0f;
-      for (int c = lane; c < CH; c += 64) {
-        const float e = (m_new == -INFINITY) ? 0.0f : expf(pr[c] - m_new);
-        pr[c] = e;
-        sum += e;
-      }
-      sum = wave_sum_xor(sum, 64);
-      if (lane == 0) {
-        const float alpha = (m_old == -INFINITY) ? 0.0f : expf(m_old - m_new);
-        st[r * 3 + 0] = m_new;
-        st[r * 3 + 1] = st[r * 3 + 1] * alpha + sum;
-        st[r * 3 + 2] = alpha;
-      }
-    }
-    __syncthreads();
-    // ---- PV ----
-    {
-      constexpr int UNR = 8;
-#pragma unroll
-      for (int it = 0; it < IT; it++) {
-        const int r = KP ? it : wave + W * it;
-        if (r < R) {
-          const float alpha = st[r * 3 + 2];
-          acc[it][0] *= alpha;
-          acc[it][1] *= alpha;
-        }
-      }
-      // keys [kb0, kb1) of this wave; masked / out-of-range keys have p = 0
-      const int kb0 = KP ? c0 + wave * 64 : c0;
-      const int nk = KP ? max(0, min(64, kend - kb0)) : min(CH, kend - c0);
-      const int pc0 = KP ? wave * 64 : 0;
-      for (int c = 0; c < nk; c += UNR) {
-        float v0[UNR], v1[UNR];
-#pragma unroll
-        for (int u = 0; u < UNR; u++) {
-          const int key = kb0 + min(c + u, nk - 1);
-          const uint32_t vv = *reinterpret_cast<const uint32_t*>(vb + static_cast<int64_t>(key) * kD + 2 * lane);
-          v0[u] = bf2f(vv & 0xffffu);
-          v1[u] = bf2f(vv >> 16);
-        }
-#pragma unroll
-        for (int u = 0; u < UNR; u++) {
-          if (c + u < nk) {
-#pragma unroll
-            for (int it = 0; it < IT; it++) {
-              const int r = KP ? it : wave + W * it;
-              if (r < R) {
-                const float pv = ps[r * CH + pc0 + c + u];
-                acc[it][0] += pv * v0[u];
-                acc[it][1] += pv * v1[u];
-              }
-            }
-          }
-        }
-      }
-    }
-    __syncthreads();
-  }
-
-  if (KP) {
-    // add the W waves' partials: wave 0 ends up with the totals
-    float* red = st + R * 3;  // [W][IT][128], its own region after the softmax state
-    if (wave > 0) {
-#pragma unroll
-      for (int it = 0; it < IT; it++) {
-        red[((wave * IT + it) * kD) + 2 * lane] = acc[it][0];
-        red[((wave * IT + it) * kD) + 2 * lane + 1] = acc[it][1];
-      }
-    }
-    __syncthreads();
-    if (wave != 0) return;
-    for (int w2 = 1; w2 < W; w2++) {
-#pragma unroll
-      for (int it = 0; it < IT; it++) {
-        acc[it][0] += red[((w2 * IT + it) * kD) + 2 * lane];
-        acc[it][1] += red[((w2 * IT + it) * kD) + 2 * lane + 1];
-      }
-    }
-  }
-
-  // ---- write ----
-#pragma unroll
-  for (int it = 0; it < IT; it++) {
-    const int r = KP ? it : wave + W * it;
-    if (r >= R) continue;
-    const int j = r / tn, i = r - j * tn;
-    const int h = kvh * rep + j, t = t0 + i;
-    const float m = st[r * 3 + 0], l = st[r * 3 + 1];
-    if (p.ns == 1) {
-      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-      uint16_t* o = p.out + static_cast<int64_t>(t) * p.Hq * kD + h * kD + 2 * lane;
-      o[0] = f2bf(acc[it][0] * inv);
-      o[1] = f2bf(acc[it][1] * inv);
-    } else {
-      const int64_t base = (static_cast<int64_t>(h) * p.M + t) * p.ns + split;
-      float* o = p.part_o + base * kD + 2 * lane;
-      o[0] = acc[it][0];
-      o[1] = acc[it][1];
-      if (lane == 0) {
-        p.part_ml[base * 2 + 0] = m;
-        p.part_ml[base * 2 + 1] = l;
-      }
-    }
-  }
-}
 
 // Decode / short verify (R = tokens x heads-per-kv-head query rows of one kv
 // head, up to 64).  A workgroup of 8 waves owns one kv head, one tile of
@@ -402,7 +213,9 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
 //   O += P V with B = V^T from LDS, staged transposed (4 keys x 8 dims per
 //     thread, transposed in registers) so that the same 8 keys are two
 //     8-byte reads.  p is rounded to bf16 for the product (and the row sums
-//     add the rounded values); O and the softmax statistics stay fp32.
+//     add the rounded values); O and the softmax statistics stay fp32.  The
+//     softmax runs in base 2 (v_exp_f32 on scores pre-multiplied by log2 e),
+//     and O is rescaled only in blocks where some row's running max moved.
 // The K and V^T tiles are double-buffered: the loads of key block j+1 are
 // issued before the products of block j.  Causal masking (query t sees keys
 // <= offset + t) stops at the block holding the diagonal and masks inside.
@@ -484,6 +297,7 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnParams p) {
   for (int j = 0; j < 8; j++) o[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = -INFINITY, l_run = 0.0f;
   const int lim = p.causal ? min(L, offset + t + 1) : L;  // keys < lim are visible to query t
+  const float scale2 = p.scale * 1.44269504088896340736f;  // scale * log2(e)
 
   load_block(0);
   store_block(0);
@@ -506,20 +320,24 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnParams p) {
                                                          __builtin_bit_cast(bf16x8_t, qf[ks]), sc[kt], 0, 0, 0);
       }
     }
-    // ---- online softmax of the lane's query over the block's 64 keys ----
+    // ---- online softmax of the lane's query over the block's 64 keys, in
+    // base 2: scores carry scale * log2(e), p = 2^(s - m) on v_exp_f32 ----
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 4; kt++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int key = k0 + kt * 16 + 4 * g + i;
-        sc[kt][i] = key < lim ? sc[kt][i] * p.scale : -INFINITY;
+        sc[kt][i] = key < lim ? sc[kt][i] * scale2 : -INFINITY;
         mx = fmaxf(mx, sc[kt][i]);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
-    const float alpha = (m_run == -INFINITY) ? 0.0f : expf(m_run - m_new);
+    // 2^(-inf) = 0 covers the first block (m_run = -inf) and masked keys; a
+    // row with nothing visible yet keeps m = -inf and is skipped
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     float sum = 0.0f;
     bf16x8_t pa[2];
 #pragma unroll
@@ -528,9 +346,8 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnParams p) {
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int kt = 2 * c + (u >> 1), i0 = 2 * (u & 1);
-        const float e0 = (sc[kt][i0] == -INFINITY) ? 0.0f : expf(sc[kt][i0] - m_new);
-        const float e1 = (sc[kt][i0 + 1] == -INFINITY) ? 0.0f : expf(sc[kt][i0 + 1] - m_new);
-        const uint16_t b0 = f2bf(e0), b1 = f2bf(e1);
+        const uint16_t b0 = f2bf(__builtin_amdgcn_exp2f(sc[kt][i0] - m_use));
+        const uint16_t b1 = f2bf(__builtin_amdgcn_exp2f(sc[kt][i0 + 1] - m_use));
         sum += bf2f(b0) + bf2f(b1);
         pw[u] = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
       }
@@ -540,14 +357,17 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnParams p) {
     sum += __shfl_xor(sum, 32, 64);
     l_run = l_run * alpha + sum;
     m_run = m_new;
-    // ---- rescale O (rows = queries 4 g + i) and O += P V ----
-    float ar[4];
+    // ---- rescale O (rows = queries 4 g + i) when a running max moved, then
+    // O += P V ----
+    if (__any(alpha != 1.0f)) {
+      float ar[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * g + i, 64);
+      for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * g + i, 64);
 #pragma unroll
-    for (int j = 0; j < 8; j++)
+      for (int j = 0; j < 8; j++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) o[j][i] *= ar[i];
+        for (int i = 0; i < 4; i++) o[j][i] *= ar[i];
+    }
 #pragma unroll
     for (int c = 0; c < 2; c++)
 #pragma unroll
@@ -621,45 +441,11 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const AttnParams p) {
   o[1] = f2bf(o1 * inv);
 }
 
-template <int W>
-int launch_w(const AttnParams& p, dim3 grid, int R, hipStream_t st) {
-  // q rows, scores of one chunk, softmax state; plus the cross-wave partials
-  // [W][IT][128] of the key-split variant
-  const size_t lds = static_cast<size_t>(R) * (kD + 64 * W + 3) * 4;
-  const size_t red4 = static_cast<size_t>(W) * 4 * kD * 4, red8 = static_cast<size_t>(W) * 8 * kD * 4;
-  if (R > 32 || R < 1) return set_error(BMX_E_SHAPE, "attention: %d query rows per workgroup", R);
-  if (R <= 4) hipLaunchKernelGGL((attn_kernel<W, 4, true>), grid, dim3(W * 64), lds + red4, st, p);
-  else if (R <= 8) hipLaunchKernelGGL((attn_kernel<W, 8, true>), grid, dim3(W * 64), lds + red8, st, p);
-  else {
-    const int it = (R + W - 1) / W;
-    if (it <= 4) hipLaunchKernelGGL((attn_kernel<W, 4, false>), grid, dim3(W * 64), lds, st, p);
-    else hipLaunchKernelGGL((attn_kernel<W, 8, false>), grid, dim3(W * 64), lds, st, p);
-  }
-  return check_launch("attention");
-}
-
 }  // namespace
 
 // Workspace floats needed for the split partials of one call.
 size_t attention_workspace_floats(int Hq, int M, int ns) {
   return static_cast<size_t>(Hq) * M * ns * (kD + 2);
-}
-
-// Picks the query tile / split shape.  `max_ns` bounds the splits by the
-// workspace available (0 = no workspace: single split).
-void attention_shape(int Hq, int Hkv, int M, int L_max, int max_ns, int* tq, int* ns, int* w) {
-  const int rep = Hq / Hkv;
-  // R = tq * rep query rows share a workgroup; R <= 32 keeps LDS <= 50 KB
-  *tq = M <= 8 ? M : 8;
-  while (*tq > 1 && *tq * rep > 32) (*tq)--;
-  *w = 4;
-  const int qtiles = (M + *tq - 1) / *tq;
-  const int blocks = Hkv * qtiles;
-  int n = 1;
-  const int chunks = (L_max + 64 * *w - 1) / (64 * *w);
-  while (blocks * n < 512 && n * 2 <= chunks) n *= 2;
-  if (n > max_ns) n = max_ns > 0 ? max_ns : 1;
-  *ns = n;
 }
 
 int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* ws,
@@ -697,17 +483,6 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
     hipLaunchKernelGGL(attn_prefill_kernel, dim3((M + kFaQ - 1) / kFaQ, Hq), dim3(256), kFaLds, stream, p);
     return check_launch("attention_prefill");
   }
-  int tq, ns, w;
-  attention_shape(Hq, Hkv, M, L_max, max_ns, &tq, &ns, &w);
-  AttnParams p{q, k, v, out, ws, ws ? ws + static_cast<size_t>(Hq) * M * ns * kD : nullptr, offset_dev, offset,
-               Hq, Hkv, M, cap, tq, ns, M > 1 ? 1 : 0, scale};
-  const dim3 grid(Hkv, (M + tq - 1) / tq, ns);
-  if (int rc = launch_w<4>(p, grid, tq * rep, stream)) return rc;
-  if (ns > 1) {
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((Hq * M + 3) / 4), dim3(256), 0, stream, p);
-    return check_launch("attention_combine");
-  }
-  return BMX_OK;
 }
 
 }  // namespace bmx
