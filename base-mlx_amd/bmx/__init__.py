@@ -183,7 +183,7 @@ def qk_norm_rope_kv(q, k, v, q_norm, k_norm, k_cache, v_cache, offset, eps=1e-6,
     return q_out
 
 
-def attention(q, k_cache, v_cache, offset, scale=None, use_workspace=True, stream=None):
+def attention(q, k_cache, v_cache, offset, scale=None, use_workspace=True, workspace=None, stream=None):
     """GQA SDPA of q [Hq, M, D] over cache rows [0, offset + M); returns [M, Hq*D]."""
     torch = _torch()
     _require_cuda(q, k_cache, v_cache)
@@ -191,10 +191,36 @@ def attention(q, k_cache, v_cache, offset, scale=None, use_workspace=True, strea
     Hkv, cap, _ = k_cache.shape
     scale = 1.0 / (D ** 0.5) if scale is None else scale
     out = torch.empty(M, Hq * D, dtype=torch.bfloat16, device=q.device)
-    nbytes = load().bmx_attention_workspace_bytes(Hq, M) if use_workspace else 0
-    ws = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=q.device) if use_workspace else None
+    if use_workspace and workspace is None:
+        workspace = attention_workspace(Hq, M, q.device)
+    nbytes = workspace.numel() * 4 if use_workspace else 0
     call("bmx_attention_gqa", _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), Hq, Hkv, M, D, cap, offset,
-         ctypes.c_float(scale), _ptr(ws), nbytes, _stream(stream))
+         ctypes.c_float(scale), _ptr(workspace if use_workspace else None), nbytes, _stream(stream))
+    return out
+
+
+def attention_workspace(Hq, M, device="cuda"):
+    """A zero-filled attention workspace (arrival counters + split partials)."""
+    torch = _torch()
+    nbytes = load().bmx_attention_workspace_bytes(Hq, M)
+    return torch.zeros(max(nbytes // 4, 1), dtype=torch.float32, device=device)
+
+
+def qk_norm_rope_kv_attention(q, k, v, q_norm, k_norm, k_cache, v_cache, offset, eps=1e-6, theta=1e6, scale=None,
+                              workspace=None, stream=None):
+    """Fused QK-norm + RoPE + KV write + GQA attention of M new tokens; returns [M, Hq*128]."""
+    torch = _torch()
+    _require_cuda(q, k, v, q_norm, k_norm, k_cache, v_cache)
+    Hkv, cap, D = k_cache.shape
+    M = q.shape[0]
+    Hq = q.shape[-1] // D
+    scale = 1.0 / (D ** 0.5) if scale is None else scale
+    if workspace is None:
+        workspace = attention_workspace(Hq, M, q.device)
+    out = torch.empty(M, Hq * D, dtype=torch.bfloat16, device=q.device)
+    call("bmx_qk_norm_rope_kv_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm), _ptr(k_norm), _ptr(k_cache),
+         _ptr(v_cache), _ptr(out), M, Hq, Hkv, D, cap, offset, ctypes.c_float(eps), ctypes.c_float(theta),
+         ctypes.c_float(scale), _ptr(workspace), workspace.numel() * 4, _stream(stream))
     return out
 
 

@@ -27,12 +27,13 @@ namespace {
 constexpr int kD = 128;  // head_dim
 
 struct AttnParams {
-  const uint16_t* q;  // [Hq, M, 128]
+  const uint16_t* q;  // [Hq, M, 128]; fused prologue: raw q projection rows [M, Hq*128]
   const uint16_t* k;  // [Hkv, cap, 128]
   const uint16_t* v;  // [Hkv, cap, 128]
   uint16_t* out;      // [M, Hq*128]
   float* part_o;      // [Hq, M, NS, 128]
   float* part_ml;     // [Hq, M, NS, 2]
+  unsigned* cnt;      // [Hkv, row tiles] arrival counters, zero between calls
   const int* offset_dev;
   int offset;
   int Hq, Hkv, M, cap;
@@ -42,39 +43,124 @@ struct AttnParams {
   float scale;
 };
 
+// Inputs of the fused QK-norm + RoPE + KV-write prologue of the decode
+// kernel (the operation of qk_norm_rope_kv_kernel): raw k / v projection
+// rows, the q / k norm weights and the rope table.
+struct FuseParams {
+  const uint16_t* k_new;  // [M, Hkv*128]
+  const uint16_t* v_new;  // [M, Hkv*128]
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  float eps;
+  RopeTable tab;
+};
+
+// The split partials travel between workgroups on different XCDs (each with
+// its own L2) through agent-scope atomic loads and stores (relaxed), which
+// the compiler issues with sc1 -- coherent across the XCDs without the L2
+// writeback / invalidate of a device-scope fence.
+__device__ __forceinline__ void store_agent(float* a, float v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* a) {
+  return __hip_atomic_load(const_cast<float*>(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merges the NS partials (o, m, l) of one (head, token) pair `wid` into
+// out; one wave, lane = 2 dims.  Up to 32 splits are read per batch (all
+// loads in flight), batches folded with an online rescale.
+__device__ __forceinline__ void combine_pair(const AttnParams& p, int wid, int lane) {
+  const int h = wid / p.M, t = wid - h * p.M;
+  const int64_t base = static_cast<int64_t>(wid) * p.ns;
+  constexpr int B = 32;
+  float mx = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  for (int s0 = 0; s0 < p.ns; s0 += B) {
+    float2 ml[B], ov[B];
+#pragma unroll
+    for (int u = 0; u < B; u++) {
+      const int s = min(s0 + u, p.ns - 1);
+      const float* pm = p.part_ml + (base + s) * 2;
+      const float* po = p.part_o + (base + s) * kD + 2 * lane;
+      ml[u] = make_float2(load_agent(pm), load_agent(pm + 1));
+      ov[u] = make_float2(load_agent(po), load_agent(po + 1));
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < B; u++)
+      if (s0 + u < p.ns) bm = fmaxf(bm, ml[u].x);
+    const float nm = fmaxf(mx, bm);
+    if (nm == -INFINITY) continue;
+    const float a = (mx == -INFINITY) ? 0.0f : expf(mx - nm);
+    l *= a;
+    o0 *= a;
+    o1 *= a;
+#pragma unroll
+    for (int u = 0; u < B; u++) {
+      if (s0 + u >= p.ns || ml[u].x == -INFINITY) continue;
+      const float w = expf(ml[u].x - nm);
+      l += w * ml[u].y;
+      o0 += w * ov[u].x;
+      o1 += w * ov[u].y;
+    }
+    mx = nm;
+  }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  uint16_t* o = p.out + static_cast<int64_t>(t) * p.Hq * kD + h * kD + 2 * lane;
+  o[0] = f2bf(o0 * inv);
+  o[1] = f2bf(o1 * inv);
+}
+
 // Decode / short verify (R = tokens x heads-per-kv-head query rows of one kv
 // head, up to 64).  A workgroup of 8 waves owns one kv head, one tile of
 // RMAX <= 16 of those rows and 256 keys, 32 per wave.  Every K, V and q load
 // of a wave is issued before any arithmetic:
 //   QK on MFMA (v_mfma_f32_16x16x32_bf16): A = the tile's query rows (padded
-//     to 16; lane l holds row l%16, dims 32*ks + 8*(l/16), 4 fragments read
-//     straight from global: the R rows of one kv head are contiguous in
-//     [Hq, M, 128]), B = K^T (lane l holds key l%16 of each 16-key tile,
-//     same dims).  The result tile puts key l%16 and rows 4*(l/16)+i in
-//     lane l; scores are scaled after the exact bf16 x bf16 products.
+//     to 16; lane l holds row l%16, dims 32*ks + 8*(l/16), 4 fragments; the
+//     R rows of one kv head are contiguous in [Hq, M, 128]), B = K^T (lane l
+//     holds key l%16 of each 16-key tile, same dims).  The result tile puts
+//     key l%16 and rows 4*(l/16)+i in lane l; scores are scaled after the
+//     exact bf16 x bf16 products.
 //   softmax over the wave's 32 keys: registers + DPP reductions inside
 //     16-lane rows; p goes to LDS as [key][row].
 //   PV on VALU: lane = 2 dims over all 32 keys (V read one 256-byte key row
 //     per load instruction), so no cross-lane reduction is needed.
 // The 8 waves' (o, m, l) are merged in LDS, 8 rows at a time, and one
 // unnormalised partial per row and workgroup goes to the split workspace
-// (NS = ceil(L / 256)).
+// (NS = ceil(L / 256)).  The last workgroup of a (kv head, row tile) to
+// finish -- an arrival counter per pair, bumped once the workgroup's partial
+// stores have completed, wrapping back to zero on the last arrival -- merges
+// the NS partials of its rows into out; no workgroup waits for another.
+//
+// FUSED: q holds the raw q projection rows, and the prologue does the work
+// of qk_norm_rope_kv_kernel first: each wave norms and rotates whole head
+// rows (qk_norm_rope_lane) -- the tile's q rows into LDS, and the new keys
+// offset + t that fall in this workgroup's 256 keys into LDS and (row tile
+// 0 only) into the caches.  K / V rows of new keys come from LDS instead of
+// the (possibly not yet written) cache rows.
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 constexpr int kDecWaves = 8, kDecWaveKeys = 32, kDecKeys = kDecWaveKeys * kDecWaves;
 constexpr int kDecMaxRows = 64;  // query rows per kv head on this path
 constexpr int kMergeRows = 8;    // rows merged per LDS pass
+constexpr int kFuseMaxM = 16;    // new tokens of the fused prologue
+constexpr int kQS = kD + 8;      // LDS row stride of the prologue's q / k rows
+constexpr int kCounters = 1024;  // arrival counters at the head of the workspace
 
-template <int RMAX>
-__global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnParams p) {
+template <int RMAX, bool FUSED>
+__global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnParams p, const FuseParams f) {
   __shared__ __align__(16) float ps[kDecWaves][kDecWaveKeys][RMAX];
   __shared__ __align__(16) float os[kDecWaves][kMergeRows][kD];
   __shared__ float ms[kDecWaves][RMAX], ls[kDecWaves][RMAX];
+  __shared__ __align__(16) uint16_t qs[FUSED ? RMAX : 1][kQS];
+  __shared__ __align__(16) uint16_t kn[FUSED ? kFuseMaxM : 1][kQS];
+  __shared__ __align__(16) uint16_t vn[FUSED ? kFuseMaxM : 1][kD];
+  __shared__ int last;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int li = lane & 15, g = lane >> 4;
   const int tn = p.M;
-  const int R = tn * (p.Hq / p.Hkv);  // row r = j * tn + i: head kvh*rep + j, token i
+  const int rep = p.Hq / p.Hkv;
+  const int R = tn * rep;  // row r = j * tn + i: head kvh*rep + j, token i
   const int kvh = blockIdx.x, split = blockIdx.y;
   const int r0 = blockIdx.z * RMAX;   // first row of this workgroup's tile
   const int RT = min(RMAX, R - r0);   // rows in the tile
@@ -82,9 +168,38 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   const int L = offset + p.M;
   const int c0 = split * kDecKeys + wave * kDecWaveKeys;
   const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
+  // ---- fused prologue, part 1: raw rows of this wave's items (issued first,
+  // so that waiting for them does not wait for the K / V loads) ----
+  // items: it < RT: q row r0 + it; else new token t_lo + it - RT
+  constexpr int kItems = FUSED ? (RMAX + kFuseMaxM + kDecWaves - 1) / kDecWaves : 0;
+  const int t_lo = max(0, split * kDecKeys - offset);
+  const int t_hi = min(p.M, split * kDecKeys + kDecKeys - offset);
+  const int n_items = RT + max(0, t_hi - t_lo);
+  float ra[kItems > 0 ? kItems : 1], rb[kItems > 0 ? kItems : 1];
+  uint16_t rv0[kItems > 0 ? kItems : 1], rv1[kItems > 0 ? kItems : 1];
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int u = 0; u < kItems; u++) {
+      const int it = wave + u * kDecWaves;
+      if (it < n_items) {
+        const uint16_t* src;
+        if (it < RT) {
+          const int rg = r0 + it, j = rg / tn, i = rg - j * tn;
+          src = p.q + (static_cast<int64_t>(i) * p.Hq + kvh * rep + j) * kD;
+        } else {
+          const int64_t row = static_cast<int64_t>(t_lo + it - RT) * p.Hkv + kvh;
+          src = f.k_new + row * kD;
+          rv0[u] = f.v_new[row * kD + lane];
+          rv1[u] = f.v_new[row * kD + lane + 64];
+        }
+        ra[u] = bf2f(src[lane]);
+        rb[u] = bf2f(src[lane + 64]);
+      }
+    }
+  }
   // ---- issue loads: q fragments, K fragments, V rows ----
   uint4 qa[4];
-  {
+  if constexpr (!FUSED) {
     const uint16_t* qrow = p.q + (static_cast<int64_t>(kvh) * R + r0 + min(li, RT - 1)) * kD + g * 8;
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) qa[ks] = *reinterpret_cast<const uint4*>(qrow + ks * 32);
@@ -102,6 +217,60 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   for (int k = 0; k < kDecWaveKeys; k++) {
     const int key = max(min(c0 + k, L - 1), 0);
     vr[k] = *reinterpret_cast<const uint32_t*>(p.v + hbase + static_cast<int64_t>(key) * kD + 2 * lane);
+  }
+  if constexpr (FUSED) {
+    // ---- fused prologue, part 2: norm + rope into LDS (and the caches) ----
+#pragma unroll
+    for (int u = 0; u < kItems; u++) {
+      const int it = wave + u * kDecWaves;
+      if (it < n_items) {
+        const bool is_q = it < RT;
+        const int t = is_q ? (r0 + it) % tn : t_lo + it - RT;
+        uint16_t o1, o2;
+        qk_norm_rope_lane(ra[u], rb[u], is_q ? f.q_norm : f.k_norm, f.tab.inv_freq[lane],
+                          static_cast<float>(offset + t), f.eps, lane, o1, o2);
+        if (is_q) {
+          qs[it][lane] = o1;
+          qs[it][lane + 64] = o2;
+        } else {
+          kn[t][lane] = o1;
+          kn[t][lane + 64] = o2;
+          vn[t][lane] = rv0[u];
+          vn[t][lane + 64] = rv1[u];
+          if (blockIdx.z == 0) {
+            // the cache rows offset + t (qwen3.rs:431-489); written once per launch
+            const int64_t slot = hbase + static_cast<int64_t>(offset + t) * kD;
+            uint16_t* kc = const_cast<uint16_t*>(p.k) + slot;
+            uint16_t* vc = const_cast<uint16_t*>(p.v) + slot;
+            kc[lane] = o1;
+            kc[lane + 64] = o2;
+            vc[lane] = rv0[u];
+            vc[lane + 64] = rv1[u];
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (li < RT) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ks++) qa[ks] = *reinterpret_cast<const uint4*>(&qs[li][ks * 32 + g * 8]);
+    }
+    // new keys: K fragments and V rows from LDS
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const int tt = c0 + t * 16 + li - offset;
+      if (tt >= 0 && tt < p.M) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) kb[t][ks] = *reinterpret_cast<const uint4*>(&kn[tt][ks * 32 + g * 8]);
+      }
+    }
+    if (t_hi > t_lo) {
+#pragma unroll
+      for (int k = 0; k < kDecWaveKeys; k++) {
+        const int tt = c0 + k - offset;
+        if (tt >= 0 && tt < p.M) vr[k] = *reinterpret_cast<const uint32_t*>(&vn[tt][2 * lane]);
+      }
+    }
   }
   if (li >= RT) qa[0] = qa[1] = qa[2] = qa[3] = make_uint4(0, 0, 0, 0);
   // ---- S = q K^T on MFMA ----
@@ -194,10 +363,29 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
       }
       // (h * M + token) * ns + split
       const int64_t base = (static_cast<int64_t>(kvh) * R + r0 + r) * p.ns + split;
-      *reinterpret_cast<float4*>(p.part_o + base * kD + d4 * 4) = o;
-      if (d4 == 0) *reinterpret_cast<float2*>(p.part_ml + base * 2) = make_float2(m, l);
+      float* po = p.part_o + base * kD + d4 * 4;
+      store_agent(po, o.x);
+      store_agent(po + 1, o.y);
+      store_agent(po + 2, o.z);
+      store_agent(po + 3, o.w);
+      if (d4 == 0) {
+        store_agent(p.part_ml + base * 2, m);
+        store_agent(p.part_ml + base * 2 + 1, l);
+      }
     }
   }
+  // ---- the last of the ns workgroups of this (kv head, row tile) merges ----
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // wraps to 0 on the ns-th arrival, ready for the next call
+    last = atomicInc(p.cnt + kvh * gridDim.z + blockIdx.z, static_cast<unsigned>(p.ns - 1)) ==
+           static_cast<unsigned>(p.ns - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  // every partial of the pair completed before its workgroup's arrival
+  for (int r = wave; r < RT; r += kDecWaves) combine_pair(p, kvh * R + r0 + r, lane);
 }
 
 // Prefill / long verify: flash attention on MFMA.  A workgroup of 4 waves
@@ -396,93 +584,91 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnParams p) {
   }
 }
 
-// Merges the NS partials (o, m, l) of each (head, token); one wave per pair,
-// lane = 2 dims.  Up to 32 splits are read per batch (all loads in flight),
-// batches folded with an online rescale.
-__global__ void __launch_bounds__(256) attn_combine_kernel(const AttnParams p) {
-  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (wid >= p.Hq * p.M) return;
-  const int h = wid / p.M, t = wid - h * p.M;
-  const int64_t base = static_cast<int64_t>(wid) * p.ns;
-  constexpr int B = 32;
-  float mx = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (int s0 = 0; s0 < p.ns; s0 += B) {
-    float2 ml[B], ov[B];
-#pragma unroll
-    for (int u = 0; u < B; u++) {
-      const int s = min(s0 + u, p.ns - 1);
-      ml[u] = *reinterpret_cast<const float2*>(p.part_ml + (base + s) * 2);
-      ov[u] = *reinterpret_cast<const float2*>(p.part_o + (base + s) * kD + 2 * lane);
-    }
-    float bm = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < B; u++)
-      if (s0 + u < p.ns) bm = fmaxf(bm, ml[u].x);
-    const float nm = fmaxf(mx, bm);
-    if (nm == -INFINITY) continue;
-    const float a = (mx == -INFINITY) ? 0.0f : expf(mx - nm);
-    l *= a;
-    o0 *= a;
-    o1 *= a;
-#pragma unroll
-    for (int u = 0; u < B; u++) {
-      if (s0 + u >= p.ns || ml[u].x == -INFINITY) continue;
-      const float w = expf(ml[u].x - nm);
-      l += w * ml[u].y;
-      o0 += w * ov[u].x;
-      o1 += w * ov[u].y;
-    }
-    mx = nm;
-  }
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  uint16_t* o = p.out + static_cast<int64_t>(t) * p.Hq * kD + h * kD + 2 * lane;
-  o[0] = f2bf(o0 * inv);
-  o[1] = f2bf(o1 * inv);
-}
-
 }  // namespace
 
-// Workspace floats needed for the split partials of one call.
+// Workspace floats of one call: the arrival counters, then the split
+// partials.
 size_t attention_workspace_floats(int Hq, int M, int ns) {
-  return static_cast<size_t>(Hq) * M * ns * (kD + 2);
+  return kCounters + static_cast<size_t>(Hq) * M * ns * (kD + 2);
 }
 
-int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* ws,
-                     size_t ws_floats, int Hq, int Hkv, int M, int D, int cap, int offset, const int* offset_dev,
-                     int L_max, float scale, hipStream_t stream) {
+namespace {
+
+// The split-key decode path, if the call fits it: R = M * rep <= 64 rows per
+// kv head, a workspace with room for one split per 256 keys, and (fused) at
+// most kFuseMaxM new tokens.  Returns kNoFit when it does not apply.
+int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, size_t ws_floats, int L_max,
+                  hipStream_t stream) {
+  const int Hq = base.Hq, Hkv = base.Hkv, M = base.M;
+  const int rep = Hq / Hkv, R = M * rep;
+  if (!ws || R > kDecMaxRows || (fuse && M > kFuseMaxM)) return kNoFit;
+  if (ws_floats < kCounters) return kNoFit;
+  const int max_ns = static_cast<int>((ws_floats - kCounters) / (static_cast<size_t>(Hq) * M * (kD + 2)));
+  const int chunks = (L_max + kDecKeys - 1) / kDecKeys;
+  if (chunks > max_ns) return kNoFit;
+  const int rmax = R <= 4 ? 4 : R <= 8 ? 8 : 16;
+  const int tiles = (R + rmax - 1) / rmax;
+  if (Hkv * tiles > kCounters) return kNoFit;
+  AttnParams p = base;
+  p.cnt = reinterpret_cast<unsigned*>(ws);
+  p.part_o = ws + kCounters;
+  p.part_ml = p.part_o + static_cast<size_t>(Hq) * M * chunks * kD;
+  p.tq = M;
+  p.ns = chunks;
+  p.causal = M > 1 ? 1 : 0;
+  const FuseParams f = fuse ? *fuse : FuseParams{};
+  const dim3 grid(Hkv, chunks, tiles), block(64 * kDecWaves);
+#define BMX_DECODE_LAUNCH(RM)                                                                   \
+  do {                                                                                          \
+    if (fuse)                                                                                   \
+      hipLaunchKernelGGL((attn_decode_kernel<RM, true>), grid, block, 0, stream, p, f);         \
+    else                                                                                        \
+      hipLaunchKernelGGL((attn_decode_kernel<RM, false>), grid, block, 0, stream, p, f);        \
+  } while (0)
+  if (rmax == 4)
+    BMX_DECODE_LAUNCH(4);
+  else if (rmax == 8)
+    BMX_DECODE_LAUNCH(8);
+  else
+    BMX_DECODE_LAUNCH(16);
+#undef BMX_DECODE_LAUNCH
+  return check_launch(fuse ? "attention_decode_fused" : "attention_decode");
+}
+
+int check_attention_shape(int Hq, int Hkv, int M, int D, int cap, int offset, const int* offset_dev) {
   if (D != kD) return set_error(BMX_E_UNSUPPORTED, "attention: head_dim must be 128 (got %d)", D);
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || M <= 0) return set_error(BMX_E_SHAPE, "attention: bad head counts");
   if (!offset_dev && (offset < 0 || offset + M > cap))
     return set_error(BMX_E_KV_CAPACITY, "attention: %d positions exceed capacity %d", offset + M, cap);
-  const int max_ns = ws ? static_cast<int>(ws_floats / (static_cast<size_t>(Hq) * M * (kD + 2))) : 1;
-  const int rep = Hq / Hkv;
-  const int chunks = (L_max + kDecKeys - 1) / kDecKeys;
-  if (ws && M * rep <= kDecMaxRows && chunks <= max_ns) {
-    // 256 keys and up to 16 query rows per workgroup, splits merged by the
-    // combine kernel
-    AttnParams p{q, k, v, out, ws, ws + static_cast<size_t>(Hq) * M * chunks * kD, offset_dev, offset,
-                 Hq, Hkv, M, cap, M, chunks, M > 1 ? 1 : 0, scale};
-    const int R = M * rep;
-    if (R <= 4) {
-      hipLaunchKernelGGL((attn_decode_kernel<4>), dim3(Hkv, chunks, 1), dim3(64 * kDecWaves), 0, stream, p);
-    } else if (R <= 8) {
-      hipLaunchKernelGGL((attn_decode_kernel<8>), dim3(Hkv, chunks, 1), dim3(64 * kDecWaves), 0, stream, p);
-    } else {
-      hipLaunchKernelGGL((attn_decode_kernel<16>), dim3(Hkv, chunks, (R + 15) / 16), dim3(64 * kDecWaves), 0, stream,
-                         p);
-    }
-    if (int rc = check_launch("attention_decode")) return rc;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((Hq * M + 3) / 4), dim3(256), 0, stream, p);
-    return check_launch("attention_combine");
-  }
-  {
-    // flash attention: no split workspace
-    AttnParams p{q, k, v, out, nullptr, nullptr, offset_dev, offset, Hq, Hkv, M, cap, kFaQ, 1, M > 1 ? 1 : 0, scale};
-    if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(attn_prefill_kernel), kFaLds)) return rc;
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3((M + kFaQ - 1) / kFaQ, Hq), dim3(256), kFaLds, stream, p);
-    return check_launch("attention_prefill");
-  }
+  return BMX_OK;
+}
+
+}  // namespace
+
+int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* ws,
+                     size_t ws_floats, int Hq, int Hkv, int M, int D, int cap, int offset, const int* offset_dev,
+                     int L_max, float scale, hipStream_t stream) {
+  if (int rc = check_attention_shape(Hq, Hkv, M, D, cap, offset, offset_dev)) return rc;
+  AttnParams p{q, k, v, out, nullptr, nullptr, nullptr, offset_dev, offset, Hq, Hkv, M, cap, kFaQ, 1,
+               M > 1 ? 1 : 0, scale};
+  const int rc = launch_decode(p, nullptr, ws, ws_floats, L_max, stream);
+  if (rc != kNoFit) return rc;
+  // flash attention: no split workspace
+  if (int e = allow_lds_ptr(reinterpret_cast<const void*>(attn_prefill_kernel), kFaLds)) return e;
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3((M + kFaQ - 1) / kFaQ, Hq), dim3(256), kFaLds, stream, p);
+  return check_launch("attention_prefill");
+}
+
+int launch_qkv_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                         const uint16_t* k_norm, uint16_t* k_cache, uint16_t* v_cache, uint16_t* out, float* ws,
+                         size_t ws_floats, int Hq, int Hkv, int M, int D, int cap, int offset,
+                         const int* offset_dev, int L_max, float eps, const RopeTable& tab, float scale,
+                         hipStream_t stream) {
+  if (int rc = check_attention_shape(Hq, Hkv, M, D, cap, offset, offset_dev)) return rc;
+  AttnParams p{q, k_cache, v_cache, out, nullptr, nullptr, nullptr, offset_dev, offset, Hq, Hkv, M, cap, M, 1,
+               M > 1 ? 1 : 0, scale};
+  FuseParams f{k, v, q_norm, k_norm, eps, tab};
+  return launch_decode(p, &f, ws, ws_floats, L_max, stream);
 }
 
 }  // namespace bmx
@@ -490,7 +676,7 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
 using namespace bmx;
 
 extern "C" size_t bmx_attention_workspace_bytes(int n_heads, int M) {
-  // enough for one split per 64 keys of a 16384-position cache
+  // enough for one split per 256 keys of a 65536-position cache
   return attention_workspace_floats(n_heads, M, 256) * sizeof(float);
 }
 
@@ -501,4 +687,23 @@ extern "C" int bmx_attention_gqa(const bmx_bf16* q, const bmx_bf16* k_cache, con
   return launch_attention(q, k_cache, v_cache, out, static_cast<float*>(workspace), workspace_bytes / sizeof(float),
                           n_heads, n_kv_heads, M, head_dim, capacity, offset, nullptr, offset + M, scale,
                           as_stream(stream));
+}
+
+extern "C" int bmx_qk_norm_rope_kv_attention(const bmx_bf16* q, const bmx_bf16* k, const bmx_bf16* v,
+                                             const bmx_bf16* q_norm, const bmx_bf16* k_norm, bmx_bf16* k_cache,
+                                             bmx_bf16* v_cache, bmx_bf16* out, int M, int n_heads, int n_kv_heads,
+                                             int head_dim, int capacity, int offset, float eps, float theta,
+                                             float scale, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!q || !k || !v || !q_norm || !k_norm || !k_cache || !v_cache || !out || !workspace)
+    return set_error(BMX_E_ARG, "qk_norm_rope_kv_attention: null pointer");
+  const int rc = launch_qkv_attention(q, k, v, q_norm, k_norm, k_cache, v_cache, out, static_cast<float*>(workspace),
+                                      workspace_bytes / sizeof(float), n_heads, n_kv_heads, M, head_dim, capacity,
+                                      offset, nullptr, offset + M, eps, make_rope_table(head_dim, theta), scale,
+                                      as_stream(stream));
+  if (rc == kNoFit)
+    return set_error(BMX_E_UNSUPPORTED,
+                     "qk_norm_rope_kv_attention: needs M <= %d, M * (n_heads / n_kv_heads) <= %d and a workspace of "
+                     "bmx_attention_workspace_bytes(n_heads, M) bytes",
+                     kFuseMaxM, kDecMaxRows);
+  return rc;
 }

@@ -84,7 +84,18 @@ int launch_qk_norm_rope_kv(const uint16_t* q, const uint16_t* k, const uint16_t*
                            const uint16_t* k_norm, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int M,
                            int Hq, int Hkv, int D, int cap, int offset, const int* offset_dev, float eps,
                            const RopeTable& tab, hipStream_t stream);
+// Returned by a launcher whose kernel does not fit the call (nothing launched).
+constexpr int kNoFit = -100;
+// Attention workspace (floats): arrival counters, then split partials; the
+// counters must be zero before the first call, and every call leaves them so.
 size_t attention_workspace_floats(int Hq, int M, int ns);
+// QK-norm + RoPE + KV write + decode attention in one kernel; kNoFit unless
+// M <= 16, M * (Hq / Hkv) <= 64 and ws holds one split per 256 keys of L_max.
+int launch_qkv_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                         const uint16_t* k_norm, uint16_t* k_cache, uint16_t* v_cache, uint16_t* out, float* ws,
+                         size_t ws_floats, int Hq, int Hkv, int M, int D, int cap, int offset,
+                         const int* offset_dev, int L_max, float eps, const RopeTable& tab, float scale,
+                         hipStream_t stream);
 int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* ws,
                      size_t ws_floats, int Hq, int Hkv, int M, int D, int cap, int offset, const int* offset_dev,
                      int L_max, float scale, hipStream_t stream);

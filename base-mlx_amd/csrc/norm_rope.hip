@@ -125,21 +125,16 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kv_kernel(const QkvRopeParam
   const uint16_t* src = is_q ? p.q + (static_cast<int64_t>(t) * p.Hq + h) * 128
                              : p.k + (static_cast<int64_t>(t) * p.Hkv + hk) * 128;
   const uint16_t* nw = is_q ? p.q_norm : p.k_norm;
-  const float a = bf2f(src[lane]), b = bf2f(src[lane + 64]);
-  const float ss = wave_sum_xor(a * a + b * b, 64);
-  const float inv = 1.0f / sqrtf(ss / 128.0f + p.eps);
-  const float na = bf2f(f2bf(bf2f(nw[lane]) * round_bf(a * inv)));
-  const float nb = bf2f(f2bf(bf2f(nw[lane + 64]) * round_bf(b * inv)));
-  float o1, o2;
-  rope_pair(na, nb, pos * p.tab.inv_freq[lane], o1, o2);
+  uint16_t o1, o2;
+  qk_norm_rope_lane(bf2f(src[lane]), bf2f(src[lane + 64]), nw, p.tab.inv_freq[lane], pos, p.eps, lane, o1, o2);
   if (is_q) {
     uint16_t* dst = p.q_out + (static_cast<int64_t>(h) * p.M + t) * 128;
-    dst[lane] = f2bf(o1);
-    dst[lane + 64] = f2bf(o2);
+    dst[lane] = o1;
+    dst[lane + 64] = o2;
   } else {
     const int64_t slot = (static_cast<int64_t>(hk) * p.cap + offset + t) * 128;
-    p.k_cache[slot + lane] = f2bf(o1);
-    p.k_cache[slot + lane + 64] = f2bf(o2);
+    p.k_cache[slot + lane] = o1;
+    p.k_cache[slot + lane + 64] = o2;
     const uint16_t* vs = p.v + (static_cast<int64_t>(t) * p.Hkv + hk) * 128;
     p.v_cache[slot + lane] = vs[lane];
     p.v_cache[slot + lane + 64] = vs[lane + 64];

@@ -197,14 +197,22 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       if (int rc = launch_qmm(m->h, L.p[SLOT_K].w, L.p[SLOT_K].s, L.p[SLOT_K].b, m->k, M, kvd, H, st)) return rc;
       if (int rc = launch_qmm(m->h, L.p[SLOT_V].w, L.p[SLOT_V].s, L.p[SLOT_V].b, m->v, M, kvd, H, st)) return rc;
     }
-    // ---- QK-norm, RoPE at the cache offset, KV write (qwen3.rs:392-489) ----
-    if (int rc = launch_qk_norm_rope_kv(m->q, m->k, m->v, L.q_norm, L.k_norm, m->qr, c->k(l), c->v(l), M, nq, nkv,
-                                        hd, c->cap, offset, pos_dev, cf.eps, m->rope, st))
-      return rc;
-    // ---- SDPA over [0, offset + M) with the causal-offset mask (qwen3.rs:491-518) ----
-    if (int rc = launch_attention(m->qr, c->k(l), c->v(l), m->att, m->attn_ws, m->attn_ws_floats, nq, nkv, M, hd,
-                                  c->cap, offset, pos_dev, L_max, scale, st))
-      return rc;
+    // ---- QK-norm, RoPE at the cache offset, KV write (qwen3.rs:392-489) and
+    // SDPA over [0, offset + M) with the causal-offset mask (qwen3.rs:491-518):
+    // one fused kernel for decode / short verify, else two steps ----
+    const int fused = launch_qkv_attention(m->q, m->k, m->v, L.q_norm, L.k_norm, c->k(l), c->v(l), m->att,
+                                           m->attn_ws, m->attn_ws_floats, nq, nkv, M, hd, c->cap, offset, pos_dev,
+                                           L_max, cf.eps, m->rope, scale, st);
+    if (fused != kNoFit) {
+      if (fused) return fused;
+    } else {
+      if (int rc = launch_qk_norm_rope_kv(m->q, m->k, m->v, L.q_norm, L.k_norm, m->qr, c->k(l), c->v(l), M, nq,
+                                          nkv, hd, c->cap, offset, pos_dev, cf.eps, m->rope, st))
+        return rc;
+      if (int rc = launch_attention(m->qr, c->k(l), c->v(l), m->att, m->attn_ws, m->attn_ws_floats, nq, nkv, M, hd,
+                                    c->cap, offset, pos_dev, L_max, scale, st))
+        return rc;
+    }
     // ---- o_proj + residual (qwen3.rs:520-521) ----
     if (M <= 8) {
       QmvParams p{};
@@ -382,11 +390,13 @@ extern "C" int bmx_qwen3_create_random(const bmx_qwen3_config* cfg, uint64_t see
   if (!rc) rc = dalloc_t(m, &m->u, T * I);
   if (!rc) rc = dalloc_t(m, &m->a, T * I);
   if (!rc) rc = dalloc_t(m, &m->logits1, static_cast<size_t>(cfg->vocab));
-  // split partials: one split per 64 keys for decode (up to 16384 cached
-  // positions), 64 splits for short verify forwards
+  // attention split partials: 256 splits of 256 keys for decode (65536
+  // cached positions), 64 for verify forwards of up to 16 tokens
   m->attn_ws_floats = std::max(attention_workspace_floats(cfg->n_heads, 1, 256),
                                attention_workspace_floats(cfg->n_heads, 16, 64));
   if (!rc) rc = dalloc_t(m, &m->attn_ws, m->attn_ws_floats);
+  // the arrival counters at its head start at zero (and every call leaves them so)
+  if (!rc) rc = check_hip(hipMemsetAsync(m->attn_ws, 0, m->attn_ws_floats * sizeof(float), st), "hipMemsetAsync");
   if (!rc) rc = dalloc_t(m, &m->ids, T);
   if (!rc) rc = dalloc_t(m, &m->tok_u, T < 64 ? 64 : T);
   if (!rc) rc = dalloc_t(m, &m->next_tok, 64);

@@ -138,8 +138,11 @@ int bmx_qk_norm_rope_kv(const bmx_bf16 *q, const bmx_bf16 *k, const bmx_bf16 *v,
  * k_cache, v_cache [n_kv_heads, capacity, 128] rows 0..offset+M-1:
  * out [M, n_heads*128] = softmax(scale q k^T + mask) v, query head h using
  * kv head h / (n_heads / n_kv_heads); for M > 1 query t sees keys
- * j <= offset + t.  `workspace` (may be NULL: no key split) holds split
- * partials; bmx_attention_workspace_bytes(n_heads, M) is enough.
+ * j <= offset + t.  `workspace` (may be NULL: no key split) holds arrival
+ * counters and split partials; bmx_attention_workspace_bytes(n_heads, M) is
+ * enough.  It must be zero-filled before its first use; every call leaves
+ * the counters zero again, so it is reused as is.  Calls that share one
+ * workspace must not run concurrently.
  * Replaces: mlx_rs::fast::scaled_dot_product_attention with the
  *   causal_mask_offset mask (crates/base-mlx-core/src/model/qwen3.rs:491-518,
  *   629-653). */
@@ -147,6 +150,21 @@ int bmx_attention_gqa(const bmx_bf16 *q, const bmx_bf16 *k_cache, const bmx_bf16
                       int n_heads, int n_kv_heads, int M, int head_dim, int capacity, int offset, float scale,
                       void *workspace, size_t workspace_bytes, void *stream);
 size_t bmx_attention_workspace_bytes(int n_heads, int M);
+
+/* bmx_qk_norm_rope_kv followed by bmx_attention_gqa, as one kernel: q, k, v
+ * are the raw projection rows [M, n_heads*128] / [M, n_kv_heads*128]; the
+ * new keys and values go to k_cache / v_cache rows offset..offset+M-1 as
+ * bmx_qk_norm_rope_kv writes them, and out is bit-identical to the two-call
+ * sequence (the normed q itself is not stored).  Needs M <= 16,
+ * M * (n_heads / n_kv_heads) <= 64 and a zero-filled workspace as for
+ * bmx_attention_gqa (else BMX_E_UNSUPPORTED, nothing written).
+ * Replaces: the same per-layer sequence of Qwen3::forward_internal
+ *   (crates/base-mlx-core/src/model/qwen3.rs:392-518) on decode and
+ *   speculative-verify steps. */
+int bmx_qk_norm_rope_kv_attention(const bmx_bf16 *q, const bmx_bf16 *k, const bmx_bf16 *v, const bmx_bf16 *q_norm,
+                                  const bmx_bf16 *k_norm, bmx_bf16 *k_cache, bmx_bf16 *v_cache, bmx_bf16 *out, int M,
+                                  int n_heads, int n_kv_heads, int head_dim, int capacity, int offset, float eps,
+                                  float theta, float scale, void *workspace, size_t workspace_bytes, void *stream);
 
 /* out[r] = index of the max of x[r, 0:n] (first index on ties), uint32.
  * Replaces: argmax / argmax_axis in pick_next and the speculative loop

@@ -93,6 +93,80 @@ def test_attention(gpu, orc, Hq, Hkv, M, offset):
         assert _close(yb, ref, ulps=2, floor=2e-3) > 0.999
 
 
+def test_attention_workspace_reuse(gpu, orc):
+    """One zero-filled workspace over calls of different split counts and row
+    tilings: the arrival counters come back to zero after every call."""
+    import torch
+
+    scale = 1 / np.sqrt(128)
+    ws = gpu.attention_workspace(64, 8)
+    for i, (Hq, M, offset) in enumerate([(32, 1, 4000), (32, 1, 10), (64, 5, 700), (64, 8, 1000), (32, 1, 3)]):
+        cap = offset + M + 1
+        q = gpu.fill_normal_bf16(40 + i, (Hq, M, 128))
+        kc = gpu.fill_normal_bf16(50 + i, (8, cap, 128))
+        vc = gpu.fill_normal_bf16(60 + i, (8, cap, 128))
+        y = gpu.attention(q, kc, vc, offset, scale, workspace=ws)
+        ref = orc.sdpa(torch_bf16_bits(q), torch_bf16_bits(kc), torch_bf16_bits(vc), offset + M, offset, M > 1,
+                       np.float32(scale))
+        assert _close(torch_bf16_bits(y), ref, ulps=2, floor=2e-3) > 0.999, (Hq, M, offset)
+    torch.cuda.synchronize()
+    assert not ws[:1024].any()  # counters
+
+
+# (Hq, Hkv, M, offset): decode at several context lengths, new keys straddling
+# a 256-key split boundary (253 + 5), 16 new tokens with 4 q heads per kv head
+# (64 rows, four row tiles), rep 8 verify
+@pytest.mark.parametrize("Hq,Hkv,M,offset", [(32, 8, 1, 0), (32, 8, 1, 4095), (32, 8, 1, 300), (64, 8, 5, 2043),
+                                             (32, 8, 5, 253), (32, 8, 16, 100), (16, 8, 3, 511)])
+def test_qk_norm_rope_kv_attention_fused(gpu, orc, Hq, Hkv, M, offset):
+    """The fused kernel against the two-call sequence (bit-identical out and
+    cache rows), twice in a row on one workspace, and against the oracle."""
+    import torch
+
+    cap = offset + 2 * M + 3
+    kc0 = gpu.fill_normal_bf16(20, (Hkv, cap, 128))
+    vc0 = gpu.fill_normal_bf16(21, (Hkv, cap, 128))
+    qn = gpu.fill_normal_bf16(22, (128,), sigma=0.3)
+    kn = gpu.fill_normal_bf16(23, (128,), sigma=0.3)
+    kc_a, vc_a = kc0.clone(), vc0.clone()
+    kc_b, vc_b = kc0.clone(), vc0.clone()
+    ws = gpu.attention_workspace(Hq, M)
+    for step in range(2):
+        off = offset + step * M
+        q = gpu.fill_normal_bf16(24 + step, (M, Hq * 128), sigma=3.0)
+        k = gpu.fill_normal_bf16(26 + step, (M, Hkv * 128), sigma=3.0)
+        v = gpu.fill_normal_bf16(28 + step, (M, Hkv * 128))
+        qr = gpu.qk_norm_rope_kv(q, k, v, qn, kn, kc_a, vc_a, off)
+        y_a = gpu.attention(qr, kc_a, vc_a, off)
+        y_b = gpu.qk_norm_rope_kv_attention(q, k, v, qn, kn, kc_b, vc_b, off, workspace=ws)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(torch_bf16_bits(y_b), torch_bf16_bits(y_a))
+        np.testing.assert_array_equal(torch_bf16_bits(kc_b), torch_bf16_bits(kc_a))
+        np.testing.assert_array_equal(torch_bf16_bits(vc_b), torch_bf16_bits(vc_a))
+        ref = orc.sdpa(torch_bf16_bits(qr), torch_bf16_bits(kc_a), torch_bf16_bits(vc_a), off + M, off, M > 1,
+                       np.float32(1 / np.sqrt(128)))
+        assert _close(torch_bf16_bits(y_b), ref, ulps=2, floor=2e-3) > 0.999
+    assert not ws[:1024].any()  # counters back at zero
+
+
+def test_qk_norm_rope_kv_attention_limits(gpu):
+    import torch
+
+    q = gpu.fill_normal_bf16(30, (17, 32 * 128))
+    k = gpu.fill_normal_bf16(31, (17, 8 * 128))
+    kc = torch.zeros(8, 64, 128, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    n = gpu.fill_normal_bf16(32, (128,))
+    with pytest.raises(gpu.BmxError) as ei:  # 17 new tokens: more than the fused prologue takes
+        gpu.qk_norm_rope_kv_attention(q, k, k, n, n, kc, vc, 0)
+    assert ei.value.code == gpu.BMX_E_UNSUPPORTED
+    with pytest.raises(gpu.BmxError) as ei:
+        gpu.qk_norm_rope_kv_attention(q[:4], k[:4], k[:4], n, n, kc, vc, 61)
+    assert ei.value.code == gpu.BMX_E_KV_CAPACITY
+    torch.cuda.synchronize()
+    assert not kc.any() and not vc.any()
+
+
 @pytest.mark.parametrize("n", [151936, 1001])
 def test_argmax(gpu, orc, n):
     """16-byte vector path (rows of a multiple of 8) and the scalar path."""
