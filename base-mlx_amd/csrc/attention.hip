@@ -59,30 +59,34 @@ struct FuseParams {
 // its own L2) through agent-scope atomic loads and stores (relaxed), which
 // the compiler issues with sc1 -- coherent across the XCDs without the L2
 // writeback / invalidate of a device-scope fence.
-__device__ __forceinline__ void store_agent(float* a, float v) {
-  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Pairs of floats move as one 8-byte access (8-byte aligned addresses).
+__device__ __forceinline__ void store_agent2(float* a, float x, float y) {
+  const uint64_t v = static_cast<uint64_t>(__float_as_uint(x)) | (static_cast<uint64_t>(__float_as_uint(y)) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(a), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float load_agent(const float* a) {
-  return __hip_atomic_load(const_cast<float*>(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ float2 load_agent2(const float* a) {
+  const uint64_t v =
+      __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(a)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float(static_cast<uint32_t>(v)), __uint_as_float(static_cast<uint32_t>(v >> 32)));
 }
 
 // Merges the NS partials (o, m, l) of one (head, token) pair `wid` into
-// out; one wave, lane = 2 dims.  Up to 32 splits are read per batch (all
-// loads in flight), batches folded with an online rescale.
+// out; one wave, lane = 2 dims.  Up to 24 splits are read per batch (48
+// loads, all in flight within the 63 outstanding loads a wave can count),
+// batches folded with an online rescale.
 __device__ __forceinline__ void combine_pair(const AttnParams& p, int wid, int lane) {
   const int h = wid / p.M, t = wid - h * p.M;
   const int64_t base = static_cast<int64_t>(wid) * p.ns;
-  constexpr int B = 32;
+  constexpr int B = 24;
   float mx = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
   for (int s0 = 0; s0 < p.ns; s0 += B) {
     float2 ml[B], ov[B];
 #pragma unroll
     for (int u = 0; u < B; u++) {
-      const int s = min(s0 + u, p.ns - 1);
-      const float* pm = p.part_ml + (base + s) * 2;
-      const float* po = p.part_o + (base + s) * kD + 2 * lane;
-      ml[u] = make_float2(load_agent(pm), load_agent(pm + 1));
-      ov[u] = make_float2(load_agent(po), load_agent(po + 1));
+      if (s0 + u < p.ns) {
+        ml[u] = load_agent2(p.part_ml + (base + s0 + u) * 2);
+        ov[u] = load_agent2(p.part_o + (base + s0 + u) * kD + 2 * lane);
+      }
     }
     float bm = -INFINITY;
 #pragma unroll
@@ -122,8 +126,10 @@ __device__ __forceinline__ void combine_pair(const AttnParams& p, int wid, int l
 //     exact bf16 x bf16 products.
 //   softmax over the wave's 32 keys: registers + DPP reductions inside
 //     16-lane rows; p goes to LDS as [key][row].
-//   PV on VALU: lane = 2 dims over all 32 keys (V read one 256-byte key row
-//     per load instruction), so no cross-lane reduction is needed.
+//   PV on VALU in fp32.  RMAX <= 8: V in 16-byte loads, lane = 8 dims x 8
+//     keys, the four key quarters added by permlane swap butterflies;
+//     RMAX = 16: lane = 2 dims over all 32 keys (4-byte loads, no cross-lane
+//     reduction).
 // The 8 waves' (o, m, l) are merged in LDS, 8 rows at a time, and one
 // unnormalised partial per row and workgroup goes to the split workspace
 // (NS = ceil(L / 256)).  The last workgroup of a (kv head, row tile) to
@@ -156,6 +162,7 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   __shared__ __align__(16) uint16_t kn[FUSED ? kFuseMaxM : 1][kQS];
   __shared__ __align__(16) uint16_t vn[FUSED ? kFuseMaxM : 1][kD];
   __shared__ int last;
+  constexpr bool kWideV = RMAX <= kMergeRows;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int li = lane & 15, g = lane >> 4;
   const int tn = p.M;
@@ -175,27 +182,29 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   const int t_lo = max(0, split * kDecKeys - offset);
   const int t_hi = min(p.M, split * kDecKeys + kDecKeys - offset);
   const int n_items = RT + max(0, t_hi - t_lo);
-  float ra[kItems > 0 ? kItems : 1], rb[kItems > 0 ? kItems : 1];
-  uint16_t rv0[kItems > 0 ? kItems : 1], rv1[kItems > 0 ? kItems : 1];
+  // (every load unconditional, from a valid row, so that the waits for
+  // them come after the K / V stream is issued and count only these)
+  constexpr int kI = kItems > 0 ? kItems : 1;
+  uint16_t ra[kI], rb[kI], rv0[kI], rv1[kI], wa[kI], wb[kI];
+  float freq = 0.0f;
   if constexpr (FUSED) {
+    freq = f.tab.inv_freq[lane];
 #pragma unroll
     for (int u = 0; u < kItems; u++) {
       const int it = wave + u * kDecWaves;
-      if (it < n_items) {
-        const uint16_t* src;
-        if (it < RT) {
-          const int rg = r0 + it, j = rg / tn, i = rg - j * tn;
-          src = p.q + (static_cast<int64_t>(i) * p.Hq + kvh * rep + j) * kD;
-        } else {
-          const int64_t row = static_cast<int64_t>(t_lo + it - RT) * p.Hkv + kvh;
-          src = f.k_new + row * kD;
-          rv0[u] = f.v_new[row * kD + lane];
-          rv1[u] = f.v_new[row * kD + lane + 64];
-        }
-        ra[u] = bf2f(src[lane]);
-        rb[u] = bf2f(src[lane + 64]);
-      }
+      const bool is_q = it < RT;
+      const int rg = r0 + min(it, RT - 1), j = rg / tn, i = rg - j * tn;
+      const int64_t krow = static_cast<int64_t>(min(max(t_lo + it - RT, 0), p.M - 1)) * p.Hkv + kvh;
+      const uint16_t* src = is_q ? p.q + (static_cast<int64_t>(i) * p.Hq + kvh * rep + j) * kD : f.k_new + krow * kD;
+      const uint16_t* nw = is_q ? f.q_norm : f.k_norm;
+      ra[u] = src[lane];
+      rb[u] = src[lane + 64];
+      rv0[u] = f.v_new[krow * kD + lane];
+      rv1[u] = f.v_new[krow * kD + lane + 64];
+      wa[u] = nw[lane];
+      wb[u] = nw[lane + 64];
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
   // ---- issue loads: q fragments, K fragments, V rows ----
   uint4 qa[4];
@@ -212,11 +221,24 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) kb[t][ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
   }
-  uint32_t vr[kDecWaveKeys];
+  // V, wide (RMAX <= 8): lane holds dims 8 vc .. 8 vc + 7 of keys vq + 4 j,
+  // j < 8 (one 16-byte load per key; an instruction reads 4 whole key rows);
+  // narrow: lane holds dims 2 lane, 2 lane + 1 of all 32 keys
+  const int vc = lane & 15, vq = lane >> 4;
+  uint4 vw[kWideV ? 8 : 1];
+  uint32_t vr[kWideV ? 1 : kDecWaveKeys];
+  if constexpr (kWideV) {
 #pragma unroll
-  for (int k = 0; k < kDecWaveKeys; k++) {
-    const int key = max(min(c0 + k, L - 1), 0);
-    vr[k] = *reinterpret_cast<const uint32_t*>(p.v + hbase + static_cast<int64_t>(key) * kD + 2 * lane);
+    for (int j = 0; j < 8; j++) {
+      const int key = max(min(c0 + vq + 4 * j, L - 1), 0);
+      vw[j] = *reinterpret_cast<const uint4*>(p.v + hbase + static_cast<int64_t>(key) * kD + 8 * vc);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kDecWaveKeys; k++) {
+      const int key = max(min(c0 + k, L - 1), 0);
+      vr[k] = *reinterpret_cast<const uint32_t*>(p.v + hbase + static_cast<int64_t>(key) * kD + 2 * lane);
+    }
   }
   if constexpr (FUSED) {
     // ---- fused prologue, part 2: norm + rope into LDS (and the caches) ----
@@ -227,8 +249,8 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
         const bool is_q = it < RT;
         const int t = is_q ? (r0 + it) % tn : t_lo + it - RT;
         uint16_t o1, o2;
-        qk_norm_rope_lane(ra[u], rb[u], is_q ? f.q_norm : f.k_norm, f.tab.inv_freq[lane],
-                          static_cast<float>(offset + t), f.eps, lane, o1, o2);
+        qk_norm_rope_lane(bf2f(ra[u]), bf2f(rb[u]), bf2f(wa[u]), bf2f(wb[u]), freq, static_cast<float>(offset + t),
+                          f.eps, o1, o2);
         if (is_q) {
           qs[it][lane] = o1;
           qs[it][lane + 64] = o2;
@@ -265,10 +287,18 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
       }
     }
     if (t_hi > t_lo) {
+      if constexpr (kWideV) {
 #pragma unroll
-      for (int k = 0; k < kDecWaveKeys; k++) {
-        const int tt = c0 + k - offset;
-        if (tt >= 0 && tt < p.M) vr[k] = *reinterpret_cast<const uint32_t*>(&vn[tt][2 * lane]);
+        for (int j = 0; j < 8; j++) {
+          const int tt = c0 + vq + 4 * j - offset;
+          if (tt >= 0 && tt < p.M) vw[j] = *reinterpret_cast<const uint4*>(&vn[tt][8 * vc]);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < kDecWaveKeys; k++) {
+          const int tt = c0 + k - offset;
+          if (tt >= 0 && tt < p.M) vr[k] = *reinterpret_cast<const uint32_t*>(&vn[tt][2 * lane]);
+        }
       }
     }
   }
@@ -309,22 +339,65 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
     }
   }
   __syncthreads();
-  // ---- PV: lane = dims 2 lane, 2 lane + 1 over the wave's 32 keys ----
-  float acc[RMAX][2];
+  // ---- PV ----
+  // wide: lane sums its 8 keys for every (row, dim 8 vc + d), then the four
+  // key quarters (lane bits 4, 5) are added by two swap-and-add butterflies
+  // (v_permlane32_swap: X' = [X.lo, Y.lo], Y' = [X.hi, Y.hi];
+  // v_permlane16_swap: X' = [X.r0, Y.r0, X.r2, Y.r2], Y' = [X.r1, Y.r1, X.r3,
+  // Y.r3] in 16-lane rows), which leave lane group vq with rows 4 i + vq;
+  // narrow: lane = dims 2 lane, 2 lane + 1 over the wave's 32 keys
+  float acc[RMAX][kWideV ? 8 : 2];
 #pragma unroll
-  for (int r = 0; r < RMAX; r++) acc[r][0] = acc[r][1] = 0.0f;
+  for (int r = 0; r < RMAX; r++)
 #pragma unroll
-  for (int k = 0; k < kDecWaveKeys; k++) {
-    const float v0 = bf2f(vr[k] & 0xffffu), v1 = bf2f(vr[k] >> 16);
+    for (int d = 0; d < (kWideV ? 8 : 2); d++) acc[r][d] = 0.0f;
+  if constexpr (kWideV) {
 #pragma unroll
-    for (int r4 = 0; r4 < RMAX; r4 += 4) {
-      if (r4 >= RT) break;
-      const float4 pv = *reinterpret_cast<const float4*>(&ps[wave][k][r4]);
-      const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
+    for (int j = 0; j < 8; j++) {
+      const uint32_t w4[4] = {vw[j].x, vw[j].y, vw[j].z, vw[j].w};
+      float v[8];
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        acc[r4 + q][0] += pr[q] * v0;
-        acc[r4 + q][1] += pr[q] * v1;
+      for (int e = 0; e < 4; e++) {
+        v[2 * e] = bf2f(w4[e] & 0xffffu);
+        v[2 * e + 1] = bf2f(w4[e] >> 16);
+      }
+#pragma unroll
+      for (int r4 = 0; r4 < RMAX; r4 += 4) {
+        const float4 pv = *reinterpret_cast<const float4*>(&ps[wave][vq + 4 * j][r4]);
+        const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+          for (int d = 0; d < 8; d++) acc[r4 + q][d] += pr[q] * v[d];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RMAX / 4; i++)
+#pragma unroll
+      for (int d = 0; d < 8; d++) {
+        const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[4 * i][d]),
+                                                        __float_as_uint(acc[4 * i + 2][d]), false, false);
+        const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[4 * i + 1][d]),
+                                                        __float_as_uint(acc[4 * i + 3][d]), false, false);
+        const float r1 = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+        const float r2 = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+        const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(r1), __float_as_uint(r2), false, false);
+        acc[i][d] = __uint_as_float(c[0]) + __uint_as_float(c[1]);  // row 4 i + vq, dim 8 vc + d
+      }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kDecWaveKeys; k++) {
+      const float v0 = bf2f(vr[k] & 0xffffu), v1 = bf2f(vr[k] >> 16);
+#pragma unroll
+      for (int r4 = 0; r4 < RMAX; r4 += 4) {
+        if (r4 >= RT) break;
+        const float4 pv = *reinterpret_cast<const float4*>(&ps[wave][k][r4]);
+        const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          acc[r4 + q][0] += pr[q] * v0;
+          acc[r4 + q][1] += pr[q] * v1;
+        }
       }
     }
   }
@@ -333,10 +406,19 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   for (int h0 = 0; h0 < RMAX; h0 += kMergeRows) {
     if (h0 >= RT) break;
     if (h0 > 0) __syncthreads();  // the previous pass has read os
+    if constexpr (kWideV) {  // RMAX <= kMergeRows: one pass
 #pragma unroll
-    for (int r = 0; r < kMergeRows && r < RMAX; r++) {
-      if (h0 + r >= RT) break;
-      *reinterpret_cast<float2*>(&os[wave][r][2 * lane]) = make_float2(acc[h0 + r][0], acc[h0 + r][1]);
+      for (int i = 0; i < RMAX / 4; i++) {
+        float* dst = &os[wave][4 * i + vq][8 * vc];
+        *reinterpret_cast<float4*>(dst) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < kMergeRows && r < RMAX; r++) {
+        if (h0 + r >= RT) break;
+        *reinterpret_cast<float2*>(&os[wave][r][2 * lane]) = make_float2(acc[h0 + r][0], acc[h0 + r][1]);
+      }
     }
     __syncthreads();
     const int nr = min(kMergeRows, RT - h0);
@@ -364,14 +446,9 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
       // (h * M + token) * ns + split
       const int64_t base = (static_cast<int64_t>(kvh) * R + r0 + r) * p.ns + split;
       float* po = p.part_o + base * kD + d4 * 4;
-      store_agent(po, o.x);
-      store_agent(po + 1, o.y);
-      store_agent(po + 2, o.z);
-      store_agent(po + 3, o.w);
-      if (d4 == 0) {
-        store_agent(p.part_ml + base * 2, m);
-        store_agent(p.part_ml + base * 2 + 1, l);
-      }
+      store_agent2(po, o.x, o.y);
+      store_agent2(po + 2, o.z, o.w);
+      if (d4 == 0) store_agent2(p.part_ml + base * 2, m, l);
     }
   }
   // ---- the last of the ns workgroups of this (kv head, row tile) merges ----

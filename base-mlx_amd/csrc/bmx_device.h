@@ -43,18 +43,19 @@ __device__ __forceinline__ T wave_sum_xor(T v, int width) {
   return v;
 }
 
-// Per-head RMSNorm (weight nw, fp32 inside, bf16 result) followed by
-// rotate-half RoPE at angle pos * freq, for one head row of 128 held by a
-// whole wave: lane holds dims lane and lane + 64 (a, b on entry; the rotated
-// bf16 pair on return).  QK-norm and rope of Qwen3::forward_internal
-// (crates/base-mlx-core/src/model/qwen3.rs:392-413).  Every kernel that
-// norms and rotates q or k calls this, so they agree bit for bit.
-__device__ __forceinline__ void qk_norm_rope_lane(float a, float b, const uint16_t* nw, float freq, float pos,
-                                                  float eps, int lane, uint16_t& o1, uint16_t& o2) {
+// Per-head RMSNorm (fp32 inside, bf16 result) followed by rotate-half RoPE
+// at angle pos * freq, for one head row of 128 held by a whole wave: lane
+// holds dims lane and lane + 64 (values a, b and norm weights wa, wb on
+// entry; the rotated bf16 pair on return).  QK-norm and rope of
+// Qwen3::forward_internal (crates/base-mlx-core/src/model/qwen3.rs:392-413).
+// Every kernel that norms and rotates q or k calls this, so they agree bit
+// for bit.
+__device__ __forceinline__ void qk_norm_rope_lane(float a, float b, float wa, float wb, float freq, float pos,
+                                                  float eps, uint16_t& o1, uint16_t& o2) {
   const float ss = wave_sum_xor(a * a + b * b, 64);
   const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
-  const float na = bf2f(f2bf(bf2f(nw[lane]) * round_bf(a * inv)));
-  const float nb = bf2f(f2bf(bf2f(nw[lane + 64]) * round_bf(b * inv)));
+  const float na = bf2f(f2bf(wa * round_bf(a * inv)));
+  const float nb = bf2f(f2bf(wb * round_bf(b * inv)));
   const float ang = pos * freq;
   const float c = cosf(ang), s = sinf(ang);
   o1 = f2bf(na * c - nb * s);

@@ -126,7 +126,8 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kv_kernel(const QkvRopeParam
                              : p.k + (static_cast<int64_t>(t) * p.Hkv + hk) * 128;
   const uint16_t* nw = is_q ? p.q_norm : p.k_norm;
   uint16_t o1, o2;
-  qk_norm_rope_lane(bf2f(src[lane]), bf2f(src[lane + 64]), nw, p.tab.inv_freq[lane], pos, p.eps, lane, o1, o2);
+  qk_norm_rope_lane(bf2f(src[lane]), bf2f(src[lane + 64]), bf2f(nw[lane]), bf2f(nw[lane + 64]), p.tab.inv_freq[lane],
+                    pos, p.eps, o1, o2);
   if (is_q) {
     uint16_t* dst = p.q_out + (static_cast<int64_t>(h) * p.M + t) * 128;
     dst[lane] = o1;
