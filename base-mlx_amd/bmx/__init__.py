@@ -224,6 +224,25 @@ def qk_norm_rope_kv_attention(q, k, v, q_norm, k_norm, k_cache, v_cache, offset,
     return out
 
 
+def gather_qmm(x, w, scales, biases, rhs_indices, x_bcast=1, out=None, stream=None):
+    """mlx_ext::gather_qmm (transpose=true, gs 64, 4 bits, lhs_indices None):
+    x [R / x_bcast, M, K] bf16, w [E, N, K/8] uint32 (int32 storage), scales /
+    biases [E, N, K/64] bf16, rhs_indices [R] int32/uint32 on the device ->
+    [R, M, N] bf16; route r uses x block r // x_bcast and expert rhs[r]."""
+    torch = _torch()
+    _require_cuda(x, w, scales, biases, rhs_indices)
+    E, N = w.shape[0], w.shape[1]
+    M, K = x.shape[-2], x.shape[-1]
+    R = rhs_indices.numel()
+    if x.numel() != (R // x_bcast) * M * K or R % x_bcast:
+        raise BmxError(BMX_E_SHAPE, f"x holds {x.numel()} values; {R // x_bcast} blocks of [{M}, {K}] expected")
+    if out is None:
+        out = torch.empty(R, M, N, dtype=torch.bfloat16, device=x.device)
+    call("bmx_gather_qmm", _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), _ptr(rhs_indices), _ptr(out), R, x_bcast,
+         E, M, N, K, 64, 4, _stream(stream))
+    return out
+
+
 def argmax_rows(x, stream=None):
     torch = _torch()
     _require_cuda(x)

@@ -43,6 +43,19 @@ __device__ __forceinline__ T wave_sum_xor(T v, int width) {
   return v;
 }
 
+// Dot of one packed word (8 nibbles q_0..q_7) with its pair-permuted x
+// (permute_pairs: (x_e, x_{e+4}) per word), +128 bias on every q:
+// (w >> 4j & 0x000F000F) | 0x43004300 is the bf16 pair (128 + q_j, 128 +
+// q_{j+4}), fed straight to v_dot2c_f32_bf16.
+__device__ __forceinline__ float word_dot(uint32_t w, uint4 xp, float acc) {
+  const uint32_t magic = 0x43004300u;
+  acc = dot2_bf16((w & 0x000f000fu) | magic, xp.x, acc);
+  acc = dot2_bf16(((w >> 4) & 0x000f000fu) | magic, xp.y, acc);
+  acc = dot2_bf16(((w >> 8) & 0x000f000fu) | magic, xp.z, acc);
+  acc = dot2_bf16(((w >> 12) & 0x000f000fu) | magic, xp.w, acc);
+  return acc;
+}
+
 // Per-head RMSNorm (fp32 inside, bf16 result) followed by rotate-half RoPE
 // at angle pos * freq, for one head row of 128 held by a whole wave: lane
 // holds dims lane and lane + 64 (values a, b and norm weights wa, wb on

@@ -42,16 +42,6 @@ constexpr int kThreads = 256;
 constexpr int kChunkBytes = 80;  // 64 data bytes + 16 pad per 32 x values
 constexpr int kLdsBudget = 40 * 1024;
 
-// Dot of one packed word (8 nibbles) with its permuted x pairs, +128 bias.
-__device__ __forceinline__ float word_dot(uint32_t w, uint4 xp, float acc) {
-  const uint32_t magic = 0x43004300u;
-  acc = dot2_bf16((w & 0x000f000fu) | magic, xp.x, acc);
-  acc = dot2_bf16(((w >> 4) & 0x000f000fu) | magic, xp.y, acc);
-  acc = dot2_bf16(((w >> 8) & 0x000f000fu) | magic, xp.z, acc);
-  acc = dot2_bf16(((w >> 12) & 0x000f000fu) | magic, xp.w, acc);
-  return acc;
-}
-
 template <int MT, int S, int EPI>
 __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
   extern __shared__ __align__(16) unsigned char smem[];

@@ -124,6 +124,63 @@ def time_qmm(bmx, torch, M, N, K):
     return us, nbytes, flops
 
 
+# Qwen3-30B-A3B-shaped routed experts: 128 experts, top-8, hidden 2048,
+# moe_intermediate 768 (gate|up concatenated: N = 1536)
+MOE_SHAPES = [("gate_up", 1536, 2048, 8), ("down", 2048, 768, 1)]
+
+
+def time_gather(bmx, torch, N, K, x_bcast, E=128, top_k=8, reps=200):
+    """Average duration (us) of one routed decode projection (one token, top_k
+    routes to distinct experts), graph-captured over rotating route sets; the
+    128 experts of each of 4 stacked copies (>= 1 GiB in all) keep the reads
+    HBM-cold."""
+    import numpy as np
+
+    per_expert = int(0.5625 * N * K)
+    copies = max(1, -(-(1 << 30) // (E * per_expert)))
+    ws = []
+    for c in range(copies):
+        ex = [bmx.init_qlinear(9000 + c * E + e, N, K) for e in range(E)]
+        ws.append(tuple(torch.stack([t[i] for t in ex]).contiguous() for i in range(3)))
+        del ex
+    rng = np.random.default_rng(5)
+    routes = [torch.from_numpy(rng.choice(E, top_k, replace=False).astype(np.int32)).cuda() for _ in range(reps)]
+    x = bmx.fill_normal_bf16(79, (top_k // x_bcast, 1, K))
+    y = torch.empty(top_k, 1, N, dtype=torch.bfloat16, device="cuda")
+    st = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        bmx.gather_qmm(x, *ws[0], routes[0], x_bcast, out=y)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=st):
+            for i in range(reps):
+                bmx.gather_qmm(x, *ws[i % copies], routes[i], x_bcast, out=y)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        g.replay()
+        e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / reps
+    nbytes = top_k * per_expert + 2 * (top_k // x_bcast) * K + 2 * top_k * N
+    del g, ws
+    torch.cuda.empty_cache()
+    return us, nbytes
+
+
+def moe_bench(bmx, torch):
+    out = []
+    for name, N, K, xb in MOE_SHAPES:
+        us, nb = time_gather(bmx, torch, N, K, xb)
+        gbs = nb / us / 1e3
+        out.append({"proj": name, "experts": 128, "top_k": 8, "N": N, "K": K, "us": round(us, 3),
+                    "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        log(f"gather_qmm {name} 8 of 128 experts ({N}, {K}): {us:.2f} us, {gbs:.0f} GB/s")
+    return out
+
+
 def qmm_sweep(bmx, torch):
     out = []
     for M in QMM_M:
@@ -252,6 +309,8 @@ def main():
                     help="also time the quantized GEMM at M = 5, 128, 512, 2048 (4B and 8B projection shapes)")
     ap.add_argument("--speculative", action="store_true",
                     help="also run 32B-target / 0.6B-draft greedy speculative decoding (M = 5 verify)")
+    ap.add_argument("--moe", action="store_true",
+                    help="also time gather_qmm on Qwen3-30B-A3B-shaped routed experts (decode, top-8 of 128)")
     ap.add_argument("--profile-roofline", action="store_true",
                     help="only run the roofline GEMV and a copy of known size (for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -325,6 +384,7 @@ def main():
 
     qmm = qmm_sweep(bmx, torch) if args.qmm_sweep else []
     spec = speculative_bench(bmx, torch) if args.speculative else None
+    moe = moe_bench(bmx, torch) if args.moe else []
 
     cpu = None
     if not args.no_cpu:
@@ -350,7 +410,7 @@ def main():
         "config": {"workload": "Qwen3-4B-shape 4-bit greedy decode, batch 1, after a 4096-token prefill",
                    "prompt_tokens": args.prompt, "kv_cache": [36, 2, 8, max(cap, 4352), 128],
                    "prefill_ms": round(prefill_s * 1000, 1), "qmv_sweep": sweep, "qmm_sweep": qmm,
-                   "speculative": spec},
+                   "speculative": spec, "gather_qmm": moe},
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -62,6 +62,23 @@ int bmx_qmatmul_affine(const bmx_bf16 *x, const uint32_t *w, const bmx_bf16 *sca
                        const bmx_bf16 *biases, bmx_bf16 *y, int64_t M, int64_t N, int64_t K,
                        int group_size, int bits, void *stream);
 
+/* Routed (MoE expert) quantized matmul: w [n_experts, N, K/8] u32, scales /
+ * biases [n_experts, N, K/64] bf16; for route r < n_routes,
+ *   out[r] [M, N] = x[r / x_bcast] [M, K] . W[rhs_indices[r]]^T
+ * with quantized_matmul's numerics (fp32 accumulate, bf16 out).  x holds
+ * n_routes / x_bcast row blocks of [M, K] (x_bcast = top_k when every slot
+ * of a token shares its x, 1 for one block per route).  rhs_indices is a
+ * device array of n_routes uint32; ids >= n_experts are clamped to
+ * n_experts - 1.  M <= 8, K % 64 == 0, n_routes <= 65535; x and w 16-byte
+ * aligned.
+ * Replaces: mlx_ext::gather_qmm(x, w, scales, biases, None, Some(indices),
+ *   transpose=true, gs, bits, sorted=false) (crates/base-mlx-core/src/
+ *   mlx_ext.rs:66-117) as called by QSwitchLinear::forward
+ *   (crates/base-mlx-core/src/model/granite.rs:74-88). */
+int bmx_gather_qmm(const bmx_bf16 *x, const uint32_t *w, const bmx_bf16 *scales, const bmx_bf16 *biases,
+                   const uint32_t *rhs_indices, bmx_bf16 *out, int n_routes, int x_bcast, int n_experts, int M,
+                   int N, int K, int group_size, int bits, void *stream);
+
 /* out[N,K] = scales * q + biases (fp32, rounded to bf16).
  * Replaces: mlx_rs::ops::dequantize(w, s, b, group_size, bits)
  *   (crates/base-mlx-core/src/model/qwen3.rs:75). */

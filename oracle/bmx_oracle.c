@@ -327,6 +327,27 @@ int orc_qlinear(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
   return orc_qmm_dequant(x, wq, s, b, y, M, N, K, gs, bits);
 }
 
+/* gather_qmm (mlx_ext.rs:66-117) as QSwitchLinear::forward calls it
+ * (granite.rs:74-88): route r multiplies x block r / x_bcast by expert
+ * rhs[r] of the stacked [E, N, K/8] weights, with quantized_matmul's
+ * numerics for each route (M <= 8 rows: the GEMV group decomposition).
+ * Expert ids >= E are clamped to E - 1, as the HIP library does. */
+int orc_gather_qmm(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
+                   const uint16_t *b, const uint32_t *rhs, uint16_t *y,
+                   int64_t R, int64_t x_bcast, int64_t E, int64_t M, int64_t N,
+                   int64_t K, int gs, int bits) {
+  if (bits != 4) return ORC_E_UNSUPPORTED;
+  if (gs != 64 || K % 64 || E <= 0 || x_bcast <= 0 || M <= 0 || M > 8) return ORC_E_SHAPE;
+  const int64_t G = K / 64;
+  for (int64_t r = 0; r < R; r++) {
+    const int64_t e = rhs[r] < (uint32_t)E ? (int64_t)rhs[r] : E - 1;
+    int rc = orc_qmatmul(x + (r / x_bcast) * M * K, wq + e * N * (K / 8), s + e * N * G, b + e * N * G,
+                         y + r * M * N, M, N, K, gs, bits);
+    if (rc) return rc;
+  }
+  return ORC_OK;
+}
+
 /* Same product evaluated in float64 on the dequantized weights
  * (s*q + b exact in double); the high-precision yardstick for tests. */
 int orc_qmatmul_f64(const uint16_t *x, const uint32_t *wq, const uint16_t *s,

@@ -71,6 +71,10 @@ int orc_qmm_dequant(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
 int orc_qlinear(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
                 const uint16_t *b, uint16_t *y, int64_t M, int64_t N, int64_t K,
                 int gs, int bits);
+int orc_gather_qmm(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
+                   const uint16_t *b, const uint32_t *rhs, uint16_t *y,
+                   int64_t R, int64_t x_bcast, int64_t E, int64_t M, int64_t N,
+                   int64_t K, int gs, int bits);
 int orc_qmatmul_f64(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
                     const uint16_t *b, double *y, int64_t M, int64_t N,
                     int64_t K, int gs, int bits);

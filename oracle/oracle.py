@@ -38,6 +38,7 @@ _SIGS = {
     "orc_dequantize": (INT, [P, P, P, I64, I64, INT, INT, P]),
     "orc_dequant_gather": (INT, [P, I64, I64, P, P, P, I64, INT, INT, P]),
     "orc_qmatmul": (INT, [P, P, P, P, P, I64, I64, I64, INT, INT]),
+    "orc_gather_qmm": (INT, [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, INT, INT]),
     "orc_qmatmul_f64": (INT, [P, P, P, P, P, I64, I64, I64, INT, INT]),
     "orc_qmm_dequant": (INT, [P, P, P, P, P, I64, I64, I64, INT, INT]),
     "orc_qlinear": (INT, [P, P, P, P, P, I64, I64, I64, INT, INT]),
@@ -169,6 +170,22 @@ def qmatmul(x, wq, s, b, gs=64, bits=4):
     N = wq.shape[0]
     y = np.empty((M, N), np.uint16)
     _chk(lib().orc_qmatmul(_p(x), _p(wq), _p(s), _p(b), _p(y), M, N, K, gs, bits))
+    return y
+
+
+def gather_qmm(x, wq, s, b, rhs, x_bcast=1, gs=64, bits=4):
+    """Routed qmm: x [R / x_bcast, M, K], wq [E, N, K/8], rhs [R] -> [R, M, N]."""
+    x = np.ascontiguousarray(x, np.uint16)
+    wq = np.ascontiguousarray(wq, np.uint32)
+    s = np.ascontiguousarray(s, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    rhs = np.ascontiguousarray(rhs, np.uint32)
+    E, N = wq.shape[0], wq.shape[1]
+    M, K = x.shape[-2], x.shape[-1]
+    R = rhs.size
+    assert x.size == (R // x_bcast) * M * K
+    y = np.empty((R, M, N), np.uint16)
+    _chk(lib().orc_gather_qmm(_p(x), _p(wq), _p(s), _p(b), _p(rhs), _p(y), R, x_bcast, E, M, N, K, gs, bits))
     return y
 
 

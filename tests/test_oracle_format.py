@@ -194,3 +194,43 @@ def test_qmm_dequant_vs_float64_on_dequantized_weights(orc, M, N, K):
     # dispatch: qlinear is qmatmul up to 8 rows and qmm_dequant beyond
     np.testing.assert_array_equal(orc.qlinear(x, wq, s, b), orc.qmm_dequant(x, wq, s, b))
     np.testing.assert_array_equal(orc.qlinear(x[:8], wq, s, b), orc.qmatmul(x[:8], wq, s, b))
+
+
+@pytest.mark.parametrize("M,x_bcast", [(1, 4), (3, 1)])
+def test_gather_qmm_vs_float64(orc, M, x_bcast):
+    """Routed qmm: route r is x block r // x_bcast times expert rhs[r]; numpy
+    float64 on the exact dequantized experts is the yardstick.  A route
+    reading the wrong expert or the wrong x block (r % blocks instead of
+    r // x_bcast) fails the per-element bound."""
+    E, N, K, R = 5, 40, 256, 8
+    ex = [orc.init_qlinear(700 + e, N, K) for e in range(E)]
+    wq = np.stack([t[0] for t in ex])
+    s = np.stack([t[1] for t in ex])
+    b = np.stack([t[2] for t in ex])
+    rhs = np.array([3, 0, 3, 4, 1, 1, 2, 0], np.uint32)
+    blocks = R // x_bcast
+    x = orc.fill_normal_bf16(800 + M, blocks * M * K).reshape(blocks, M, K)
+    y = bf16_to_f32(orc.gather_qmm(x, wq, s, b, rhs, x_bcast))
+    nib = ((wq[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(E, N, K)
+    Wx = np.repeat(bf16_to_f32(s), 64, 2).astype(np.float64) * nib + np.repeat(bf16_to_f32(b), 64, 2)
+    xf = bf16_to_f32(x).astype(np.float64)
+
+    def ref_for(block_of):
+        return np.stack([xf[block_of(r)] @ Wx[rhs[r]].T for r in range(R)])
+
+    ref = ref_for(lambda r: r // x_bcast)
+    tol = np.abs(ref) * 2 ** -8 + 1e-5 * np.sqrt(K) * np.max(np.abs(ref))
+    assert np.all(np.abs(y - ref) <= tol)
+    if x_bcast > 1:
+        wrong = ref_for(lambda r: r % blocks)
+        assert not np.all(np.abs(y - wrong) <= tol)
+    # each route is exactly quantized_matmul on its expert
+    r = 2
+    np.testing.assert_array_equal(orc.gather_qmm(x, wq, s, b, rhs, x_bcast)[r],
+                                  orc.qmatmul(x[r // x_bcast], wq[rhs[r]], s[rhs[r]], b[rhs[r]]))
+    # ids past the last expert are clamped to it
+    hi = rhs.copy()
+    hi[5] = 77
+    clamp = rhs.copy()
+    clamp[5] = E - 1
+    np.testing.assert_array_equal(orc.gather_qmm(x, wq, s, b, hi, x_bcast), orc.gather_qmm(x, wq, s, b, clamp, x_bcast))
