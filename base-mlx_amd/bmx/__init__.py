@@ -16,6 +16,7 @@ Errors surface as :class:`BmxError` (the reference maps them to
 from __future__ import annotations
 
 import ctypes
+import os
 
 from ._lib import (  # noqa: F401
     BMX_E_ALIGN,
@@ -283,6 +284,13 @@ def qwen3_config(hidden, inter, layers, n_heads, n_kv_heads, head_dim=128, vocab
     return Qwen3Config(hidden, inter, layers, n_heads, n_kv_heads, head_dim, vocab, tied, 64, 4, eps, rope_theta)
 
 
+def qwen3_config_from_json(path):
+    """ModelConfig::from_path: a config.json -> Qwen3Config (host only)."""
+    cfg = Qwen3Config()
+    call("bmx_qwen3_config_from_json", os.fsencode(path), ctypes.byref(cfg))
+    return cfg
+
+
 # Qwen3-shaped configurations of the benchmark workloads
 QWEN3_0_6B = dict(hidden=1024, inter=3072, layers=28, n_heads=16, n_kv_heads=8)
 QWEN3_4B = dict(hidden=2560, inter=9728, layers=36, n_heads=32, n_kv_heads=8)
@@ -370,6 +378,17 @@ class Qwen3:
              ctypes.byref(h))
         self.h = h
         self.max_tokens = max_tokens
+
+    @classmethod
+    def load(cls, path, max_tokens=256):
+        """Qwen3::load: an MLX checkpoint directory (config.json + *.safetensors)."""
+        self = cls.__new__(cls)
+        self.cfg = qwen3_config_from_json(os.path.join(path, "config.json"))
+        h = ctypes.c_void_p()
+        call("bmx_qwen3_load", os.fsencode(path), max_tokens, ctypes.byref(h))
+        self.h = h
+        self.max_tokens = max_tokens
+        return self
 
     def close(self):
         if self.h:

@@ -70,6 +70,8 @@ SIGNATURES = {
     "bmx_attention_gqa": (c_int, [c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_int, c_f, c_p,
                                   ctypes.c_size_t, c_p]),
     "bmx_attention_workspace_bytes": (ctypes.c_size_t, [c_int, c_int]),
+    "bmx_qwen3_config_from_json": (c_int, [ctypes.c_char_p, c_p]),
+    "bmx_qwen3_load": (c_int, [ctypes.c_char_p, c_int, c_p]),
     "bmx_gather_qmm": (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                c_int, c_p]),
     "bmx_qk_norm_rope_kv_attention": (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int,

@@ -81,7 +81,7 @@ extern "C" int bmx_qmatmul_affine(const bmx_bf16* x, const uint32_t* w, const bm
   if (M == 0) return BMX_OK;
   if (M > 8) {
     if (M > INT32_MAX) return set_error(BMX_E_SHAPE, "qmatmul: M too large");
-    return launch_qmm(x, w, scales, biases, y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
+    return launch_qmm(x, w, scales, biases, y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), nullptr, 0,
                       as_stream(stream));
   }
   QmvParams p{};

@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+#include <vector>
+
 #include "bmx.h"
 
 namespace bmx {
@@ -72,8 +75,13 @@ int try_launch_qmvx(QmvParams p, QmvEpilogue epi, hipStream_t stream);
 int qmv_blocks(const QmvParams& p, QmvEpilogue epi);
 
 // ---- other kernels (one launch each, errors recorded) --------------------
+// Dequantizing MFMA GEMM (M > 8).  Split-K partials go to ws when it holds
+// qmm_workspace_floats of the shape, else to a buffer of the (device,
+// stream) pair that the library keeps.
 int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M,
-               int N, int K, hipStream_t stream);
+               int N, int K, float* ws, size_t ws_floats, hipStream_t stream);
+// Split-K partial floats the GEMM needs for any M up to max_M (0 if none).
+size_t qmm_workspace_floats(int max_M, int N, int K);
 int launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t rows, int dim, float eps,
                     hipStream_t stream);
 struct RopeTable {
@@ -84,6 +92,19 @@ int launch_qk_norm_rope_kv(const uint16_t* q, const uint16_t* k, const uint16_t*
                            const uint16_t* k_norm, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int M,
                            int Hq, int Hkv, int D, int cap, int offset, const int* offset_dev, float eps,
                            const RopeTable& tab, hipStream_t stream);
+// A weight tensor of a bmx_qwen3 under its MLX checkpoint name: rows x cols
+// of uint32 (packed 4-bit weights) or bf16 (scales, biases, norm weights).
+struct WeightSlot {
+  std::string name;
+  void* dev;
+  int rows, cols;
+  bool u32;
+};
+// Allocates a Qwen3 of shape cfg (weights uninitialised) with its forward
+// workspace; every weight tensor, named as in an MLX checkpoint.
+int qwen3_alloc(const bmx_qwen3_config* cfg, int max_tokens, bmx_qwen3** out);
+std::vector<WeightSlot> qwen3_weight_slots(bmx_qwen3* m);
+
 // Returned by a launcher whose kernel does not fit the call (nothing launched).
 constexpr int kNoFit = -100;
 // Attention workspace (floats): arrival counters, then split partials; the

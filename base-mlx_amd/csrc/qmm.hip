@@ -21,6 +21,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <map>
 #include <mutex>
 
 #include "bmx_device.h"
@@ -180,50 +181,82 @@ __global__ void __launch_bounds__(256) qmm_reduce_kernel(const float* part, uint
   }
 }
 
-// Split-K partials: one device buffer per process, grown on demand (the
-// GEMM path is never inside a captured graph).
+// Split-K partials for callers that bring no workspace: one device buffer
+// per (device, stream), grown on demand (the GEMM path is never inside a
+// captured graph).  Work on one stream runs in order, so its launches may
+// share a buffer; work on different streams never shares one.
+struct PartBuf {
+  float* p = nullptr;
+  size_t floats = 0;
+};
 std::mutex g_part_mu;
-float* g_part = nullptr;
-size_t g_part_floats = 0;
+std::map<std::pair<int, hipStream_t>, PartBuf> g_parts;
 
-int part_buffer(size_t floats, float** out) {
+int part_buffer(size_t floats, hipStream_t stream, float** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(BMX_E_ARG, "qmm: no current HIP device");
   std::lock_guard<std::mutex> lock(g_part_mu);
-  if (floats > g_part_floats) {
-    if (g_part) {
-      // earlier launches may still read the old buffer
-      if (hipDeviceSynchronize() != hipSuccess) return set_error(BMX_E_ALLOC, "qmm: device sync failed");
-      (void)hipFree(g_part);
+  PartBuf& b = g_parts[{dev, stream}];
+  if (floats > b.floats) {
+    if (b.p) {
+      // earlier launches on this stream may still read the old buffer
+      if (hipStreamSynchronize(stream) != hipSuccess) return set_error(BMX_E_ALLOC, "qmm: stream sync failed");
+      (void)hipFree(b.p);
     }
-    g_part = nullptr;
-    g_part_floats = 0;
-    if (hipMalloc(&g_part, floats * sizeof(float)) != hipSuccess)
+    b.p = nullptr;
+    b.floats = 0;
+    if (hipMalloc(&b.p, floats * sizeof(float)) != hipSuccess)
       return set_error(BMX_E_ALLOC, "qmm: no memory for %zu split-K partials", floats);
-    g_part_floats = floats;
+    b.floats = floats;
   }
-  *out = g_part;
+  *out = b.p;
   return BMX_OK;
 }
 
-}  // namespace
-
-int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M, int N,
-               int K, hipStream_t stream) {
-  if (M <= 0) return BMX_OK;
-  if (K % 64 || N <= 0) return set_error(BMX_E_SHAPE, "qmm: N=%d K=%d", N, K);
-  if (!aligned(x, 16) || !aligned(w, 16)) return set_error(BMX_E_ALIGN, "qmm: x and W must be 16-byte aligned");
-  if ((M + QBM - 1) / QBM > 65535) return set_error(BMX_E_SHAPE, "qmm: M=%d too large", M);
+// K splits of an M x N x K product: split while the tiles leave most of the
+// device idle (splits of at least 8 groups, a multiple of 8 groups each).
+void qmm_split(int M, int N, int K, int* splits_out, int* gps_out) {
   const int G = K / 64;
   const int tiles = ((N + QBN - 1) / QBN) * ((M + QBM - 1) / QBM);
-  // split K while the tiles leave most of the device idle (splits of at
-  // least 8 groups, a multiple of 8 groups each)
   int splits = 1;
   while (tiles * splits * 2 <= 512 && G / (splits * 2) >= 8) splits *= 2;
   int gps = (G + splits - 1) / splits;
   if (splits > 1) gps = (gps + 7) / 8 * 8;
-  splits = (G + gps - 1) / gps;
+  *splits_out = (G + gps - 1) / gps;
+  *gps_out = gps;
+}
+
+}  // namespace
+
+size_t qmm_workspace_floats(int max_M, int N, int K) {
+  size_t need = 0;
+  // the split count depends on M only through the row-tile count
+  for (int t = 1; t <= (max_M + QBM - 1) / QBM; t++) {
+    const int M = std::min(t * QBM, max_M);
+    int splits, gps;
+    qmm_split(M, N, K, &splits, &gps);
+    if (splits > 1) need = std::max(need, static_cast<size_t>(splits) * M * N);
+  }
+  return need;
+}
+
+int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M, int N,
+               int K, float* ws, size_t ws_floats, hipStream_t stream) {
+  if (M <= 0) return BMX_OK;
+  if (K % 64 || N <= 0) return set_error(BMX_E_SHAPE, "qmm: N=%d K=%d", N, K);
+  if (!aligned(x, 16) || !aligned(w, 16)) return set_error(BMX_E_ALIGN, "qmm: x and W must be 16-byte aligned");
+  if ((M + QBM - 1) / QBM > 65535) return set_error(BMX_E_SHAPE, "qmm: M=%d too large", M);
+  int splits, gps;
+  qmm_split(M, N, K, &splits, &gps);
   QmmParams p{x, w, s, b, y, nullptr, M, N, K, gps};
-  if (splits > 1)
-    if (int rc = part_buffer(static_cast<size_t>(splits) * M * N, &p.part)) return rc;
+  if (splits > 1) {
+    const size_t need = static_cast<size_t>(splits) * M * N;
+    if (ws && ws_floats >= need) {
+      p.part = ws;
+    } else if (int rc = part_buffer(need, stream, &p.part)) {
+      return rc;
+    }
+  }
   if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(qmm_kernel), kQmmLds)) return rc;
   const dim3 grid((N + QBN - 1) / QBN, (M + QBM - 1) / QBM, splits);
   hipLaunchKernelGGL(qmm_kernel, grid, dim3(QT), kQmmLds, stream, p);

@@ -90,6 +90,8 @@ struct bmx_qwen3 {
            *o = nullptr, *g = nullptr, *u = nullptr, *a = nullptr, *logits1 = nullptr;
   float* attn_ws = nullptr;
   size_t attn_ws_floats = 0;
+  float* qmm_ws = nullptr;  // split-K partials of the prefill GEMMs (per model: models on
+  size_t qmm_ws_floats = 0;  // different streams never share one)
   int32_t* ids = nullptr;     // [max_tokens] token ids for the embedding gather
   uint32_t* tok_u = nullptr;  // [max(max_tokens, 64)] token staging
   uint32_t* next_tok = nullptr;  // argmax output of the decode step
@@ -129,9 +131,8 @@ int alloc_qlin(bmx_qwen3* m, QLin* q, int N, int K) {
   return dalloc_t(m, &q->b, static_cast<size_t>(N) * (K / 64));
 }
 
-int ones(bmx_qwen3* m, uint16_t** p, int n, hipStream_t st) {
-  if (int rc = dalloc_t(m, p, static_cast<size_t>(n))) return rc;
-  hipLaunchKernelGGL(fill_ones_kernel, dim3((n + 255) / 256), dim3(256), 0, st, *p, n);
+int fill_ones(uint16_t* p, int n, hipStream_t st) {
+  hipLaunchKernelGGL(fill_ones_kernel, dim3((n + 255) / 256), dim3(256), 0, st, p, n);
   return check_launch("fill_ones");
 }
 
@@ -193,9 +194,15 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       if (int rc = launch_qmv(p, QMV_STORE, st)) return rc;
     } else {
       if (int rc = launch_rms_norm(m->x, L.in_norm, m->h, M, H, cf.eps, st)) return rc;
-      if (int rc = launch_qmm(m->h, L.p[SLOT_Q].w, L.p[SLOT_Q].s, L.p[SLOT_Q].b, m->q, M, qd, H, st)) return rc;
-      if (int rc = launch_qmm(m->h, L.p[SLOT_K].w, L.p[SLOT_K].s, L.p[SLOT_K].b, m->k, M, kvd, H, st)) return rc;
-      if (int rc = launch_qmm(m->h, L.p[SLOT_V].w, L.p[SLOT_V].s, L.p[SLOT_V].b, m->v, M, kvd, H, st)) return rc;
+      if (int rc = launch_qmm(m->h, L.p[SLOT_Q].w, L.p[SLOT_Q].s, L.p[SLOT_Q].b, m->q, M, qd, H,
+                              m->qmm_ws, m->qmm_ws_floats, st))
+        return rc;
+      if (int rc = launch_qmm(m->h, L.p[SLOT_K].w, L.p[SLOT_K].s, L.p[SLOT_K].b, m->k, M, kvd, H,
+                              m->qmm_ws, m->qmm_ws_floats, st))
+        return rc;
+      if (int rc = launch_qmm(m->h, L.p[SLOT_V].w, L.p[SLOT_V].s, L.p[SLOT_V].b, m->v, M, kvd, H,
+                              m->qmm_ws, m->qmm_ws_floats, st))
+        return rc;
     }
     // ---- QK-norm, RoPE at the cache offset, KV write (qwen3.rs:392-489) and
     // SDPA over [0, offset + M) with the causal-offset mask (qwen3.rs:491-518):
@@ -226,7 +233,9 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       p.res = m->x;
       if (int rc = launch_qmv(p, QMV_RESIDUAL, st)) return rc;
     } else {
-      if (int rc = launch_qmm(m->att, L.p[SLOT_O].w, L.p[SLOT_O].s, L.p[SLOT_O].b, m->o, M, H, qd, st)) return rc;
+      if (int rc = launch_qmm(m->att, L.p[SLOT_O].w, L.p[SLOT_O].s, L.p[SLOT_O].b, m->o, M, H, qd,
+                              m->qmm_ws, m->qmm_ws_floats, st))
+        return rc;
       if (int rc = launch_add(m->x, m->o, m->x, static_cast<int64_t>(M) * H, st)) return rc;
     }
     // ---- mlp_block + residual (kernels.rs:55-78; qwen3.rs:523-541) ----
@@ -255,10 +264,16 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       if (int rc = launch_qmv(d, QMV_RESIDUAL, st)) return rc;
     } else {
       if (int rc = launch_rms_norm(m->x, L.post_norm, m->h, M, H, cf.eps, st)) return rc;
-      if (int rc = launch_qmm(m->h, L.p[SLOT_GATE].w, L.p[SLOT_GATE].s, L.p[SLOT_GATE].b, m->g, M, I, H, st)) return rc;
-      if (int rc = launch_qmm(m->h, L.p[SLOT_UP].w, L.p[SLOT_UP].s, L.p[SLOT_UP].b, m->u, M, I, H, st)) return rc;
+      if (int rc = launch_qmm(m->h, L.p[SLOT_GATE].w, L.p[SLOT_GATE].s, L.p[SLOT_GATE].b, m->g, M, I, H,
+                              m->qmm_ws, m->qmm_ws_floats, st))
+        return rc;
+      if (int rc = launch_qmm(m->h, L.p[SLOT_UP].w, L.p[SLOT_UP].s, L.p[SLOT_UP].b, m->u, M, I, H,
+                              m->qmm_ws, m->qmm_ws_floats, st))
+        return rc;
       if (int rc = launch_silu_mul(m->g, m->u, m->a, static_cast<int64_t>(M) * I, st)) return rc;
-      if (int rc = launch_qmm(m->a, L.p[SLOT_DOWN].w, L.p[SLOT_DOWN].s, L.p[SLOT_DOWN].b, m->o, M, H, I, st)) return rc;
+      if (int rc = launch_qmm(m->a, L.p[SLOT_DOWN].w, L.p[SLOT_DOWN].s, L.p[SLOT_DOWN].b, m->o, M, H, I,
+                              m->qmm_ws, m->qmm_ws_floats, st))
+        return rc;
       if (int rc = launch_add(m->x, m->o, m->x, static_cast<int64_t>(M) * H, st)) return rc;
     }
   }
@@ -268,7 +283,7 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
   const uint16_t* xin = all_logits ? m->x : m->x + static_cast<size_t>(M - 1) * H;
   if (rows <= 8) return qmv(m, xin, rows, head, logits, st, m->final_norm, rows == 1 ? amax : nullptr, amax_nblk);
   if (int rc = launch_rms_norm(xin, m->final_norm, m->h, rows, H, cf.eps, st)) return rc;
-  return launch_qmm(m->h, head.w, head.s, head.b, logits, rows, cf.vocab, H, st);
+  return launch_qmm(m->h, head.w, head.s, head.b, logits, rows, cf.vocab, H, m->qmm_ws, m->qmm_ws_floats, st);
 }
 
 // Decode step with token and position in device memory (step_io[0], [1]):
@@ -339,14 +354,18 @@ hipStream_t pick_stream(bmx_qwen3* m, void* stream) {
 // C ABI
 // ======================================================================
 
-extern "C" int bmx_qwen3_create_random(const bmx_qwen3_config* cfg, uint64_t seed, double sigma, int max_tokens,
-                                       bmx_qwen3** out) {
+namespace bmx {
+
+// Allocates a model of shape cfg with uninitialised weights and the forward
+// workspace for up to max_tokens tokens; the caller fills the weights.
+int qwen3_alloc(const bmx_qwen3_config* cfg, int max_tokens, bmx_qwen3** out) {
   if (!cfg || !out) return set_error(BMX_E_ARG, "qwen3_create: null pointer");
   *out = nullptr;
   if (cfg->bits != 4 || cfg->group_size != 64)
-    return set_error(BMX_E_UNSUPPORTED, "qwen3_create: only bits=4, group_size=64");
-  if (cfg->head_dim != 128 || cfg->n_heads % cfg->n_kv_heads || cfg->hidden % 64 || cfg->inter % 64 ||
-      (cfg->n_heads * cfg->head_dim) % 64 || cfg->layers <= 0 || cfg->vocab <= 0)
+    return set_error(BMX_E_UNSUPPORTED, "qwen3_create: only bits=4, group_size=64 (got %d, %d)", cfg->bits,
+                     cfg->group_size);
+  if (cfg->head_dim != 128 || cfg->n_kv_heads <= 0 || cfg->n_heads % cfg->n_kv_heads || cfg->hidden % 64 ||
+      cfg->inter % 64 || (cfg->n_heads * cfg->head_dim) % 64 || cfg->layers <= 0 || cfg->vocab <= 0)
     return set_error(BMX_E_SHAPE, "qwen3_create: unsupported shape");
   if (max_tokens < 1 || max_tokens > 65535) return set_error(BMX_E_ARG, "qwen3_create: max_tokens=%d", max_tokens);
   bmx_qwen3* m = new bmx_qwen3();
@@ -354,27 +373,19 @@ extern "C" int bmx_qwen3_create_random(const bmx_qwen3_config* cfg, uint64_t see
   m->max_tokens = max_tokens;
   m->rope = make_rope_table(cfg->head_dim, cfg->rope_theta);
   const int H = cfg->hidden, I = cfg->inter, qd = cfg->n_heads * cfg->head_dim, kvd = cfg->n_kv_heads * cfg->head_dim;
-  const float c = static_cast<float>(sigma / kIrwin4Std);
   hipStream_t st = nullptr;
   int rc = alloc_qlin(m, &m->embed, cfg->vocab, H);
-  if (!rc) rc = launch_init_qlinear(tensor_seed(seed, -1, 0), cfg->vocab, H, c, m->embed.w, m->embed.s, m->embed.b, st);
-  if (!rc && !cfg->tied) {
-    rc = alloc_qlin(m, &m->lm_head, cfg->vocab, H);
-    if (!rc) rc = launch_init_qlinear(tensor_seed(seed, -2, 0), cfg->vocab, H, c, m->lm_head.w, m->lm_head.s, m->lm_head.b, st);
-  }
-  if (!rc) rc = ones(m, &m->final_norm, H, st);
+  if (!rc && !cfg->tied) rc = alloc_qlin(m, &m->lm_head, cfg->vocab, H);
+  if (!rc) rc = dalloc_t(m, &m->final_norm, static_cast<size_t>(H));
   m->layers.resize(cfg->layers);
   const int dims[NSLOT][2] = {{qd, H}, {kvd, H}, {kvd, H}, {H, qd}, {I, H}, {I, H}, {H, I}};
   for (int l = 0; !rc && l < cfg->layers; l++) {
     Layer& L = m->layers[l];
-    for (int sl = 0; !rc && sl < NSLOT; sl++) {
-      rc = alloc_qlin(m, &L.p[sl], dims[sl][0], dims[sl][1]);
-      if (!rc) rc = launch_init_qlinear(tensor_seed(seed, l, sl), dims[sl][0], dims[sl][1], c, L.p[sl].w, L.p[sl].s, L.p[sl].b, st);
-    }
-    if (!rc) rc = ones(m, &L.in_norm, H, st);
-    if (!rc) rc = ones(m, &L.post_norm, H, st);
-    if (!rc) rc = ones(m, &L.q_norm, cfg->head_dim, st);
-    if (!rc) rc = ones(m, &L.k_norm, cfg->head_dim, st);
+    for (int sl = 0; !rc && sl < NSLOT; sl++) rc = alloc_qlin(m, &L.p[sl], dims[sl][0], dims[sl][1]);
+    if (!rc) rc = dalloc_t(m, &L.in_norm, static_cast<size_t>(H));
+    if (!rc) rc = dalloc_t(m, &L.post_norm, static_cast<size_t>(H));
+    if (!rc) rc = dalloc_t(m, &L.q_norm, static_cast<size_t>(cfg->head_dim));
+    if (!rc) rc = dalloc_t(m, &L.k_norm, static_cast<size_t>(cfg->head_dim));
   }
   // workspace
   const size_t T = static_cast<size_t>(max_tokens);
@@ -397,6 +408,10 @@ extern "C" int bmx_qwen3_create_random(const bmx_qwen3_config* cfg, uint64_t see
   if (!rc) rc = dalloc_t(m, &m->attn_ws, m->attn_ws_floats);
   // the arrival counters at its head start at zero (and every call leaves them so)
   if (!rc) rc = check_hip(hipMemsetAsync(m->attn_ws, 0, m->attn_ws_floats * sizeof(float), st), "hipMemsetAsync");
+  for (int sl = 0; sl < NSLOT; sl++)
+    m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmm_workspace_floats(max_tokens, dims[sl][0], dims[sl][1]));
+  m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmm_workspace_floats(max_tokens, cfg->vocab, H));
+  if (!rc && m->qmm_ws_floats) rc = dalloc_t(m, &m->qmm_ws, m->qmm_ws_floats);
   if (!rc) rc = dalloc_t(m, &m->ids, T);
   if (!rc) rc = dalloc_t(m, &m->tok_u, T < 64 ? 64 : T);
   if (!rc) rc = dalloc_t(m, &m->next_tok, 64);
@@ -408,6 +423,67 @@ extern "C" int bmx_qwen3_create_random(const bmx_qwen3_config* cfg, uint64_t see
   if (!rc) rc = check_hip(hipEventCreateWithFlags(&m->stage_done, hipEventDisableTiming), "event create");
   if (!rc) rc = check_hip(hipEventRecord(m->stage_done, st), "event record");
   if (!rc) rc = check_hip(hipStreamCreate(&m->own_stream), "stream create");
+  if (!rc) rc = check_hip(hipStreamSynchronize(st), "init sync");
+  if (rc) {
+    bmx_qwen3_destroy(m);
+    return rc;
+  }
+  *out = m;
+  return BMX_OK;
+}
+
+// Every weight tensor of the model under its MLX checkpoint name, in the
+// order Qwen3::load takes them (crates/base-mlx-core/src/model/qwen3.rs:
+// 194-295; names via qlin / rms, qwen3.rs:585-605).
+std::vector<WeightSlot> qwen3_weight_slots(bmx_qwen3* m) {
+  const bmx_qwen3_config& c = m->cfg;
+  std::vector<WeightSlot> v;
+  auto qlin = [&](const std::string& prefix, const QLin& q) {
+    v.push_back({prefix + ".weight", q.w, q.N, q.K / 8, true});
+    v.push_back({prefix + ".scales", q.s, q.N, q.K / 64, false});
+    v.push_back({prefix + ".biases", q.b, q.N, q.K / 64, false});
+  };
+  auto norm = [&](const std::string& name, uint16_t* p, int n) { v.push_back({name, p, 1, n, false}); };
+  qlin("model.embed_tokens", m->embed);
+  static const char* const kProj[NSLOT] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                                           "self_attn.o_proj", "mlp.gate_proj",    "mlp.up_proj",
+                                           "mlp.down_proj"};
+  for (int l = 0; l < c.layers; l++) {
+    const std::string p = "model.layers." + std::to_string(l) + ".";
+    Layer& L = m->layers[l];
+    norm(p + "input_layernorm.weight", L.in_norm, c.hidden);
+    for (int sl = 0; sl < NSLOT; sl++) qlin(p + kProj[sl], L.p[sl]);
+    norm(p + "self_attn.q_norm.weight", L.q_norm, c.head_dim);
+    norm(p + "self_attn.k_norm.weight", L.k_norm, c.head_dim);
+    norm(p + "post_attention_layernorm.weight", L.post_norm, c.hidden);
+  }
+  norm("model.norm.weight", m->final_norm, c.hidden);
+  if (!c.tied) qlin("lm_head", m->lm_head);
+  return v;
+}
+
+}  // namespace bmx
+
+extern "C" int bmx_qwen3_create_random(const bmx_qwen3_config* cfg, uint64_t seed, double sigma, int max_tokens,
+                                       bmx_qwen3** out) {
+  bmx_qwen3* m = nullptr;
+  if (int rc = qwen3_alloc(cfg, max_tokens, &m)) return rc;
+  const int H = cfg->hidden;
+  const float c = static_cast<float>(sigma / kIrwin4Std);
+  hipStream_t st = nullptr;
+  int rc = launch_init_qlinear(tensor_seed(seed, -1, 0), cfg->vocab, H, c, m->embed.w, m->embed.s, m->embed.b, st);
+  if (!rc && !cfg->tied)
+    rc = launch_init_qlinear(tensor_seed(seed, -2, 0), cfg->vocab, H, c, m->lm_head.w, m->lm_head.s, m->lm_head.b, st);
+  if (!rc) rc = fill_ones(m->final_norm, H, st);
+  for (int l = 0; !rc && l < cfg->layers; l++) {
+    Layer& L = m->layers[l];
+    for (int sl = 0; !rc && sl < NSLOT; sl++)
+      rc = launch_init_qlinear(tensor_seed(seed, l, sl), L.p[sl].N, L.p[sl].K, c, L.p[sl].w, L.p[sl].s, L.p[sl].b, st);
+    if (!rc) rc = fill_ones(L.in_norm, H, st);
+    if (!rc) rc = fill_ones(L.post_norm, H, st);
+    if (!rc) rc = fill_ones(L.q_norm, cfg->head_dim, st);
+    if (!rc) rc = fill_ones(L.k_norm, cfg->head_dim, st);
+  }
   if (!rc) rc = check_hip(hipStreamSynchronize(st), "init sync");
   if (rc) {
     bmx_qwen3_destroy(m);

@@ -221,6 +221,30 @@ typedef struct bmx_kv_cache bmx_kv_cache;
 int bmx_qwen3_create_random(const bmx_qwen3_config *cfg, uint64_t seed, double sigma, int max_tokens,
                             bmx_qwen3 **out);
 void bmx_qwen3_destroy(bmx_qwen3 *model);
+
+/* HuggingFace config.json -> shape parameters: `quantization` and
+ * `quantization_config` merged (the first wins), num_key_value_heads
+ * defaulting to num_attention_heads, head_dim to hidden / heads,
+ * rms_norm_eps to 1e-6, rope_theta to 10000, tie_word_embeddings to false;
+ * a model_type other than "qwen3" is BMX_E_UNSUPPORTED.  Host only.
+ * Replaces: ModelConfig::from_path (crates/base-mlx-core/src/model/config.rs:
+ *   149-167, defaults config.rs:109-135, 184-191). */
+int bmx_qwen3_config_from_json(const char *path, bmx_qwen3_config *out);
+
+/* A Qwen3 from an MLX checkpoint directory: config.json plus every
+ * *.safetensors shard (sorted; a later shard overrides a name), tensors taken
+ * by their MLX names (model.embed_tokens.{weight,scales,biases},
+ * model.layers.{i}.self_attn.{q,k,v,o}_proj.*, .mlp.{gate,up,down}_proj.*,
+ * .self_attn.{q,k}_norm.weight, .input_layernorm.weight,
+ * .post_attention_layernorm.weight, model.norm.weight, lm_head.* when
+ * untied).  Packed weights U32 (or I32); scales, biases, norms BF16, or
+ * F16 / F32 rounded to bf16.  A missing tensor, a shape that disagrees with
+ * the config, or tensors left over are errors (BMX_E_SHAPE, the message
+ * names them), all found before any GPU allocation.
+ * Replaces: Qwen3::load with read_all_shards (crates/base-mlx-core/src/model/
+ *   qwen3.rs:194-295, 580-627) and the bits check of infer_bits
+ *   (crates/base-mlx-core/src/model/gemma.rs:760-779). */
+int bmx_qwen3_load(const char *dir, int max_tokens, bmx_qwen3 **out);
 /* Device pointers of a projection: layer >= 0 with slot 0..6 = q,k,v,o,
  * gate,up,down; layer -1 = embed_tokens; layer -2 = lm head (tied: embed).
  * Mirrors the tensor map of Qwen3::load (qwen3.rs:205-273). */

@@ -315,6 +315,15 @@ class Qwen3:
         ba = np.ctypeslib.as_array(ctypes.cast(b, ctypes.POINTER(ctypes.c_uint16)), (n, k // 64))
         return wa, sa, ba
 
+    def norm(self, layer, which):
+        """Writable view of a norm weight (bf16 bits): layer -1 = final norm;
+        which 0..3 = input, post-attention, q, k."""
+        p = lib().orc_qwen3_norm(self.h, layer, which)
+        if not p:
+            raise IndexError((layer, which))
+        n = self.cfg.head_dim if (layer >= 0 and which >= 2) else self.cfg.hidden
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint16)), (n,))
+
     def new_cache(self, capacity):
         return KvCache(self, capacity)
 

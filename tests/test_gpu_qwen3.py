@@ -174,3 +174,43 @@ def test_qwen3_4b_shape_prefill_and_decode(gpu, orc):
     rows = [len(prompt), 1, 1, 1, len(v)]
     assert np.dot(agree, rows) / np.sum(rows) >= 0.75
     print("done", flush=True)
+
+
+def test_two_models_concurrent_prefill(gpu, orc):
+    """Two models' prefills (split-K GEMMs) launched back to back on their own
+    streams, no sync in between: each matches its oracle (no shared scratch)."""
+    import torch
+
+    toks = orc.fill_tokens(5, 9, SMALL["vocab"])
+    pairs = [_pair(gpu, orc, seed=s, max_tokens=32) for s in (31, 32)]
+    caches = [gm.new_cache(64) for gm, _ in pairs]
+    outs = [gm.forward(c, toks, all_logits=True) for (gm, _), c in zip(pairs, caches)]
+    torch.cuda.synchronize()
+    for (gm, om), g in zip(pairs, outs):
+        o = om.forward(om.new_cache(64), toks, all_logits=True)
+        assert _check_logits(g, o) >= 0.9
+
+
+def test_qmatmul_two_streams(gpu, orc):
+    """The public GEMM path (M > 8, split K) on two streams at once."""
+    import torch
+
+    from _util import to_torch_bf16
+
+    M, N, K = 64, 1024, 2560
+    args = []
+    for i in range(2):
+        wq, s, b = orc.init_qlinear(40 + i, N, K)
+        x = orc.fill_normal_bf16(50 + i, M * K).reshape(M, K)
+        w_d, s_d, b_d = gpu.init_qlinear(40 + i, N, K)
+        args.append((to_torch_bf16(x), w_d, s_d, b_d, orc.qlinear(x, wq, s, b)))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = []
+    for (x, w, s, b, _), st in zip(args, streams):
+        with torch.cuda.stream(st):
+            outs.append(gpu.quantized_matmul(x, w, s, b))
+    torch.cuda.synchronize()
+    for (_, _, _, _, ref), y in zip(args, outs):
+        yb = bf16_to_f32(torch_bf16_bits(y)).astype(np.float64)
+        r = bf16_to_f32(ref).astype(np.float64)
+        assert np.mean(np.abs(yb - r) <= np.maximum(2 * np.abs(r) * 2.0 ** -7, 1e-3 * np.max(np.abs(r)))) > 0.999
