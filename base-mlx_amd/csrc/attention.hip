@@ -19,6 +19,8 @@
 // Both run Q K^T and (prefill) P V on the matrix cores.
 #include <math.h>
 
+#include <algorithm>
+
 #include "bmx_device.h"
 
 namespace bmx {
@@ -41,6 +43,7 @@ struct AttnParams {
   int ns;     // key splits
   int causal;
   float scale;
+  int kps;    // keys per split (decode kernel: a multiple of 32, at most 256)
 };
 
 // Inputs of the fused QK-norm + RoPE + KV-write prologue of the decode
@@ -70,20 +73,24 @@ __device__ __forceinline__ float2 load_agent2(const float* a) {
   return make_float2(__uint_as_float(static_cast<uint32_t>(v)), __uint_as_float(static_cast<uint32_t>(v >> 32)));
 }
 
-// Merges the NS partials (o, m, l) of one (head, token) pair `wid` into
-// out; one wave, lane = 2 dims.  Up to 24 splits are read per batch (48
+// A running (max, sum, o) of softmax partials: lane = 2 dims.
+struct Part {
+  float mx, l, o0, o1;
+};
+
+// Folds the partials of splits [s_begin, s_end) of one (head, token) pair
+// `wid`; one wave, lane = 2 dims.  Up to 24 splits are read per batch (48
 // loads, all in flight within the 63 outstanding loads a wave can count),
 // batches folded with an online rescale.
-__device__ __forceinline__ void combine_pair(const AttnParams& p, int wid, int lane) {
-  const int h = wid / p.M, t = wid - h * p.M;
+__device__ __forceinline__ Part combine_range(const AttnParams& p, int wid, int lane, int s_begin, int s_end) {
   const int64_t base = static_cast<int64_t>(wid) * p.ns;
   constexpr int B = 24;
-  float mx = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (int s0 = 0; s0 < p.ns; s0 += B) {
+  Part r{-INFINITY, 0.0f, 0.0f, 0.0f};
+  for (int s0 = s_begin; s0 < s_end; s0 += B) {
     float2 ml[B], ov[B];
 #pragma unroll
     for (int u = 0; u < B; u++) {
-      if (s0 + u < p.ns) {
+      if (s0 + u < s_end) {
         ml[u] = load_agent2(p.part_ml + (base + s0 + u) * 2);
         ov[u] = load_agent2(p.part_o + (base + s0 + u) * kD + 2 * lane);
       }
@@ -91,27 +98,33 @@ __device__ __forceinline__ void combine_pair(const AttnParams& p, int wid, int l
     float bm = -INFINITY;
 #pragma unroll
     for (int u = 0; u < B; u++)
-      if (s0 + u < p.ns) bm = fmaxf(bm, ml[u].x);
-    const float nm = fmaxf(mx, bm);
+      if (s0 + u < s_end) bm = fmaxf(bm, ml[u].x);
+    const float nm = fmaxf(r.mx, bm);
     if (nm == -INFINITY) continue;
-    const float a = (mx == -INFINITY) ? 0.0f : expf(mx - nm);
-    l *= a;
-    o0 *= a;
-    o1 *= a;
+    const float a = (r.mx == -INFINITY) ? 0.0f : expf(r.mx - nm);
+    r.l *= a;
+    r.o0 *= a;
+    r.o1 *= a;
 #pragma unroll
     for (int u = 0; u < B; u++) {
-      if (s0 + u >= p.ns || ml[u].x == -INFINITY) continue;
+      if (s0 + u >= s_end || ml[u].x == -INFINITY) continue;
       const float w = expf(ml[u].x - nm);
-      l += w * ml[u].y;
-      o0 += w * ov[u].x;
-      o1 += w * ov[u].y;
+      r.l += w * ml[u].y;
+      r.o0 += w * ov[u].x;
+      r.o1 += w * ov[u].y;
     }
-    mx = nm;
+    r.mx = nm;
   }
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  return r;
+}
+
+// Normalises a merged partial and writes the pair `wid` (head h, token t).
+__device__ __forceinline__ void store_pair(const AttnParams& p, int wid, int lane, Part r) {
+  const int h = wid / p.M, t = wid - h * p.M;
+  const float inv = r.l > 0.0f ? 1.0f / r.l : 0.0f;
   uint16_t* o = p.out + static_cast<int64_t>(t) * p.Hq * kD + h * kD + 2 * lane;
-  o[0] = f2bf(o0 * inv);
-  o[1] = f2bf(o1 * inv);
+  o[0] = f2bf(r.o0 * inv);
+  o[1] = f2bf(r.o1 * inv);
 }
 
 // Decode / short verify (R = tokens x heads-per-kv-head query rows of one kv
@@ -173,14 +186,17 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   const int RT = min(RMAX, R - r0);   // rows in the tile
   const int offset = p.offset_dev ? *p.offset_dev : p.offset;
   const int L = offset + p.M;
-  const int c0 = split * kDecKeys + wave * kDecWaveKeys;
+  // this workgroup's keys: [kbase, kbase + kps), of which those < kend exist
+  const int kbase = split * p.kps;
+  const int kend = min(L, kbase + p.kps);
+  const int c0 = kbase + wave * kDecWaveKeys;
   const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
   // ---- fused prologue, part 1: raw rows of this wave's items (issued first,
   // so that waiting for them does not wait for the K / V loads) ----
   // items: it < RT: q row r0 + it; else new token t_lo + it - RT
   constexpr int kItems = FUSED ? (RMAX + kFuseMaxM + kDecWaves - 1) / kDecWaves : 0;
-  const int t_lo = max(0, split * kDecKeys - offset);
-  const int t_hi = min(p.M, split * kDecKeys + kDecKeys - offset);
+  const int t_lo = max(0, kbase - offset);
+  const int t_hi = min(p.M, kbase + p.kps - offset);
   const int n_items = RT + max(0, t_hi - t_lo);
   // (every load unconditional, from a valid row, so that the waits for
   // them come after the K / V stream is issued and count only these)
@@ -277,11 +293,11 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
 #pragma unroll
       for (int ks = 0; ks < 4; ks++) qa[ks] = *reinterpret_cast<const uint4*>(&qs[li][ks * 32 + g * 8]);
     }
-    // new keys: K fragments and V rows from LDS
+    // new keys of this split: K fragments and V rows from LDS
 #pragma unroll
     for (int t = 0; t < 2; t++) {
       const int tt = c0 + t * 16 + li - offset;
-      if (tt >= 0 && tt < p.M) {
+      if (tt >= t_lo && tt < t_hi) {
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) kb[t][ks] = *reinterpret_cast<const uint4*>(&kn[tt][ks * 32 + g * 8]);
       }
@@ -291,13 +307,13 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
 #pragma unroll
         for (int j = 0; j < 8; j++) {
           const int tt = c0 + vq + 4 * j - offset;
-          if (tt >= 0 && tt < p.M) vw[j] = *reinterpret_cast<const uint4*>(&vn[tt][8 * vc]);
+          if (tt >= t_lo && tt < t_hi) vw[j] = *reinterpret_cast<const uint4*>(&vn[tt][8 * vc]);
         }
       } else {
 #pragma unroll
         for (int k = 0; k < kDecWaveKeys; k++) {
           const int tt = c0 + k - offset;
-          if (tt >= 0 && tt < p.M) vr[k] = *reinterpret_cast<const uint32_t*>(&vn[tt][2 * lane]);
+          if (tt >= t_lo && tt < t_hi) vr[k] = *reinterpret_cast<const uint32_t*>(&vn[tt][2 * lane]);
         }
       }
     }
@@ -320,7 +336,7 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
     if (r >= RMAX) break;
     const int rg = r0 + r;
     const int ti = rg - (rg / tn) * tn;
-    const int lim = p.causal ? min(L, offset + ti + 1) : L;  // keys < lim are visible
+    const int lim = p.causal ? min(kend, offset + ti + 1) : kend;  // keys < lim are visible
     float s[2];
 #pragma unroll
     for (int t = 0; t < 2; t++) s[t] = (c0 + t * 16 + li < lim) ? sc[t][i] * p.scale : -INFINITY;
@@ -354,7 +370,10 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   if constexpr (kWideV) {
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      const uint32_t w4[4] = {vw[j].x, vw[j].y, vw[j].z, vw[j].w};
+      // rows past this split's keys (clamped or another split's) are never
+      // weighted, and are zeroed so that stale contents cannot be NaN
+      const uint4 vj = (c0 + vq + 4 * j < kend) ? vw[j] : make_uint4(0, 0, 0, 0);
+      const uint32_t w4[4] = {vj.x, vj.y, vj.z, vj.w};
       float v[8];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -387,7 +406,8 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   } else {
 #pragma unroll
     for (int k = 0; k < kDecWaveKeys; k++) {
-      const float v0 = bf2f(vr[k] & 0xffffu), v1 = bf2f(vr[k] >> 16);
+      const uint32_t vk = (c0 + k < kend) ? vr[k] : 0u;
+      const float v0 = bf2f(vk & 0xffffu), v1 = bf2f(vk >> 16);
 #pragma unroll
       for (int r4 = 0; r4 < RMAX; r4 += 4) {
         if (r4 >= RT) break;
@@ -461,8 +481,11 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   }
   __syncthreads();
   if (!last) return;
-  // every partial of the pair completed before its workgroup's arrival
-  for (int r = wave; r < RT; r += kDecWaves) combine_pair(p, kvh * R + r0 + r, lane);
+  // every partial of the pair completed before its workgroup's arrival.  (Two
+  // waves per row, each folding half of the splits and merged through LDS,
+  // measured 2% slower end to end.)
+  for (int r = wave; r < RT; r += kDecWaves)
+    store_pair(p, kvh * R + r0 + r, lane, combine_range(p, kvh * R + r0 + r, lane, 0, p.ns));
 }
 
 // Prefill / long verify: flash attention on MFMA.  A workgroup of 4 waves
@@ -681,10 +704,15 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   if (!ws || R > kDecMaxRows || (fuse && M > kFuseMaxM)) return kNoFit;
   if (ws_floats < kCounters) return kNoFit;
   const int max_ns = static_cast<int>((ws_floats - kCounters) / (static_cast<size_t>(Hq) * M * (kD + 2)));
-  const int chunks = (L_max + kDecKeys - 1) / kDecKeys;
-  if (chunks > max_ns) return kNoFit;
   const int rmax = R <= 4 ? 4 : R <= 8 ? 8 : 16;
   const int tiles = (R + rmax - 1) / rmax;
+  // 256 keys per split (one per wave of 32 keys).  Smaller splits to spread
+  // a 4K context over all 256 CUs measured slower: the K / V stream is
+  // latency-bound (its first loads take ~3.5 us to return either way) and
+  // more splits lengthen the merge.
+  const int kps = kDecKeys;
+  const int chunks = (L_max + kps - 1) / kps;
+  if (chunks > max_ns) return kNoFit;
   if (Hkv * tiles > kCounters) return kNoFit;
   AttnParams p = base;
   p.cnt = reinterpret_cast<unsigned*>(ws);
@@ -692,6 +720,7 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   p.part_ml = p.part_o + static_cast<size_t>(Hq) * M * chunks * kD;
   p.tq = M;
   p.ns = chunks;
+  p.kps = kps;
   p.causal = M > 1 ? 1 : 0;
   const FuseParams f = fuse ? *fuse : FuseParams{};
   const dim3 grid(Hkv, chunks, tiles), block(64 * kDecWaves);

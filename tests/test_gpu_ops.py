@@ -149,6 +149,31 @@ def test_qk_norm_rope_kv_attention_fused(gpu, orc, Hq, Hkv, M, offset):
     assert not ws[:1024].any()  # counters back at zero
 
 
+@pytest.mark.parametrize("M,offset", [(1, 300), (5, 253), (3, 0)])
+def test_qk_norm_rope_kv_attention_stale_nan_rows(gpu, M, offset):
+    """Cache rows from the new positions on hold NaN (never written memory):
+    the fused kernel reads those rows before it writes them, and positions past
+    the context are clamped onto them; neither may leak into the output."""
+    import torch
+
+    Hq, Hkv = 32, 8
+    cap = offset + M + 40
+    kc = gpu.fill_normal_bf16(60, (Hkv, cap, 128))
+    vc = gpu.fill_normal_bf16(61, (Hkv, cap, 128))
+    kc[:, offset:] = float("nan")
+    vc[:, offset:] = float("nan")
+    kc_a, vc_a = kc.clone(), vc.clone()
+    q = gpu.fill_normal_bf16(62, (M, Hq * 128), sigma=3.0)
+    k = gpu.fill_normal_bf16(63, (M, Hkv * 128), sigma=3.0)
+    v = gpu.fill_normal_bf16(64, (M, Hkv * 128))
+    n = gpu.fill_normal_bf16(65, (128,), sigma=0.3)
+    y_a = gpu.attention(gpu.qk_norm_rope_kv(q, k, v, n, n, kc_a, vc_a, offset), kc_a, vc_a, offset)
+    y_b = gpu.qk_norm_rope_kv_attention(q, k, v, n, n, kc, vc, offset)
+    torch.cuda.synchronize()
+    assert not torch.isnan(y_b.float()).any()
+    np.testing.assert_array_equal(torch_bf16_bits(y_b), torch_bf16_bits(y_a))
+
+
 def test_qk_norm_rope_kv_attention_limits(gpu):
     import torch
 
