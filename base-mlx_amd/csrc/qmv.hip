@@ -362,7 +362,9 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
 // an instantiated value.
 constexpr int kXU1 = 5;  // x units (8 values) per thread: K <= 256 * 8 * 5
 
-template <int NI, int EPI>
+// XU: x units per thread the launch needs (2 up to K = 4096, else kXU1), so
+// that no thread issues loads of clamped duplicates
+template <int NI, int EPI, int XU>
 __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const int S) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NH = (EPI == QMV_SWIGLU) ? 2 : 1;
@@ -396,9 +398,9 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   const uint16_t* nw = has_norm ? p.norm_w : p.x;  // a readable address either way
 
   // ---- 1. staging loads (unconditional, clamped) ----
-  uint4 xr[kXU1], nr[kXU1];
+  uint4 xr[XU], nr[XU];
 #pragma unroll
-  for (int i = 0; i < kXU1; i++) {
+  for (int i = 0; i < XU; i++) {
     const int idx = min(i * kThreads + static_cast<int>(threadIdx.x), W8 - 1);
     xr[i] = *reinterpret_cast<const uint4*>(p.x + idx * 8);
     nr[i] = *reinterpret_cast<const uint4*>(nw + idx * 8);
@@ -442,7 +444,7 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   if (has_norm) {
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kXU1; i++) {
+    for (int i = 0; i < XU; i++) {
       if (i * kThreads >= W8) break;  // uniform: the remaining units are clamped copies
       if (i * kThreads + static_cast<int>(threadIdx.x) < W8) {
         const uint32_t v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
@@ -460,7 +462,7 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   }
   // ---- 4. x (pair-permuted, chunk sums) and s|b into LDS ----
 #pragma unroll
-  for (int i = 0; i < kXU1; i++) {
+  for (int i = 0; i < XU; i++) {
     if (i * kThreads >= W8) break;  // uniform: the remaining units are clamped copies
     const int idx = i * kThreads + static_cast<int>(threadIdx.x);
     const bool act = idx < W8;
@@ -583,19 +585,25 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   }
 }
 
-template <int NI>
-int launch_qmv1_ni(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
+template <int NI, int XU>
+int launch_qmv1_xu(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
   switch (epi) {
     case QMV_STORE:
-      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_STORE>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_STORE, XU>), dim3(blocks), dim3(kThreads), lds, st, p, S);
       break;
     case QMV_RESIDUAL:
-      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_RESIDUAL>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_RESIDUAL, XU>), dim3(blocks), dim3(kThreads), lds, st, p, S);
       break;
     default:
-      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_SWIGLU>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_SWIGLU, XU>), dim3(blocks), dim3(kThreads), lds, st, p, S);
   }
   return check_launch("qmv1");
+}
+
+template <int NI>
+int launch_qmv1_ni(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
+  if (p.K / 8 <= 2 * kThreads) return launch_qmv1_xu<NI, 2>(epi, S, p, blocks, lds, st);
+  return launch_qmv1_xu<NI, kXU1>(epi, S, p, blocks, lds, st);
 }
 
 // Launches qmv1 when it applies (M = 1, one phase, 16-byte s|b staging, x
