@@ -363,8 +363,9 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
 constexpr int kXU1 = 5;  // x units (8 values) per thread: K <= 256 * 8 * 5
 
 // XU: x units per thread the launch needs (2 up to K = 4096, else kXU1), so
-// that no thread issues loads of clamped duplicates
-template <int NI, int EPI, int XU>
+// that no thread issues loads of clamped duplicates; NORM: the RMSNorm
+// prologue (p.norm_w set), whose weight loads are issued only then
+template <int NI, int EPI, int XU, bool NORM>
 __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const int S) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NH = (EPI == QMV_SWIGLU) ? 2 : 1;
@@ -394,8 +395,8 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   const int rl = wave * SLOTS + slot;
   const int row = row0 + rl;
   const bool valid = row < rows;
-  const bool has_norm = p.norm_w != nullptr;
-  const uint16_t* nw = has_norm ? p.norm_w : p.x;  // a readable address either way
+  constexpr bool has_norm = NORM;
+  const uint16_t* nw = p.norm_w;
 
   // ---- 1. staging loads (unconditional, clamped) ----
   uint4 xr[XU], nr[XU];
@@ -403,7 +404,7 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   for (int i = 0; i < XU; i++) {
     const int idx = min(i * kThreads + static_cast<int>(threadIdx.x), W8 - 1);
     xr[i] = *reinterpret_cast<const uint4*>(p.x + idx * 8);
-    nr[i] = *reinterpret_cast<const uint4*>(nw + idx * 8);
+    if constexpr (NORM) nr[i] = *reinterpret_cast<const uint4*>(nw + idx * 8);
   }
   uint4 sr[NH], br[NH];
   const int sb_units = RB * GU;
@@ -587,15 +588,25 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
 
 template <int NI, int XU>
 int launch_qmv1_xu(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
+  const bool norm = p.norm_w != nullptr;
   switch (epi) {
     case QMV_STORE:
-      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_STORE, XU>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      if (norm)
+        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_STORE, XU, true>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      else
+        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_STORE, XU, false>), dim3(blocks), dim3(kThreads), lds, st, p, S);
       break;
     case QMV_RESIDUAL:
-      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_RESIDUAL, XU>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      if (norm)
+        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_RESIDUAL, XU, true>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      else
+        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_RESIDUAL, XU, false>), dim3(blocks), dim3(kThreads), lds, st, p, S);
       break;
     default:
-      hipLaunchKernelGGL((qmv1_kernel<NI, QMV_SWIGLU, XU>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      if (norm)
+        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_SWIGLU, XU, true>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      else
+        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_SWIGLU, XU, false>), dim3(blocks), dim3(kThreads), lds, st, p, S);
   }
   return check_launch("qmv1");
 }
