@@ -52,6 +52,10 @@ struct QmvParams {
   // QMV_STORE with one segment: optional per-workgroup argmax partials of
   // the bf16 outputs, (value bits, row) at [m * qmv_blocks(...) + workgroup]
   uint2* amax;
+  // optional workspace for the K-split matrix-core GEMV (fp32 partials);
+  // without one the library's buffer of the stream is used
+  float* part;
+  size_t part_floats;
 };
 
 // Raises a kernel's dynamic-LDS limit to `bytes` (launches above 64 KB need
@@ -82,6 +86,13 @@ int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const ui
                int N, int K, float* ws, size_t ws_floats, hipStream_t stream);
 // Split-K partial floats the GEMM needs for any M up to max_M (0 if none).
 size_t qmm_workspace_floats(int max_M, int N, int K);
+// Partial floats the K-split GEMV of 2..8 rows of x needs for an N x K
+// weight (0 if it never splits that shape).
+size_t qmvx_workspace_floats(int N, int K);
+// A device buffer of at least `floats` floats owned by the library for the
+// (device, stream) pair, grown on demand (growing synchronizes the stream);
+// work on one stream runs in order, so its launches may share it.
+int stream_scratch(size_t floats, hipStream_t stream, float** out);
 int launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t rows, int dim, float eps,
                     hipStream_t stream);
 struct RopeTable {

@@ -181,10 +181,12 @@ __global__ void __launch_bounds__(256) qmm_reduce_kernel(const float* part, uint
   }
 }
 
-// Split-K partials for callers that bring no workspace: one device buffer
-// per (device, stream), grown on demand (the GEMM path is never inside a
-// captured graph).  Work on one stream runs in order, so its launches may
-// share a buffer; work on different streams never shares one.
+// Split-K partials (GEMM and matrix-core GEMV) for callers that bring no
+// workspace: one device buffer per (device, stream), grown on demand.
+// Growing allocates and synchronizes, so a call captured into a graph must
+// find the buffer big enough (an earlier uncaptured call of the shape on
+// that stream sized it).  Work on one stream runs in order, so its launches
+// may share a buffer; work on different streams never shares one.
 struct PartBuf {
   float* p = nullptr;
   size_t floats = 0;
@@ -192,26 +194,30 @@ struct PartBuf {
 std::mutex g_part_mu;
 std::map<std::pair<int, hipStream_t>, PartBuf> g_parts;
 
-int part_buffer(size_t floats, hipStream_t stream, float** out) {
+}  // namespace
+
+int stream_scratch(size_t floats, hipStream_t stream, float** out) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return set_error(BMX_E_ARG, "qmm: no current HIP device");
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(BMX_E_ARG, "scratch: no current HIP device");
   std::lock_guard<std::mutex> lock(g_part_mu);
   PartBuf& b = g_parts[{dev, stream}];
   if (floats > b.floats) {
     if (b.p) {
       // earlier launches on this stream may still read the old buffer
-      if (hipStreamSynchronize(stream) != hipSuccess) return set_error(BMX_E_ALLOC, "qmm: stream sync failed");
+      if (hipStreamSynchronize(stream) != hipSuccess) return set_error(BMX_E_ALLOC, "scratch: stream sync failed");
       (void)hipFree(b.p);
     }
     b.p = nullptr;
     b.floats = 0;
     if (hipMalloc(&b.p, floats * sizeof(float)) != hipSuccess)
-      return set_error(BMX_E_ALLOC, "qmm: no memory for %zu split-K partials", floats);
+      return set_error(BMX_E_ALLOC, "scratch: no memory for %zu split-K partials", floats);
     b.floats = floats;
   }
   *out = b.p;
   return BMX_OK;
 }
+
+namespace {
 
 // K splits of an M x N x K product: split while the tiles leave most of the
 // device idle (splits of at least 8 groups, a multiple of 8 groups each).
@@ -253,7 +259,7 @@ int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const ui
     const size_t need = static_cast<size_t>(splits) * M * N;
     if (ws && ws_floats >= need) {
       p.part = ws;
-    } else if (int rc = part_buffer(need, stream, &p.part)) {
+    } else if (int rc = stream_scratch(need, stream, &p.part)) {
       return rc;
     }
   }

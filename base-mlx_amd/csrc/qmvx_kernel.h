@@ -39,6 +39,12 @@
 // weight stream never stops and every wait is for one specific load.  After
 // a tile-set's last chunk the SK partial tiles are added in LDS and the
 // store / residual / SwiGLU epilogue runs.
+//
+// Split mode (long K, no fused norm): restaging x for every step would move
+// as many bytes as the weights, so workgroup b instead owns chunk b mod nkc
+// only -- its x chunk is staged once -- and walks every (grid / nkc)-th
+// tile-set, writing fp32 partial tiles; a second launch adds the nkc
+// partials of each output in chunk order and runs the epilogue.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -64,12 +70,17 @@ struct Shape {
   int nts;     // tile-sets
 };
 
+// Modes: the whole K in one chunk; several chunks walked by each workgroup
+// per tile-set (x restaged per step); K split over workgroups, one chunk
+// each, fp32 partial tiles reduced by a second launch.
+constexpr int kOneChunk = 0, kChunked = 1, kSplit = 2;
+
 // One launcher per x-row tile (2, 4, 5, 8 rows), each in its own
 // translation unit (qmvx_m*.hip) so the kernel variants compile in parallel.
-int launch_m2(bool chunk, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st);
-int launch_m4(bool chunk, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st);
-int launch_m5(bool chunk, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st);
-int launch_m8(bool chunk, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st);
+int launch_m2(int mode, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st);
+int launch_m4(int mode, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st);
+int launch_m5(int mode, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st);
+int launch_m8(int mode, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st);
 
 #ifdef BMX_QMVX_KERNELS
 namespace {
@@ -103,7 +114,7 @@ struct XRegs {
   uint4 n[kXU];
 };
 
-template <int MT, int NP, int EPI, bool CHUNK>
+template <int MT, int NP, int EPI, bool CHUNK, bool SPLIT>
 __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const Shape sh) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NH = (EPI == QMV_SWIGLU) ? 2 : 1;
@@ -123,7 +134,10 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
   float* nred = red + kWaves * NH * 4 * 64;                   // [kWaves + 1][MT]: sums of squares, 1 / rms
   const bool has_norm = p.norm_w != nullptr;
   const int grid = static_cast<int>(gridDim.x);
-  if (static_cast<int>(blockIdx.x) >= sh.nts) return;
+  // SPLIT: workgroup b owns chunk b mod nkc of every nkc-th tile-set (grid
+  // is a multiple of nkc) and writes fp32 partial tiles
+  const int tstride = SPLIT ? grid / nkc : grid;
+  if (static_cast<int>(blockIdx.x) / (SPLIT ? nkc : 1) >= sh.nts) return;
 
   auto seg_of = [&](int ts) {
     int sg = 0;
@@ -266,14 +280,15 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
     sxs[g * 16 + m] = 0.0f;  // rows MT..15 of the group sums stay zero
   }
   WRegs<NP, NH> A, B;
-  int ts = blockIdx.x, kc = 0;
+  int ts = SPLIT ? static_cast<int>(blockIdx.x) / nkc : static_cast<int>(blockIdx.x);
+  int kc = SPLIT ? static_cast<int>(blockIdx.x) % nkc : 0;
   {
   XRegs xr;
   SbRegs sbr;
-  issue_x(0, xr, has_norm);
-  issue_sb(ts, 0, sbr);
+  issue_x(kc, xr, has_norm);
+  issue_sb(ts, kc, sbr);
   __builtin_amdgcn_sched_barrier(0);
-  issue_w(ts, 0, A);
+  issue_w(ts, kc, A);
   __builtin_amdgcn_sched_barrier(0);
   if (has_norm) {
     float sq[MT];
@@ -380,7 +395,7 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    const bool last_chunk = ckc == nkc - 1;
+    const bool last_chunk = SPLIT || ckc == nkc - 1;
     if (last_chunk && SK > 1) {
 #pragma unroll
       for (int h = 0; h < NH; h++)
@@ -400,7 +415,17 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
         const int sg = seg_of(cts);
         const int rows = p.seg[sg].rows;
         const int trow = (cts - p.seg[sg].blk0) * RW + tile * 16 + n_l;
-        if (trow < rows) {
+        if constexpr (SPLIT) {
+          // fp32 partial of chunk ckc: part[ckc][m][tile-set row]
+          const int64_t ntr = static_cast<int64_t>(sh.nts) * RW;
+          float* dst = p.part + static_cast<int64_t>(ckc) * M * ntr + cts * RW + tile * 16 + n_l;
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int m = 4 * q + r;
+            if (m >= M) break;
+            dst[m * ntr] = acc[0][r];
+          }
+        } else if (trow < rows) {
 #pragma unroll
           for (int r = 0; r < 4; r++) {
             const int m = 4 * q + r;
@@ -434,6 +459,10 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
   using last = std::integral_constant<bool, false>;
   // steps of this workgroup: tile-sets blockIdx.x + i * grid, each over nkc chunks
   auto advance = [&](int& t, int& c) {
+    if constexpr (SPLIT) {
+      t += tstride;
+      return;
+    }
     if (++c == nkc) {
       c = 0;
       t += grid;
@@ -460,47 +489,54 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
   }
 }
 
-template <int MT, int NP, bool CHUNK>
+template <int MT, int NP, bool CHUNK, bool SPLIT>
 int launch_epi(QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st) {
   const void* k = nullptr;
   switch (epi) {
-    case QMV_STORE: k = reinterpret_cast<const void*>(qmvx_kernel<MT, NP, QMV_STORE, CHUNK>); break;
-    case QMV_RESIDUAL: k = reinterpret_cast<const void*>(qmvx_kernel<MT, NP, QMV_RESIDUAL, CHUNK>); break;
+    case QMV_STORE: k = reinterpret_cast<const void*>(qmvx_kernel<MT, NP, QMV_STORE, CHUNK, SPLIT>); break;
+    case QMV_RESIDUAL: k = reinterpret_cast<const void*>(qmvx_kernel<MT, NP, QMV_RESIDUAL, CHUNK, SPLIT>); break;
     default:
       // SwiGLU carries the norm (one chunk) and two matrices (at most 8 pairs)
-      if constexpr (CHUNK || NP > 8) return -1;
-      else k = reinterpret_cast<const void*>(qmvx_kernel<MT, NP, QMV_SWIGLU, false>);
+      if constexpr (CHUNK || SPLIT || NP > 8) return -1;
+      else k = reinterpret_cast<const void*>(qmvx_kernel<MT, NP, QMV_SWIGLU, false, false>);
   }
   if (int rc = allow_lds_ptr(k, lds)) return rc;
-  const int grid = std::min(sh.nts, resident_blocks(k, kThreads, lds));
+  const int res = resident_blocks(k, kThreads, lds);
+  // SPLIT: a multiple of nkc workgroups (each owns one chunk)
+  const int grid = SPLIT ? std::min(sh.nts, std::max(1, res / sh.nkc)) * sh.nkc : std::min(sh.nts, res);
   switch (epi) {
     case QMV_STORE:
-      hipLaunchKernelGGL((qmvx_kernel<MT, NP, QMV_STORE, CHUNK>), dim3(grid), dim3(kThreads), lds, st, p, sh);
+      hipLaunchKernelGGL((qmvx_kernel<MT, NP, QMV_STORE, CHUNK, SPLIT>), dim3(grid), dim3(kThreads), lds, st, p, sh);
       break;
     case QMV_RESIDUAL:
-      hipLaunchKernelGGL((qmvx_kernel<MT, NP, QMV_RESIDUAL, CHUNK>), dim3(grid), dim3(kThreads), lds, st, p, sh);
+      hipLaunchKernelGGL((qmvx_kernel<MT, NP, QMV_RESIDUAL, CHUNK, SPLIT>), dim3(grid), dim3(kThreads), lds, st, p,
+                         sh);
       break;
     default:
-      if constexpr (!CHUNK && NP <= 8)
-        hipLaunchKernelGGL((qmvx_kernel<MT, NP, QMV_SWIGLU, false>), dim3(grid), dim3(kThreads), lds, st, p, sh);
+      if constexpr (!CHUNK && !SPLIT && NP <= 8)
+        hipLaunchKernelGGL((qmvx_kernel<MT, NP, QMV_SWIGLU, false, false>), dim3(grid), dim3(kThreads), lds, st, p,
+                           sh);
   }
   return check_launch("qmvx");
 }
 
 template <int MT>
-int launch_mt(bool chunk, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st) {
+int launch_mt(int mode, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st) {
   const int n = sh.npc;
-  if (chunk) return n <= 4 ? launch_epi<MT, 4, true>(epi, p, sh, lds, st) : launch_epi<MT, 8, true>(epi, p, sh, lds, st);
+  if (mode == kChunked)
+    return n <= 4 ? launch_epi<MT, 4, true, false>(epi, p, sh, lds, st) : launch_epi<MT, 8, true, false>(epi, p, sh, lds, st);
+  if (mode == kSplit)
+    return n <= 4 ? launch_epi<MT, 4, false, true>(epi, p, sh, lds, st) : launch_epi<MT, 8, false, true>(epi, p, sh, lds, st);
   if (epi == QMV_SWIGLU) {
-    if (n <= 4) return launch_epi<MT, 4, false>(epi, p, sh, lds, st);
-    if (n <= 6) return launch_epi<MT, 6, false>(epi, p, sh, lds, st);
-    return launch_epi<MT, 8, false>(epi, p, sh, lds, st);
+    if (n <= 4) return launch_epi<MT, 4, false, false>(epi, p, sh, lds, st);
+    if (n <= 6) return launch_epi<MT, 6, false, false>(epi, p, sh, lds, st);
+    return launch_epi<MT, 8, false, false>(epi, p, sh, lds, st);
   }
-  if (n <= 4) return launch_epi<MT, 4, false>(epi, p, sh, lds, st);
-  if (n <= 6) return launch_epi<MT, 6, false>(epi, p, sh, lds, st);
-  if (n <= 8) return launch_epi<MT, 8, false>(epi, p, sh, lds, st);
-  if (n <= 12) return launch_epi<MT, 12, false>(epi, p, sh, lds, st);
-  return launch_epi<MT, 16, false>(epi, p, sh, lds, st);
+  if (n <= 4) return launch_epi<MT, 4, false, false>(epi, p, sh, lds, st);
+  if (n <= 6) return launch_epi<MT, 6, false, false>(epi, p, sh, lds, st);
+  if (n <= 8) return launch_epi<MT, 8, false, false>(epi, p, sh, lds, st);
+  if (n <= 12) return launch_epi<MT, 12, false, false>(epi, p, sh, lds, st);
+  return launch_epi<MT, 16, false, false>(epi, p, sh, lds, st);
 }
 
 }  // namespace

@@ -5,8 +5,8 @@
 namespace bmx {
 namespace qmvx {
 
-int launch_m4(bool chunk, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st) {
-  return launch_mt<4>(chunk, epi, p, sh, lds, st);
+int launch_m4(int mode, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st) {
+  return launch_mt<4>(mode, epi, p, sh, lds, st);
 }
 
 }  // namespace qmvx

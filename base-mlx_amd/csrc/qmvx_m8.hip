@@ -5,8 +5,8 @@
 namespace bmx {
 namespace qmvx {
 
-int launch_m8(bool chunk, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st) {
-  return launch_mt<8>(chunk, epi, p, sh, lds, st);
+int launch_m8(int mode, QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds, hipStream_t st) {
+  return launch_mt<8>(mode, epi, p, sh, lds, st);
 }
 
 }  // namespace qmvx

@@ -217,7 +217,8 @@ def test_silu_mul_and_add(gpu, orc):
 
 
 @pytest.mark.parametrize("M,N,K", [(9, 256, 2560), (16, 1024, 2560), (64, 4096, 2560), (128, 2560, 9728),
-                                   (300, 1000, 1024), (37, 151936, 2560)])
+                                   (300, 1000, 1024), (37, 151936, 2560), (520, 768, 1536), (24, 512, 320),
+                                   (130, 300, 576), (1100, 1024, 1536)])
 def test_qmm_vs_oracle(gpu, orc, M, N, K):
     import torch
 

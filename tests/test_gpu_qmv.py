@@ -86,6 +86,14 @@ def test_qmv_edge_shapes(gpu, orc, N, K):
     _check_qmv(gpu, orc, 5, N, K, seed=6000 + N)
 
 
+@pytest.mark.parametrize("M,N,K", [(5, 5120, 8192), (8, 4096, 12288), (2, 1320, 25600), (3, 4104, 8192)])
+def test_qmv_split_k(gpu, orc, M, N, K):
+    """Shapes whose matrix-core GEMV splits K over workgroups (fp32 partials
+    reduced by a second launch), including a row count that leaves a partial
+    16-row tile."""
+    _check_qmv(gpu, orc, M, N, K, seed=7000 + M + N)
+
+
 def test_qmv_integer_exact(gpu, orc):
     """s = b = 1 and x in {-1,0,1}: every output is an exact small integer."""
     import torch
