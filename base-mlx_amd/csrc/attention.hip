@@ -507,24 +507,43 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
 // The K and V^T tiles are double-buffered: the loads of key block j+1 are
 // issued before the products of block j.  Causal masking (query t sees keys
 // <= offset + t) stops at the block holding the diagonal and masks inside.
-constexpr int kFaQ = 64, kFaK = 64;  // queries per workgroup, keys per block
+//
+// Workgroup shape <NW, HG>: NW waves of 16 queries each, over HG q heads of
+// one kv head (a GQA group shares the K / V tiles) and 16 NW / HG tokens.
+// The K / V loads of a key block are what bound this kernel (each CU pulls
+// its tiles from L2 at a few tens of GB/s), so 8 waves over a whole group
+// (4 heads x 32 tokens for Qwen3's 32 / 8 heads) halve the tile traffic per
+// product against 4 waves over one head; with 8 waves, waves 0-3 stage V
+// and waves 4-7 stage K.
+constexpr int kFaQ = 64, kFaK = 64;  // queries per 4-wave workgroup, keys per block
 constexpr int kFaKS = kD + 8;        // K tile row stride (elements)
 constexpr int kFaVS = kFaK + 8;      // V^T tile row stride (elements)
 constexpr size_t kFaLds = 2ull * (kFaK * kFaKS + kD * kFaVS) * sizeof(uint16_t);
 
-__global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnParams p) {
+template <int NW, int HG>
+__global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams p) {
+  static_assert((NW == 4 && HG == 1) || (NW == 8 && 8 % HG == 0), "workgroup shape");
+  constexpr int TQ = 16 * NW / HG;  // tokens per workgroup
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* kt_s = reinterpret_cast<uint16_t*>(smem);  // [2][kFaK][kFaKS]
   uint16_t* vt_s = kt_s + 2 * kFaK * kFaKS;             // [2][kD][kFaVS]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // staging thread index: all 256 threads of a 4-wave workgroup stage K and
+  // V; with 8 waves, threads 0..255 stage V and 256..511 stage K
+  const int tid = threadIdx.x & 255;
+  const bool stage_k = NW == 4 || threadIdx.x >= 256, stage_v = NW == 4 || threadIdx.x < 256;
   const int n = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y, kvh = h / (p.Hq / p.Hkv);
-  const int t0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * kFaQ;  // longest rows first
+  const int rep_h = p.Hq / p.Hkv;
+  // blockIdx.y: kv head x head groups of HG
+  const int kvh = static_cast<int>(blockIdx.y) / (rep_h / HG);
+  const int h = kvh * rep_h + (static_cast<int>(blockIdx.y) % (rep_h / HG)) * HG + wave % HG;
+  const int t0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * TQ;  // longest rows first
   const int offset = p.offset_dev ? *p.offset_dev : p.offset;
   const int L = offset + p.M;
-  const int kend = p.causal ? min(L, offset + min(t0 + kFaQ, p.M)) : L;
+  const int kend = p.causal ? min(L, offset + min(t0 + TQ, p.M)) : L;
   const int nkb = (kend + kFaK - 1) / kFaK;
-  const int t = t0 + 16 * wave + n;  // this lane's query (softmax column)
+  const int tw = t0 + 16 * (wave / HG);  // the wave's first query
+  const int t = tw + n;                  // this lane's query (softmax column)
   const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
 
   // q fragments of the lane's query: dims 32 ks + 8 g .. + 7
@@ -547,14 +566,18 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnParams p) {
                                           vdc * 8);
   };
   auto load_block = [&](int k0) {
-    kr0 = *kaddr(k0, 0);
-    kr1 = *kaddr(k0, 1);
-    kr2 = *kaddr(k0, 2);
-    kr3 = *kaddr(k0, 3);
-    vr0 = *vaddr(k0, 0);
-    vr1 = *vaddr(k0, 1);
-    vr2 = *vaddr(k0, 2);
-    vr3 = *vaddr(k0, 3);
+    if (stage_k) {
+      kr0 = *kaddr(k0, 0);
+      kr1 = *kaddr(k0, 1);
+      kr2 = *kaddr(k0, 2);
+      kr3 = *kaddr(k0, 3);
+    }
+    if (stage_v) {
+      vr0 = *vaddr(k0, 0);
+      vr1 = *vaddr(k0, 1);
+      vr2 = *vaddr(k0, 2);
+      vr3 = *vaddr(k0, 3);
+    }
   };
   auto store_block = [&](int buf) {
     uint16_t* kb = kt_s + buf * kFaK * kFaKS;
@@ -562,10 +585,13 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnParams p) {
       const int e = tid + 256 * i, key = e >> 4, ch = e & 15;
       *reinterpret_cast<uint4*>(kb + key * kFaKS + ch * 8) = v;
     };
-    kput(0, kr0);
-    kput(1, kr1);
-    kput(2, kr2);
-    kput(3, kr3);
+    if (stage_k) {
+      kput(0, kr0);
+      kput(1, kr1);
+      kput(2, kr2);
+      kput(3, kr3);
+    }
+    if (!stage_v) return;
     // V^T: dim 8 vdc + d gets keys 4 vkq .. + 3 (8 bytes)
     uint16_t* vb = vt_s + buf * kD * kFaVS + 4 * vkq;
     auto vput = [&](int c, uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
@@ -675,7 +701,7 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(const AttnParams p) {
   for (int i = 0; i < 4; i++) lr[i] = __shfl(l_run, 4 * g + i, 64);
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const int tq = t0 + 16 * wave + 4 * g + i;
+    const int tq = tw + 4 * g + i;
     if (tq >= p.M) continue;
     const float inv = lr[i] > 0.0f ? 1.0f / lr[i] : 0.0f;
     uint16_t* orow = p.out + static_cast<int64_t>(tq) * p.Hq * kD + h * kD + n;
@@ -759,10 +785,20 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
                M > 1 ? 1 : 0, scale};
   const int rc = launch_decode(p, nullptr, ws, ws_floats, L_max, stream);
   if (rc != kNoFit) return rc;
-  // flash attention: no split workspace
-  if (int e = allow_lds_ptr(reinterpret_cast<const void*>(attn_prefill_kernel), kFaLds)) return e;
-  hipLaunchKernelGGL(attn_prefill_kernel, dim3((M + kFaQ - 1) / kFaQ, Hq), dim3(256), kFaLds, stream, p);
-  return check_launch("attention_prefill");
+  // flash attention (no split workspace): a GQA group per workgroup when
+  // the heads per kv head are a power of two, else one head per workgroup
+  const int rep = Hq / Hkv;
+  auto launch = [&](auto kern, int nw, int hg) {
+    if (int e = allow_lds_ptr(reinterpret_cast<const void*>(kern), kFaLds)) return e;
+    const int tq = 16 * nw / hg;
+    hipLaunchKernelGGL(kern, dim3((M + tq - 1) / tq, Hkv * (rep / hg)), dim3(64 * nw), kFaLds, stream, p);
+    return check_launch("attention_prefill");
+  };
+  if (rep % 8 == 0) return launch(attn_prefill_kernel<8, 8>, 8, 8);
+  if (rep == 4) return launch(attn_prefill_kernel<8, 4>, 8, 4);
+  if (rep == 2) return launch(attn_prefill_kernel<8, 2>, 8, 2);
+  if (rep == 1) return launch(attn_prefill_kernel<8, 1>, 8, 1);
+  return launch(attn_prefill_kernel<4, 1>, 4, 1);
 }
 
 int launch_qkv_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,

@@ -78,7 +78,7 @@ def test_qk_norm_rope_kv(gpu, orc, M, offset):
 @pytest.mark.parametrize("Hq,Hkv,M,offset", [(32, 8, 1, 0), (32, 8, 1, 4095), (32, 8, 1, 777), (16, 8, 1, 31),
                                              (32, 8, 5, 2043), (64, 8, 5, 300), (32, 8, 3, 100), (64, 8, 8, 1000),
                                              (32, 8, 37, 0), (32, 8, 40, 100), (32, 8, 200, 0), (16, 8, 130, 70),
-                                             (32, 8, 513, 3)])
+                                             (32, 8, 513, 3), (8, 8, 100, 0), (24, 8, 90, 3), (64, 8, 300, 17)])
 def test_attention(gpu, orc, Hq, Hkv, M, offset):
     cap = offset + M + 5
     q = gpu.fill_normal_bf16(11, (Hq, M, 128))
