@@ -554,8 +554,12 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     for (int ks = 0; ks < 4; ks++) qf[ks] = *reinterpret_cast<const uint4*>(qrow + 32 * ks);
   }
   // staging of one key block: K rows (4 x 16 bytes) and V (4 keys x 8 dims);
-  // plain registers (no arrays), so nothing is indexed at run time
-  uint4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
+  // plain members passed by value (no arrays or references), so the sets
+  // stay in registers.  Two sets: block j + 2 is requested while block j's
+  // products run and block j + 1 moves from registers into LDS.
+  struct Stage {
+    uint4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
+  };
   const int vdc = tid & 15, vkq = tid >> 4;  // V task: dims 8 vdc.., keys 4 vkq..
   auto kaddr = [&](int k0, int i) {
     const int e = tid + 256 * i, key = e >> 4, ch = e & 15;
@@ -566,30 +570,32 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
                                           vdc * 8);
   };
   auto load_block = [&](int k0) {
+    Stage r;
     if (stage_k) {
-      kr0 = *kaddr(k0, 0);
-      kr1 = *kaddr(k0, 1);
-      kr2 = *kaddr(k0, 2);
-      kr3 = *kaddr(k0, 3);
+      r.kr0 = *kaddr(k0, 0);
+      r.kr1 = *kaddr(k0, 1);
+      r.kr2 = *kaddr(k0, 2);
+      r.kr3 = *kaddr(k0, 3);
     }
     if (stage_v) {
-      vr0 = *vaddr(k0, 0);
-      vr1 = *vaddr(k0, 1);
-      vr2 = *vaddr(k0, 2);
-      vr3 = *vaddr(k0, 3);
+      r.vr0 = *vaddr(k0, 0);
+      r.vr1 = *vaddr(k0, 1);
+      r.vr2 = *vaddr(k0, 2);
+      r.vr3 = *vaddr(k0, 3);
     }
+    return r;
   };
-  auto store_block = [&](int buf) {
+  auto store_block = [&](const Stage r, int buf) {
     uint16_t* kb = kt_s + buf * kFaK * kFaKS;
     auto kput = [&](int i, const uint4& v) {
       const int e = tid + 256 * i, key = e >> 4, ch = e & 15;
       *reinterpret_cast<uint4*>(kb + key * kFaKS + ch * 8) = v;
     };
     if (stage_k) {
-      kput(0, kr0);
-      kput(1, kr1);
-      kput(2, kr2);
-      kput(3, kr3);
+      kput(0, r.kr0);
+      kput(1, r.kr1);
+      kput(2, r.kr2);
+      kput(3, r.kr3);
     }
     if (!stage_v) return;
     // V^T: dim 8 vdc + d gets keys 4 vkq .. + 3 (8 bytes)
@@ -600,10 +606,10 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
       *reinterpret_cast<uint2*>(vb + (vdc * 8 + 2 * c) * kFaVS) = lo;
       *reinterpret_cast<uint2*>(vb + (vdc * 8 + 2 * c + 1) * kFaVS) = hi;
     };
-    vput(0, vr0.x, vr1.x, vr2.x, vr3.x);
-    vput(1, vr0.y, vr1.y, vr2.y, vr3.y);
-    vput(2, vr0.z, vr1.z, vr2.z, vr3.z);
-    vput(3, vr0.w, vr1.w, vr2.w, vr3.w);
+    vput(0, r.vr0.x, r.vr1.x, r.vr2.x, r.vr3.x);
+    vput(1, r.vr0.y, r.vr1.y, r.vr2.y, r.vr3.y);
+    vput(2, r.vr0.z, r.vr1.z, r.vr2.z, r.vr3.z);
+    vput(3, r.vr0.w, r.vr1.w, r.vr2.w, r.vr3.w);
   };
 
   f32x4_t o[8];
@@ -613,13 +619,19 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
   const int lim = p.causal ? min(L, offset + t + 1) : L;  // keys < lim are visible to query t
   const float scale2 = p.scale * 1.44269504088896340736f;  // scale * log2(e)
 
-  load_block(0);
-  store_block(0);
+  Stage sg0 = load_block(0);
+  Stage sg1 = load_block(min(1, nkb - 1) * kFaK);
+  store_block(sg0, 0);
   __syncthreads();
-  for (int jb = 0; jb < nkb; jb++) {
+  // block jb: products from LDS buffer jb & 1; register set jb & 1 receives
+  // block jb + 2 (at the end, the last block again: every iteration issues
+  // the same loads, so each wait is for one specific block)
+  auto iter = [&](const int jb, auto par_c) {
+    constexpr int P = decltype(par_c)::value;
     const int buf = jb & 1, k0 = jb * kFaK;
     const bool more = jb + 1 < nkb;
-    if (more) load_block(k0 + kFaK);
+    if constexpr (P == 0) sg0 = load_block(min(jb + 2, nkb - 1) * kFaK);
+    else sg1 = load_block(min(jb + 2, nkb - 1) * kFaK);
     const uint16_t* kb = kt_s + buf * kFaK * kFaKS;
     const uint16_t* vb = vt_s + buf * kD * kFaVS;
     // ---- S^T = K Q^T: 4 key tiles of 16 ----
@@ -692,8 +704,12 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
         const bf16x8_t bv = __builtin_bit_cast(bf16x8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
         o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[c], bv, o[j], 0, 0, 0);
       }
-    if (more) store_block(buf ^ 1);
+    if (more) store_block(P == 0 ? sg1 : sg0, buf ^ 1);
     __syncthreads();
+  };
+  for (int jb = 0; jb < nkb; jb += 2) {
+    iter(jb, std::integral_constant<int, 0>{});
+    if (jb + 1 < nkb) iter(jb + 1, std::integral_constant<int, 1>{});
   }
   // ---- normalise and write: lane holds dim 16 j + n of queries 4 g + i ----
   float lr[4];
