@@ -84,6 +84,14 @@ int qmv_blocks(const QmvParams& p, QmvEpilogue epi);
 // stream) pair that the library keeps.
 int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M,
                int N, int K, float* ws, size_t ws_floats, hipStream_t stream);
+// The GEMM with a fused epilogue: store; residual, y = res + bf16(x W^T)
+// (res may alias y); SwiGLU of the gate W and up W2 weights,
+// y = bf16(silu(bf16(x W^T)) * bf16(x W2^T)) with MLX's roundings.  SwiGLU
+// returns kNoFit (nothing launched) when the shape would split K.
+enum QmmEpilogue { QMM_STORE = 0, QMM_RESIDUAL = 1, QMM_SWIGLU = 2 };
+int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                   const uint32_t* w2, const uint16_t* s2, const uint16_t* b2, const uint16_t* res, uint16_t* y, int M,
+                   int N, int K, float* ws, size_t ws_floats, hipStream_t stream);
 // Split-K partial floats the GEMM needs for any M up to max_M (0 if none).
 size_t qmm_workspace_floats(int max_M, int N, int K);
 // Partial floats the K-split GEMV of 2..8 rows of x needs for an N x K

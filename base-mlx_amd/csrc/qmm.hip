@@ -18,6 +18,12 @@
 // land in LDS after them.  When the tile grid is small, K is split over
 // workgroups: fp32 partial tiles go to a workspace and a reduction kernel
 // writes y.
+//
+// Epilogues (the prefill's MLX op sequence fused, with the same bf16
+// roundings): store; residual, y = res + bf16(x W^T) (qwen3.rs:520-521, 541);
+// SwiGLU of the gate and up weights (kernels.rs:73-74): the 128-row W tile
+// holds 64 gate rows (waves wn = 0) and the same 64 up rows (wn = 1), and
+// the up accumulators cross to the gate waves through LDS.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -39,12 +45,16 @@ constexpr int XP = 72, WP = 72;                // LDS row strides (elements)
 constexpr size_t kQmmLds = (1ull * QBM * XP + 1ull * QBN * WP) * 2;
 
 struct QmmParams {
-  const uint16_t* x;  // [M, K]
-  const uint32_t* w;  // [N, K/8]
-  const uint16_t* s;  // [N, K/64]
-  const uint16_t* b;  // [N, K/64]
-  uint16_t* y;        // [M, N] bf16 (one split)
-  float* part;        // [splits, M, N] fp32 partials (several splits)
+  const uint16_t* x;   // [M, K]
+  const uint32_t* w;   // [N, K/8] (SwiGLU: gate)
+  const uint16_t* s;   // [N, K/64]
+  const uint16_t* b;   // [N, K/64]
+  const uint32_t* w2;  // SwiGLU: up weight, scales and biases
+  const uint16_t* s2;
+  const uint16_t* b2;
+  const uint16_t* res;  // residual: [M, N] (may alias y)
+  uint16_t* y;          // [M, N] bf16 (one split)
+  float* part;          // [splits, M, N] fp32 partials (several splits)
   int M, N, K;
   int gps;  // groups per split
 };
@@ -54,6 +64,7 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
+template <int EPI>
 __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [QBM][XP]
@@ -62,7 +73,9 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   const int wm = wave >> 1, wn = wave & 1;  // wave sub-tile: x rows 64 wm, W rows 64 wn
   const int li = lane & 15, q = lane >> 4;
   const int M = p.M, N = p.N, K = p.K, G = K / 64;
-  const int m0 = blockIdx.y * QBM, n0 = blockIdx.x * QBN;
+  // output columns per workgroup: 128, or 64 gate / up pairs for SwiGLU
+  constexpr int CN = EPI == QMM_SWIGLU ? QBN / 2 : QBN;
+  const int m0 = blockIdx.y * QBM, n0 = blockIdx.x * CN;
   const int gb = blockIdx.z * p.gps, ge = min(G, gb + p.gps);
 
   // ---- global -> registers for one group (rows clamped: their results are
@@ -73,10 +86,11 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   const uint16_t* xp2 = xrow(tid + 2 * QT);
   const uint16_t* xp3 = xrow(tid + 3 * QT);
   const int wr = tid >> 1, wh = tid & 1;  // W row of the tile, half of the group
-  const int64_t wrow = min(n0 + wr, N - 1);
-  const uint32_t* wp = p.w + wrow * (K / 8) + wh * 4;
-  const uint16_t* sp = p.s + wrow * G;
-  const uint16_t* bp = p.b + wrow * G;
+  const bool up_row = EPI == QMM_SWIGLU && wr >= CN;
+  const int64_t wrow = min(n0 + (EPI == QMM_SWIGLU ? wr % CN : wr), N - 1);
+  const uint32_t* wp = (up_row ? p.w2 : p.w) + wrow * (K / 8) + wh * 4;
+  const uint16_t* sp = (up_row ? p.s2 : p.s) + wrow * G;
+  const uint16_t* bp = (up_row ? p.b2 : p.b) + wrow * G;
   uint4 xr0, xr1, xr2, xr3, wq;
   uint16_t sr, br;
   auto load = [&](int g) {
@@ -152,32 +166,59 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   }
 
   // ---- epilogue: lane holds W row 16 j + li, x rows 4 q + r of each tile ----
+  if constexpr (EPI == QMM_SWIGLU) {
+    // up accumulators (waves wn = 1) to the gate waves of the same rows
+    float* xch = reinterpret_cast<float*>(smem);  // [2 wm][4 i][4 j][4 r][64 lanes]
+    __syncthreads();                              // every read of the last tiles is done
+    if (wn == 1) {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) xch[(((wm * 4 + i) * 4 + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (wn == 1) return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int n = n0 + wn * 64 + j * 16 + li;
+      const int n = n0 + (EPI == QMM_SWIGLU ? 0 : wn * 64) + j * 16 + li;
       if (n >= N) continue;
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + wm * 64 + i * 16 + 4 * q + r;
         if (m >= M) continue;
-        if (p.part)
-          p.part[(static_cast<int64_t>(blockIdx.z) * M + m) * N + n] = acc[i][j][r];
-        else
-          p.y[static_cast<int64_t>(m) * N + n] = f2bf(acc[i][j][r]);
+        const int64_t o = static_cast<int64_t>(m) * N + n;
+        if constexpr (EPI == QMM_SWIGLU) {
+          // silu(gate) * up, each MLX op rounding to bf16 (kernels.rs:73-74)
+          const float g = round_bf(acc[i][j][r]);
+          const float u = round_bf(reinterpret_cast<const float*>(smem)[(((wm * 4 + i) * 4 + j) * 4 + r) * 64 + lane]);
+          const float sg = round_bf(1.0f / (1.0f + expf(-g)));
+          p.y[o] = f2bf(round_bf(g * sg) * u);
+        } else if (p.part) {
+          p.part[static_cast<int64_t>(blockIdx.z) * M * N + o] = acc[i][j][r];
+        } else if constexpr (EPI == QMM_RESIDUAL) {
+          p.y[o] = f2bf(bf2f(p.res[o]) + round_bf(acc[i][j][r]));
+        } else {
+          p.y[o] = f2bf(acc[i][j][r]);
+        }
       }
     }
 }
 
-// y = bf16(sum over splits of the fp32 partials), 4 outputs per thread
-__global__ void __launch_bounds__(256) qmm_reduce_kernel(const float* part, uint16_t* y, int64_t mn, int splits) {
+// y = bf16(sum over splits of the fp32 partials) (or res + that, rounded
+// as the residual epilogue), 4 outputs per thread
+__global__ void __launch_bounds__(256) qmm_reduce_kernel(const float* part, const uint16_t* res, uint16_t* y,
+                                                         int64_t mn, int splits) {
   const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (i0 >= mn) return;
   for (int64_t i = i0; i < min(i0 + 4, mn); i++) {
     float t = 0.0f;
     for (int s = 0; s < splits; s++) t += part[s * mn + i];
-    y[i] = f2bf(t);
+    y[i] = res ? f2bf(bf2f(res[i]) + round_bf(t)) : f2bf(t);
   }
 }
 
@@ -221,9 +262,9 @@ namespace {
 
 // K splits of an M x N x K product: split while the tiles leave most of the
 // device idle (splits of at least 8 groups, a multiple of 8 groups each).
-void qmm_split(int M, int N, int K, int* splits_out, int* gps_out) {
+void qmm_split(int M, int N, int K, int* splits_out, int* gps_out, int cols_per_tile = QBN) {
   const int G = K / 64;
-  const int tiles = ((N + QBN - 1) / QBN) * ((M + QBM - 1) / QBM);
+  const int tiles = ((N + cols_per_tile - 1) / cols_per_tile) * ((M + QBM - 1) / QBM);
   int splits = 1;
   while (tiles * splits * 2 <= 512 && G / (splits * 2) >= 8) splits *= 2;
   int gps = (G + splits - 1) / splits;
@@ -246,15 +287,20 @@ size_t qmm_workspace_floats(int max_M, int N, int K) {
   return need;
 }
 
-int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M, int N,
-               int K, float* ws, size_t ws_floats, hipStream_t stream) {
+int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                   const uint32_t* w2, const uint16_t* s2, const uint16_t* b2, const uint16_t* res, uint16_t* y, int M,
+                   int N, int K, float* ws, size_t ws_floats, hipStream_t stream) {
   if (M <= 0) return BMX_OK;
   if (K % 64 || N <= 0) return set_error(BMX_E_SHAPE, "qmm: N=%d K=%d", N, K);
-  if (!aligned(x, 16) || !aligned(w, 16)) return set_error(BMX_E_ALIGN, "qmm: x and W must be 16-byte aligned");
+  if (!aligned(x, 16) || !aligned(w, 16) || (epi == QMM_SWIGLU && !aligned(w2, 16)))
+    return set_error(BMX_E_ALIGN, "qmm: x and W must be 16-byte aligned");
   if ((M + QBM - 1) / QBM > 65535) return set_error(BMX_E_SHAPE, "qmm: M=%d too large", M);
+  const int cols = epi == QMM_SWIGLU ? QBN / 2 : QBN;  // output columns per workgroup
   int splits, gps;
-  qmm_split(M, N, K, &splits, &gps);
-  QmmParams p{x, w, s, b, y, nullptr, M, N, K, gps};
+  qmm_split(M, N, K, &splits, &gps, cols);
+  // SwiGLU needs both products of an output in one workgroup: no K split
+  if (epi == QMM_SWIGLU && splits > 1) return kNoFit;
+  QmmParams p{x, w, s, b, w2, s2, b2, res, y, nullptr, M, N, K, gps};
   if (splits > 1) {
     const size_t need = static_cast<size_t>(splits) * M * N;
     if (ws && ws_floats >= need) {
@@ -263,17 +309,28 @@ int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const ui
       return rc;
     }
   }
-  if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(qmm_kernel), kQmmLds)) return rc;
-  const dim3 grid((N + QBN - 1) / QBN, (M + QBM - 1) / QBM, splits);
-  hipLaunchKernelGGL(qmm_kernel, grid, dim3(QT), kQmmLds, stream, p);
-  if (int rc = check_launch("qmm")) return rc;
+  const dim3 grid((N + cols - 1) / cols, (M + QBM - 1) / QBM, splits);
+  auto launch = [&](auto kern) {
+    if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(kern), kQmmLds)) return rc;
+    hipLaunchKernelGGL(kern, grid, dim3(QT), kQmmLds, stream, p);
+    return check_launch("qmm");
+  };
+  const int rc = epi == QMM_SWIGLU    ? launch(qmm_kernel<QMM_SWIGLU>)
+                 : epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL>)
+                                       : launch(qmm_kernel<QMM_STORE>);
+  if (rc) return rc;
   if (splits > 1) {
     const int64_t mn = static_cast<int64_t>(M) * N;
     hipLaunchKernelGGL(qmm_reduce_kernel, dim3(static_cast<unsigned>((mn + 1023) / 1024)), dim3(256), 0, stream,
-                       p.part, y, mn, splits);
+                       p.part, epi == QMM_RESIDUAL ? res : nullptr, y, mn, splits);
     return check_launch("qmm_reduce");
   }
   return BMX_OK;
+}
+
+int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M, int N,
+               int K, float* ws, size_t ws_floats, hipStream_t stream) {
+  return launch_qmm_epi(QMM_STORE, x, w, s, b, nullptr, nullptr, nullptr, nullptr, y, M, N, K, ws, ws_floats, stream);
 }
 
 }  // namespace bmx

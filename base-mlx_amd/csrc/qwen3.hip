@@ -235,10 +235,9 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       p.part_floats = m->qmm_ws_floats;
       if (int rc = launch_qmv(p, QMV_RESIDUAL, st)) return rc;
     } else {
-      if (int rc = launch_qmm(m->att, L.p[SLOT_O].w, L.p[SLOT_O].s, L.p[SLOT_O].b, m->o, M, H, qd,
-                              m->qmm_ws, m->qmm_ws_floats, st))
+      if (int rc = launch_qmm_epi(QMM_RESIDUAL, m->att, L.p[SLOT_O].w, L.p[SLOT_O].s, L.p[SLOT_O].b, nullptr, nullptr,
+                                  nullptr, m->x, m->x, M, H, qd, m->qmm_ws, m->qmm_ws_floats, st))
         return rc;
-      if (int rc = launch_add(m->x, m->o, m->x, static_cast<int64_t>(M) * H, st)) return rc;
     }
     // ---- mlp_block + residual (kernels.rs:55-78; qwen3.rs:523-541) ----
     if (M <= 8) {
@@ -268,17 +267,20 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       if (int rc = launch_qmv(d, QMV_RESIDUAL, st)) return rc;
     } else {
       if (int rc = launch_rms_norm(m->x, L.post_norm, m->h, M, H, cf.eps, st)) return rc;
-      if (int rc = launch_qmm(m->h, L.p[SLOT_GATE].w, L.p[SLOT_GATE].s, L.p[SLOT_GATE].b, m->g, M, I, H,
-                              m->qmm_ws, m->qmm_ws_floats, st))
+      // gate, up and SwiGLU in one GEMM when it does not split K, else three steps
+      const QLin &gw = L.p[SLOT_GATE], &uw = L.p[SLOT_UP];
+      const int fused = launch_qmm_epi(QMM_SWIGLU, m->h, gw.w, gw.s, gw.b, uw.w, uw.s, uw.b, nullptr, m->a, M, I, H,
+                                       m->qmm_ws, m->qmm_ws_floats, st);
+      if (fused != kNoFit) {
+        if (fused) return fused;
+      } else {
+        if (int rc = launch_qmm(m->h, gw.w, gw.s, gw.b, m->g, M, I, H, m->qmm_ws, m->qmm_ws_floats, st)) return rc;
+        if (int rc = launch_qmm(m->h, uw.w, uw.s, uw.b, m->u, M, I, H, m->qmm_ws, m->qmm_ws_floats, st)) return rc;
+        if (int rc = launch_silu_mul(m->g, m->u, m->a, static_cast<int64_t>(M) * I, st)) return rc;
+      }
+      if (int rc = launch_qmm_epi(QMM_RESIDUAL, m->a, L.p[SLOT_DOWN].w, L.p[SLOT_DOWN].s, L.p[SLOT_DOWN].b, nullptr,
+                                  nullptr, nullptr, m->x, m->x, M, H, I, m->qmm_ws, m->qmm_ws_floats, st))
         return rc;
-      if (int rc = launch_qmm(m->h, L.p[SLOT_UP].w, L.p[SLOT_UP].s, L.p[SLOT_UP].b, m->u, M, I, H,
-                              m->qmm_ws, m->qmm_ws_floats, st))
-        return rc;
-      if (int rc = launch_silu_mul(m->g, m->u, m->a, static_cast<int64_t>(M) * I, st)) return rc;
-      if (int rc = launch_qmm(m->a, L.p[SLOT_DOWN].w, L.p[SLOT_DOWN].s, L.p[SLOT_DOWN].b, m->o, M, H, I,
-                              m->qmm_ws, m->qmm_ws_floats, st))
-        return rc;
-      if (int rc = launch_add(m->x, m->o, m->x, static_cast<int64_t>(M) * H, st)) return rc;
     }
   }
   // ---- final norm, last row unless all logits, tied head (qwen3.rs:545-555) ----
