@@ -144,6 +144,23 @@ def test_speculative_matches_greedy(gpu, orc):
     assert stats2[2] >= 0.8 * stats2[1]
 
 
+def test_prefill_unsplit_fused_epilogues(gpu, orc):
+    """A 2048-token prefill through one Qwen3-4B-shaped layer: at this size
+    the o and down GEMMs run unsplit with the residual add in their epilogue
+    and gate|up runs as one GEMM with the SwiGLU epilogue (the smaller
+    prefills above split K and add the residual in the reduction); logits of
+    every position against the oracle."""
+    shape = dict(hidden=2560, inter=9728, layers=1, n_heads=32, n_kv_heads=8, head_dim=128, vocab=1024)
+    gm = gpu.Qwen3(gpu.qwen3_config(**shape), 5, 0.02, max_tokens=2048)
+    om = orc.Qwen3(orc.make_config(**shape), 5, 0.02)
+    toks = orc.fill_tokens(21, 2048, shape["vocab"])
+    gc, oc = gm.new_cache(2048), om.new_cache(2048)
+    g = gm.forward(gc, toks, all_logits=True)
+    print("oracle forward (2048 tokens)", flush=True)
+    o = om.forward(oc, toks, all_logits=True)
+    assert _check_logits(g, o) >= 0.9
+
+
 def test_qwen3_4b_shape_prefill_and_decode(gpu, orc):
     """Full Qwen3-4B shape (36 layers, 151936 vocab): short prefill + 3 decode steps.
 
