@@ -58,7 +58,7 @@ int bmx_abi_version(void);
  * with K >= 8192) keep fp32 partials in a device buffer the library owns
  * per (device, stream), allocated or grown on first use of a larger shape
  * on that stream (which synchronizes the stream): the first call of a
- * shape on a stream must not be inside graph capture. */
+ * shape on a stream must not be inside graph capture.
  * Replaces: mlx_rs::ops::quantized_matmul(x, w, scales, biases, true, 64, 4)
  *   as called by QLinear::forward (crates/base-mlx-core/src/model/qwen3.rs:30-41),
  *   QEmbedding::lm_head (qwen3.rs:80-91) and qkv_block / mlp_block
