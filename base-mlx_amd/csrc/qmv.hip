@@ -353,11 +353,12 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
 }
 
 // M = 1 with the whole K in one LDS phase (the decode shapes).  Every load
-// of the workgroup is issued up front and unconditionally (indices are
-// clamped; duplicate addresses coalesce inside an instruction): first x, the
-// norm weight and s|b, then all NI 16-byte W chunks of each lane.  With the
-// count of loads in flight fixed, the compiler waits for each W chunk on its
-// own, so the dot products of chunk u overlap the arrival of the later ones.
+// of the workgroup is unconditional (indices are clamped; duplicate
+// addresses coalesce inside an instruction): first x, the norm weight, s|b
+// and the lane's first 16-byte W chunk; then, once x and s|b are staged in
+// LDS, the remaining NI - 1 chunks.  With the count of loads in flight
+// fixed, the compiler waits for each W chunk on its own, so the dot products
+// of chunk u overlap the arrival of the later ones.
 // S (lanes per row) is a launch parameter; NI = ceil(K/32 / S) rounded up to
 // an instantiated value.
 constexpr int kXU1 = 5;  // x units (8 values) per thread: K <= 256 * 8 * 5
@@ -420,25 +421,27 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   }
   // keep the staging loads ahead of the W stream in issue order
   __builtin_amdgcn_sched_barrier(0);
-  // ---- 2. every W chunk of this lane ----
-  // in the order they are consumed: chunk by chunk, both matrices of a chunk
-  // together
+  // ---- 2. the lane's W chunks, in the order they are consumed: chunk by
+  // chunk, both matrices of a chunk together.  Only chunk 0 goes out here;
+  // the others after x and s|b are staged (step 4): the issuing wave stalls
+  // while the load queue drains, so staging between the two batches overlaps
+  // the W stream instead of waiting behind the whole issue loop ----
   uint4 wv[NI][NH];
+  const uint32_t* wrow[NH];
   {
     const int64_t rr = min(row, rows - 1);
-    const uint32_t* wrow[NH];
 #pragma unroll
     for (int h = 0; h < NH; h++) wrow[h] = p.seg[EPI == QMV_SWIGLU ? h : seg].w + rr * (K / 8);
-#pragma unroll
-    for (int u = 0; u < NI; u++) {
-      const int c = min(sl + (u << lshift), C - 1);
-#pragma unroll
-      for (int h = 0; h < NH; h++) {
-        const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[h] + c * 4));
-        wv[u][h] = make_uint4(t.x, t.y, t.z, t.w);
-      }
-    }
   }
+  auto issue_w = [&](int u) {
+    const int c = min(sl + (u << lshift), C - 1);
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[h] + c * 4));
+      wv[u][h] = make_uint4(t.x, t.y, t.z, t.w);
+    }
+  };
+  issue_w(0);
   // ---- 3. fused RMSNorm (fast::rms_norm, qwen3.rs:50-55) from the staged x:
   //      h = w * bf16(x * rsqrt(mean(x^2) + eps)) ----
   float inv = 1.0f;
@@ -506,6 +509,9 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
       }
     }
   }
+  // the rest of the W stream (step 2)
+#pragma unroll
+  for (int u = 1; u < NI; u++) issue_w(u);
   __syncthreads();
   // ---- 5. dot products, chunk by chunk as the W stream arrives ----
   float acc[NH];
