@@ -599,7 +599,10 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     }
     if (!stage_v) return;
     // V^T: dim 8 vdc + d gets keys 4 vkq .. + 3 (8 bytes)
-    uint16_t* vb = vt_s + buf * kD * kFaVS + 4 * vkq;
+    // 4-key chunk vkq of dim row r sits at chunk vkq ^ ((r >> 3) & 7): the
+    // 8 rows of one thread share r >> 3 = vdc, so the 16 vdc lanes of a
+    // store spread over 8 chunk columns instead of one bank pair
+    uint16_t* vb = vt_s + buf * kD * kFaVS + 4 * (vkq ^ (vdc & 7));
     auto vput = [&](int c, uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
       const uint2 lo = make_uint2((a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16));
       const uint2 hi = make_uint2((a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u));
@@ -698,9 +701,12 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     for (int c = 0; c < 2; c++)
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const uint16_t* vrow = vb + (j * 16 + n) * kFaVS + 32 * c + 4 * g;
-        const uint2 v0 = *reinterpret_cast<const uint2*>(vrow);
-        const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 16);
+        // dim row j 16 + n, keys 32 c + 4 g.. and 32 c + 16 + 4 g.. (4-key
+        // chunks 8 c + g and 8 c + 4 + g, swizzled as stored)
+        const int sw = (2 * j + (n >> 3)) & 7;
+        const uint16_t* vrow = vb + (j * 16 + n) * kFaVS;
+        const uint2 v0 = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * c + g) ^ sw));
+        const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * c + 4 + g) ^ sw));
         const bf16x8_t bv = __builtin_bit_cast(bf16x8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
         o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[c], bv, o[j], 0, 0, 0);
       }
