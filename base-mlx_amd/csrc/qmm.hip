@@ -114,7 +114,10 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     auto put_word = [&](uint16_t* d, uint32_t word) {
       // nibble k of the word is value k: even k in the low nibble of byte
       // k/2, odd k in the high nibble
-      const uint32_t lo = word & 0x0f0f0f0fu, hi = (word >> 4) & 0x0f0f0f0fu;
+      uint32_t lo = word & 0x0f0f0f0fu, hi = (word >> 4) & 0x0f0f0f0fu;
+      // opaque, so each byte converts with one v_cvt_f32_ubyte<n> instead of
+      // a bit-field extract and a convert
+      asm volatile("" : "+v"(lo), "+v"(hi));
       uint4 o;
       o.x = pk_bf16(fmaf(sv, static_cast<float>(lo & 0xffu), bv), fmaf(sv, static_cast<float>(hi & 0xffu), bv));
       o.y = pk_bf16(fmaf(sv, static_cast<float>((lo >> 8) & 0xffu), bv),
