@@ -43,16 +43,29 @@ __device__ __forceinline__ T wave_sum_xor(T v, int width) {
   return v;
 }
 
+// The nibble-pair mask 0x000F000F and the bf16 magic 0x43004300 held in
+// registers the compiler cannot fold back into literals: a gfx9 VOP3
+// instruction takes no literal operand, so with literals each pair would
+// unpack as an and plus an or; with both in VGPRs it is one v_and_or_b32.
+// A kernel makes them once and passes them to word_dot.
+struct NibbleK {
+  uint32_t mask, magic;
+};
+__device__ __forceinline__ NibbleK nibble_consts() {
+  NibbleK k{0x000f000fu, 0x43004300u};
+  asm volatile("" : "+v"(k.mask), "+v"(k.magic));
+  return k;
+}
+
 // Dot of one packed word (8 nibbles q_0..q_7) with its pair-permuted x
 // (permute_pairs: (x_e, x_{e+4}) per word), +128 bias on every q:
 // (w >> 4j & 0x000F000F) | 0x43004300 is the bf16 pair (128 + q_j, 128 +
 // q_{j+4}), fed straight to v_dot2c_f32_bf16.
-__device__ __forceinline__ float word_dot(uint32_t w, uint4 xp, float acc) {
-  const uint32_t magic = 0x43004300u;
-  acc = dot2_bf16((w & 0x000f000fu) | magic, xp.x, acc);
-  acc = dot2_bf16(((w >> 4) & 0x000f000fu) | magic, xp.y, acc);
-  acc = dot2_bf16(((w >> 8) & 0x000f000fu) | magic, xp.z, acc);
-  acc = dot2_bf16(((w >> 12) & 0x000f000fu) | magic, xp.w, acc);
+__device__ __forceinline__ float word_dot(uint32_t w, uint4 xp, float acc, const NibbleK& k) {
+  acc = dot2_bf16((w & k.mask) | k.magic, xp.x, acc);
+  acc = dot2_bf16(((w >> 4) & k.mask) | k.magic, xp.y, acc);
+  acc = dot2_bf16(((w >> 8) & k.mask) | k.magic, xp.z, acc);
+  acc = dot2_bf16(((w >> 12) & k.mask) | k.magic, xp.w, acc);
   return acc;
 }
 

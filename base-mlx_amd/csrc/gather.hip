@@ -100,6 +100,7 @@ __global__ void __launch_bounds__(kGThreads) gather_qmv_kernel(const GatherParam
   }
   __syncthreads();
   // ---- dot products: y[m] += s * D + (b - 128 s) * Sx per group ----
+  const NibbleK nk = nibble_consts();
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; m++) acc[m] = 0.0f;
@@ -115,14 +116,14 @@ __global__ void __launch_bounds__(kGThreads) gather_qmv_kernel(const GatherParam
         const uint4* xp0 = reinterpret_cast<const uint4*>(xs + (m * C + 2 * g) * kGChunk);
         const uint4* xp1 = reinterpret_cast<const uint4*>(xs + (m * C + 2 * g + 1) * kGChunk);
         float d0 = 0.0f, d1 = 0.0f;
-        d0 = word_dot(w0[u].x, xp0[0], d0);
-        d1 = word_dot(w0[u].y, xp0[1], d1);
-        d0 = word_dot(w0[u].z, xp0[2], d0);
-        d1 = word_dot(w0[u].w, xp0[3], d1);
-        d0 = word_dot(w1[u].x, xp1[0], d0);
-        d1 = word_dot(w1[u].y, xp1[1], d1);
-        d0 = word_dot(w1[u].z, xp1[2], d0);
-        d1 = word_dot(w1[u].w, xp1[3], d1);
+        d0 = word_dot(w0[u].x, xp0[0], d0, nk);
+        d1 = word_dot(w0[u].y, xp0[1], d1, nk);
+        d0 = word_dot(w0[u].z, xp0[2], d0, nk);
+        d1 = word_dot(w0[u].w, xp0[3], d1, nk);
+        d0 = word_dot(w1[u].x, xp1[0], d0, nk);
+        d1 = word_dot(w1[u].y, xp1[1], d1, nk);
+        d0 = word_dot(w1[u].z, xp1[2], d0, nk);
+        d1 = word_dot(w1[u].w, xp1[3], d1, nk);
         const float sx = sxs[m * C + 2 * g] + sxs[m * C + 2 * g + 1];
         acc[m] += s * (d0 + d1);
         acc[m] += bb * sx;

@@ -258,6 +258,7 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
     __syncthreads();
 
     // ---- stream W over this phase's chunks ----
+    const NibbleK nk = nibble_consts();
     for (int i0 = 0; i0 < n_i; i0 += U) {
 #pragma unroll
       for (int u = 0; u < U; u++) {
@@ -280,10 +281,10 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
 #pragma unroll
               for (int h = 0; h < NH; h++) {
                 float d = 0.0f;
-                d = word_dot(wv[u][h].x, x0, d);
-                d = word_dot(wv[u][h].y, x1, d);
-                d = word_dot(wv[u][h].z, x2, d);
-                d = word_dot(wv[u][h].w, x3, d);
+                d = word_dot(wv[u][h].x, x0, d, nk);
+                d = word_dot(wv[u][h].y, x1, d, nk);
+                d = word_dot(wv[u][h].z, x2, d, nk);
+                d = word_dot(wv[u][h].w, x3, d, nk);
                 acc[h][m] += sv[h] * d;
                 acc[h][m] += bb[h] * sx;
               }
@@ -514,6 +515,7 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   for (int u = 1; u < NI; u++) issue_w(u);
   __syncthreads();
   // ---- 5. dot products, chunk by chunk as the W stream arrives ----
+  const NibbleK nk = nibble_consts();
   float acc[NH];
 #pragma unroll
   for (int h = 0; h < NH; h++) acc[h] = 0.0f;
@@ -530,10 +532,10 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
         const float sv = bf2f(sb & 0xffffu);
         const float bb = bf2f(sb >> 16) - 128.0f * sv;
         float d0 = 0.0f, d1 = 0.0f;  // two independent dot2 chains
-        d0 = word_dot(wv[u][h].x, x0, d0);
-        d1 = word_dot(wv[u][h].y, x1, d1);
-        d0 = word_dot(wv[u][h].z, x2, d0);
-        d1 = word_dot(wv[u][h].w, x3, d1);
+        d0 = word_dot(wv[u][h].x, x0, d0, nk);
+        d1 = word_dot(wv[u][h].y, x1, d1, nk);
+        d0 = word_dot(wv[u][h].z, x2, d0, nk);
+        d1 = word_dot(wv[u][h].w, x3, d1, nk);
         acc[h] += sv * (d0 + d1);
         acc[h] += bb * sx;
       }
@@ -882,6 +884,7 @@ __global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const
     __syncthreads();
     if constexpr (decltype(pf)::value) issue_tile(tt + static_cast<int>(gridDim.x), nxt);
     __builtin_amdgcn_sched_barrier(0);
+    const NibbleK nk = nibble_consts();
     float acc[NH][MT];
 #pragma unroll
     for (int h = 0; h < NH; h++)
@@ -907,10 +910,10 @@ __global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const
 #pragma unroll
           for (int h = 0; h < NH; h++) {
             float d0 = 0.0f, d1 = 0.0f;
-            d0 = word_dot(cur.w[u][h].x, x0, d0);
-            d1 = word_dot(cur.w[u][h].y, x1, d1);
-            d0 = word_dot(cur.w[u][h].z, x2, d0);
-            d1 = word_dot(cur.w[u][h].w, x3, d1);
+            d0 = word_dot(cur.w[u][h].x, x0, d0, nk);
+            d1 = word_dot(cur.w[u][h].y, x1, d1, nk);
+            d0 = word_dot(cur.w[u][h].z, x2, d0, nk);
+            d1 = word_dot(cur.w[u][h].w, x3, d1, nk);
             acc[h][m] += sv[h] * (d0 + d1);
             acc[h][m] += bb[h] * sx;
           }
