@@ -90,13 +90,13 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // 8 nibbles of a packed word -> bf16 (128 + q), pair-permuted order
-__device__ __forceinline__ bf16x8_t nibbles_bf16(uint32_t w) {
-  const uint32_t magic = 0x43004300u;
+// (mask and magic in registers: one v_and_or_b32 per pair, see NibbleK)
+__device__ __forceinline__ bf16x8_t nibbles_bf16(uint32_t w, const NibbleK& k) {
   uint4 p;
-  p.x = (w & 0x000f000fu) | magic;
-  p.y = ((w >> 4) & 0x000f000fu) | magic;
-  p.z = ((w >> 8) & 0x000f000fu) | magic;
-  p.w = ((w >> 12) & 0x000f000fu) | magic;
+  p.x = (w & k.mask) | k.magic;
+  p.y = ((w >> 4) & k.mask) | k.magic;
+  p.z = ((w >> 8) & k.mask) | k.magic;
+  p.w = ((w >> 12) & k.mask) | k.magic;
   return __builtin_bit_cast(bf16x8_t, p);
 }
 
@@ -336,6 +336,7 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
 #pragma unroll
   for (int h = 0; h < NH; h++) acc[h] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const int xm = n_l < MT ? n_l : 0;
+  const NibbleK nk = nibble_consts();
   const int pq = ((q & 1) << 1) | (q >> 1);  // this lane's word pair in a group after the swap
   const uint32_t keep = n_l < MT ? 0xffffffffu : 0u;  // A rows >= MT are zeros
 
@@ -380,8 +381,8 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
 #pragma unroll
           for (int h = 0; h < NH; h++) {
             f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, nibbles_bf16(wv[h][2 * e]), d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, nibbles_bf16(wv[h][2 * e + 1]), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, nibbles_bf16(wv[h][2 * e], nk), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, nibbles_bf16(wv[h][2 * e + 1], nk), d, 0, 0, 0);
             const int so = (h * RW + tile * 16 + n_l) * KC + gl;
             const float sv = bf2f(ss[so]);
             const float bb = bf2f(bs[so]) - 128.0f * sv;
