@@ -45,7 +45,7 @@ bool split_shape(int total_tiles, int G, Shape* sh) {
 size_t shape_lds(int mt, int nh, const Shape& sh) {
   const int RW = 16 * sh.TB;
   return static_cast<size_t>(mt) * (sh.KC * 8 + 1) * 16 + static_cast<size_t>(sh.KC) * 16 * 4 +
-         2ull * nh * RW * sh.KC * 2 + static_cast<size_t>(kWaves) * nh * 4 * 64 * 4 +
+         2ull * nh * RW * sb_stride(sh.KC) * 2 + static_cast<size_t>(kWaves) * nh * 4 * 64 * 4 +
          static_cast<size_t>(kWaves + 1) * mt * 4;
 }
 

@@ -70,6 +70,12 @@ struct Shape {
   int nts;     // tile-sets
 };
 
+// LDS row stride (halfwords) of the s and b tiles of a step, [RW rows][KC
+// groups]: 16-byte aligned rows whose stride in 16-byte units is odd, so
+// that the 16 rows of a tile, read at one group, fall in 16 different banks
+// (KC = 64 unpadded put all of them in one bank)
+__host__ __device__ inline int sb_stride(int KC) { return KC + ((KC / 8) % 2 == 0 ? 8 : 0); }
+
 // Modes: the whole K in one chunk; several chunks walked by each workgroup
 // per tile-set (x restaged per step); K split over workgroups, one chunk
 // each, fp32 partial tiles reduced by a second launch.
@@ -128,9 +134,10 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
   const int XS = UC + 1;   // LDS row stride in units (bank skew)
   uint4* xs = reinterpret_cast<uint4*>(smem);                 // [MT][XS]
   float* sxs = reinterpret_cast<float*>(xs + MT * XS);        // [KC][16]
-  uint16_t* ss = reinterpret_cast<uint16_t*>(sxs + KC * 16);  // [NH][RW][KC]
-  uint16_t* bs = ss + NH * RW * KC;                           // [NH][RW][KC]
-  float* red = reinterpret_cast<float*>(bs + NH * RW * KC);  // [kWaves][NH][4][64]
+  const int SBS = sb_stride(KC);
+  uint16_t* ss = reinterpret_cast<uint16_t*>(sxs + KC * 16);  // [NH][RW][SBS]
+  uint16_t* bs = ss + NH * RW * SBS;                          // [NH][RW][SBS]
+  float* red = reinterpret_cast<float*>(bs + NH * RW * SBS);  // [kWaves][NH][4][64]
   float* nred = red + kWaves * NH * 4 * 64;                   // [kWaves + 1][MT]: sums of squares, 1 / rms
   const bool has_norm = p.norm_w != nullptr;
   const int grid = static_cast<int>(gridDim.x);
@@ -191,7 +198,7 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
     auto one = [&](int i, const uint4& v) {
       if (i * kThreads + static_cast<int>(threadIdx.x) < sb_total) {
         const int hs = sb_hs[i];
-        uint16_t* dst = ((hs & 1) ? bs : ss) + ((hs >> 1) * RW + sb_r[i]) * KC + sb_u[i] * 8;
+        uint16_t* dst = ((hs & 1) ? bs : ss) + ((hs >> 1) * RW + sb_r[i]) * SBS + sb_u[i] * 8;
         *reinterpret_cast<uint4*>(dst) = v;
       }
     };
@@ -383,7 +390,7 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
             f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
             d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, nibbles_bf16(wv[h][2 * e], nk), d, 0, 0, 0);
             d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, nibbles_bf16(wv[h][2 * e + 1], nk), d, 0, 0, 0);
-            const int so = (h * RW + tile * 16 + n_l) * KC + gl;
+            const int so = (h * RW + tile * 16 + n_l) * SBS + gl;
             const float sv = bf2f(ss[so]);
             const float bb = bf2f(bs[so]) - 128.0f * sv;
 #pragma unroll
