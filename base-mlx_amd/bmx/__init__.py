@@ -70,11 +70,8 @@ def _require_cuda(*ts):
             raise BmxError(BMX_E_ARG, "tensors must be contiguous")
 
 
-def quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4, out=None, stream=None):
-    """y = x @ dequantize(w, scales, biases).T  (x [..., K] bf16, w [N, K/8] int32/uint32)."""
+def _qmatmul_args(x, w, scales, biases, group_size, bits):
     torch = _torch()
-    if not transpose:
-        raise BmxError(BMX_E_UNSUPPORTED, "only transpose=True is implemented (the reference's only use)")
     _require_cuda(x, w, scales, biases)
     if x.dtype != torch.bfloat16 or scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
         raise BmxError(BMX_E_ARG, "x, scales and biases must be bfloat16")
@@ -84,11 +81,40 @@ def quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4
         raise BmxError(BMX_E_SHAPE, f"w has {w.shape[-1]} words per row, K={K} needs {K // 8}")
     if scales.shape != biases.shape or scales.shape[0] != N or scales.shape[-1] * group_size != K:
         raise BmxError(BMX_E_SHAPE, f"scales/biases {tuple(scales.shape)} do not match N={N}, K={K}")
-    M = x.numel() // K
+    return x.numel() // K, N, K
+
+
+def quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4, out=None, stream=None):
+    """y = x @ dequantize(w, scales, biases).T  (x [..., K] bf16, w [N, K/8] int32/uint32).
+
+    transpose=False is rejected by the library (BMX_E_UNSUPPORTED), as the
+    reference only ever passes True."""
+    torch = _torch()
+    M, N, K = _qmatmul_args(x, w, scales, biases, group_size, bits)
     if out is None:
         out = torch.empty(*x.shape[:-1], N, dtype=torch.bfloat16, device=x.device)
     call("bmx_qmatmul_affine", _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), _ptr(out), M, N, K,
-         group_size, bits, _stream(stream))
+         1 if transpose else 0, group_size, bits, _stream(stream))
+    return out
+
+
+def qmatmul_workspace_bytes(M, N, K):
+    """Bytes of split-K workspace quantized_matmul_ws needs for this shape."""
+    return int(load().bmx_qmatmul_workspace_bytes(M, N, K))
+
+
+def quantized_matmul_ws(x, w, scales, biases, workspace, transpose=True, group_size=64, bits=4, out=None,
+                        stream=None):
+    """quantized_matmul with the split-K partials in `workspace` (a CUDA tensor
+    of at least qmatmul_workspace_bytes(M, N, K) bytes, or None when that is
+    0); never allocates device memory in the library."""
+    torch = _torch()
+    M, N, K = _qmatmul_args(x, w, scales, biases, group_size, bits)
+    if out is None:
+        out = torch.empty(*x.shape[:-1], N, dtype=torch.bfloat16, device=x.device)
+    wp, wb = (None, 0) if workspace is None else (_ptr(workspace), workspace.numel() * workspace.element_size())
+    call("bmx_qmatmul_affine_ws", _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), _ptr(out), M, N, K,
+         1 if transpose else 0, group_size, bits, wp, wb, _stream(stream))
     return out
 
 

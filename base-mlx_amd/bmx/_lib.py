@@ -57,7 +57,10 @@ c_f = ctypes.c_float
 SIGNATURES = {
     "bmx_last_error": (ctypes.c_char_p, []),
     "bmx_abi_version": (c_int, []),
-    "bmx_qmatmul_affine": (c_int, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_int, c_int, c_p]),
+    "bmx_qmatmul_affine": (c_int, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_p]),
+    "bmx_qmatmul_workspace_bytes": (ctypes.c_size_t, [c_i64, c_i64, c_i64]),
+    "bmx_qmatmul_affine_ws": (c_int, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_p,
+                                      ctypes.c_size_t, c_p]),
     "bmx_dequantize_affine": (c_int, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_int, c_int, c_p]),
     "bmx_dequant_gather": (c_int, [c_p, c_i64, c_i64, c_p, c_p, c_p, c_p, c_i64, c_int, c_int, c_p]),
     "bmx_init_qlinear": (c_int, [c_u64, c_i64, c_i64, c_f, c_p, c_p, c_p, c_p]),

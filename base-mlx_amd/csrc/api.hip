@@ -67,23 +67,28 @@ using namespace bmx;
 
 extern "C" const char* bmx_last_error(void) { return g_last_error; }
 
-extern "C" int bmx_abi_version(void) { return (1 << 16) | 0; }
+extern "C" int bmx_abi_version(void) { return (2 << 16) | 0; }
 
-extern "C" int bmx_qmatmul_affine(const bmx_bf16* x, const uint32_t* w, const bmx_bf16* scales,
-                                  const bmx_bf16* biases, bmx_bf16* y, int64_t M, int64_t N, int64_t K,
-                                  int group_size, int bits, void* stream) {
+namespace {
+
+// quantized_matmul for every entry point: ws (fp32 split-K partials) is the
+// caller's workspace, or null for the library's per-stream buffer.
+int qmatmul(const bmx_bf16* x, const uint32_t* w, const bmx_bf16* scales, const bmx_bf16* biases, bmx_bf16* y,
+            int64_t M, int64_t N, int64_t K, int transpose, int group_size, int bits, float* ws, size_t ws_floats,
+            hipStream_t stream) {
+  if (!transpose)
+    return set_error(BMX_E_UNSUPPORTED, "qmatmul: transpose=false is not supported (W must be [N, K/8], "
+                                        "as every quantized_matmul call of the reference passes it)");
   if (bits != 4 || group_size != 64)
     return set_error(BMX_E_UNSUPPORTED, "qmatmul: only bits=4, group_size=64 (got %d, %d)", bits, group_size);
   if (!x || !w || !scales || !biases || !y) return set_error(BMX_E_ARG, "qmatmul: null pointer");
-  if (M < 0 || N <= 0 || K <= 0 || K % 64 || N > INT32_MAX || K > INT32_MAX)
+  if (M < 0 || N <= 0 || K <= 0 || K % 64 || N > INT32_MAX || K > INT32_MAX || M > INT32_MAX)
     return set_error(BMX_E_SHAPE, "qmatmul: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
                      (long long)K);
   if (M == 0) return BMX_OK;
-  if (M > 8) {
-    if (M > INT32_MAX) return set_error(BMX_E_SHAPE, "qmatmul: M too large");
-    return launch_qmm(x, w, scales, biases, y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), nullptr, 0,
-                      as_stream(stream));
-  }
+  if (M > 8)
+    return launch_qmm(x, w, scales, biases, y, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), ws,
+                      ws_floats, stream);
   QmvParams p{};
   p.ldx = K;
   p.nseg = 1;
@@ -92,5 +97,32 @@ extern "C" int bmx_qmatmul_affine(const bmx_bf16* x, const uint32_t* w, const bm
   p.seg[0] = QmvSegment{w, scales, biases, y, static_cast<int>(N), 0};
   p.x = x;
   p.m = static_cast<int>(M);
-  return launch_qmv(p, QMV_STORE, as_stream(stream));
+  p.part = ws;
+  p.part_floats = ws_floats;
+  return launch_qmv(p, QMV_STORE, stream);
+}
+
+}  // namespace
+
+extern "C" int bmx_qmatmul_affine(const bmx_bf16* x, const uint32_t* w, const bmx_bf16* scales,
+                                  const bmx_bf16* biases, bmx_bf16* y, int64_t M, int64_t N, int64_t K, int transpose,
+                                  int group_size, int bits, void* stream) {
+  return qmatmul(x, w, scales, biases, y, M, N, K, transpose, group_size, bits, nullptr, 0, as_stream(stream));
+}
+
+extern "C" size_t bmx_qmatmul_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64 || N > INT32_MAX || K > INT32_MAX || M > INT32_MAX) return 0;
+  if (M > 8) return qmm_need_floats(QMM_STORE, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)) * 4;
+  return M >= 2 ? qmvx_workspace_floats(static_cast<int>(N), static_cast<int>(K)) * 4 : 0;
+}
+
+extern "C" int bmx_qmatmul_affine_ws(const bmx_bf16* x, const uint32_t* w, const bmx_bf16* scales,
+                                     const bmx_bf16* biases, bmx_bf16* y, int64_t M, int64_t N, int64_t K,
+                                     int transpose, int group_size, int bits, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (!workspace && workspace_bytes) return set_error(BMX_E_ARG, "qmatmul_ws: null workspace of %zu bytes", workspace_bytes);
+  if (!aligned(workspace, 16)) return set_error(BMX_E_ALIGN, "qmatmul_ws: workspace must be 16-byte aligned");
+  NoAllocScope no_alloc;
+  return qmatmul(x, w, scales, biases, y, M, N, K, transpose, group_size, bits, static_cast<float*>(workspace),
+                 workspace_bytes / sizeof(float), as_stream(stream));
 }

@@ -59,9 +59,9 @@ struct FuseParams {
 };
 
 // The split partials travel between workgroups on different XCDs (each with
-// its own L2) through agent-scope atomic loads and stores (relaxed), which
-// the compiler issues with sc1 -- coherent across the XCDs without the L2
-// writeback / invalidate of a device-scope fence.
+// its own L2) through agent-scope atomic loads and stores (relaxed, issued
+// with sc1: coherent across the XCDs); the arrival counter's agent-scope
+// acquire-release increment orders them (one per workgroup, not per wave).
 // Pairs of floats move as one 8-byte access (8-byte aligned addresses).
 __device__ __forceinline__ void store_agent2(float* a, float x, float y) {
   const uint64_t v = static_cast<uint64_t>(__float_as_uint(x)) | (static_cast<uint64_t>(__float_as_uint(y)) << 32);
@@ -139,10 +139,9 @@ __device__ __forceinline__ void store_pair(const AttnParams& p, int wid, int lan
 //     exact bf16 x bf16 products.
 //   softmax over the wave's 32 keys: registers + DPP reductions inside
 //     16-lane rows; p goes to LDS as [key][row].
-//   PV on VALU in fp32.  RMAX <= 8: V in 16-byte loads, lane = 8 dims x 8
-//     keys, the four key quarters added by permlane swap butterflies;
-//     RMAX = 16: lane = 2 dims over all 32 keys (4-byte loads, no cross-lane
-//     reduction).
+//   PV on VALU in fp32: V in 16-byte loads, lane = 8 dims x 8 keys, the
+//     four key quarters added by permlane swap butterflies (the same
+//     operations for every row, whatever RMAX).
 // The 8 waves' (o, m, l) are merged in LDS, 8 rows at a time, and one
 // unnormalised partial per row and workgroup goes to the split workspace
 // (NS = ceil(L / 256)).  The last workgroup of a (kv head, row tile) to
@@ -175,7 +174,6 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   __shared__ __align__(16) uint16_t kn[FUSED ? kFuseMaxM : 1][kQS];
   __shared__ __align__(16) uint16_t vn[FUSED ? kFuseMaxM : 1][kD];
   __shared__ int last;
-  constexpr bool kWideV = RMAX <= kMergeRows;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int li = lane & 15, g = lane >> 4;
   const int tn = p.M;
@@ -237,24 +235,14 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) kb[t][ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
   }
-  // V, wide (RMAX <= 8): lane holds dims 8 vc .. 8 vc + 7 of keys vq + 4 j,
-  // j < 8 (one 16-byte load per key; an instruction reads 4 whole key rows);
-  // narrow: lane holds dims 2 lane, 2 lane + 1 of all 32 keys
+  // V: lane holds dims 8 vc .. 8 vc + 7 of keys vq + 4 j, j < 8 (one 16-byte
+  // load per key; an instruction reads 4 whole key rows)
   const int vc = lane & 15, vq = lane >> 4;
-  uint4 vw[kWideV ? 8 : 1];
-  uint32_t vr[kWideV ? 1 : kDecWaveKeys];
-  if constexpr (kWideV) {
+  uint4 vw[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const int key = max(min(c0 + vq + 4 * j, L - 1), 0);
-      vw[j] = *reinterpret_cast<const uint4*>(p.v + hbase + static_cast<int64_t>(key) * kD + 8 * vc);
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < kDecWaveKeys; k++) {
-      const int key = max(min(c0 + k, L - 1), 0);
-      vr[k] = *reinterpret_cast<const uint32_t*>(p.v + hbase + static_cast<int64_t>(key) * kD + 2 * lane);
-    }
+  for (int j = 0; j < 8; j++) {
+    const int key = max(min(c0 + vq + 4 * j, L - 1), 0);
+    vw[j] = *reinterpret_cast<const uint4*>(p.v + hbase + static_cast<int64_t>(key) * kD + 8 * vc);
   }
   if constexpr (FUSED) {
     // ---- fused prologue, part 2: norm + rope into LDS (and the caches) ----
@@ -303,18 +291,10 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
       }
     }
     if (t_hi > t_lo) {
-      if constexpr (kWideV) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const int tt = c0 + vq + 4 * j - offset;
-          if (tt >= t_lo && tt < t_hi) vw[j] = *reinterpret_cast<const uint4*>(&vn[tt][8 * vc]);
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < kDecWaveKeys; k++) {
-          const int tt = c0 + k - offset;
-          if (tt >= t_lo && tt < t_hi) vr[k] = *reinterpret_cast<const uint32_t*>(&vn[tt][2 * lane]);
-        }
+      for (int j = 0; j < 8; j++) {
+        const int tt = c0 + vq + 4 * j - offset;
+        if (tt >= t_lo && tt < t_hi) vw[j] = *reinterpret_cast<const uint4*>(&vn[tt][8 * vc]);
       }
     }
   }
@@ -356,88 +336,67 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   }
   __syncthreads();
   // ---- PV ----
-  // wide: lane sums its 8 keys for every (row, dim 8 vc + d), then the four
-  // key quarters (lane bits 4, 5) are added by two swap-and-add butterflies
+  // lane sums its 8 keys for every (row, dim 8 vc + d), then the four key
+  // quarters (lane bits 4, 5) are added by two swap-and-add butterflies
   // (v_permlane32_swap: X' = [X.lo, Y.lo], Y' = [X.hi, Y.hi];
   // v_permlane16_swap: X' = [X.r0, Y.r0, X.r2, Y.r2], Y' = [X.r1, Y.r1, X.r3,
-  // Y.r3] in 16-lane rows), which leave lane group vq with rows 4 i + vq;
-  // narrow: lane = dims 2 lane, 2 lane + 1 over the wave's 32 keys
-  float acc[RMAX][kWideV ? 8 : 2];
+  // Y.r3] in 16-lane rows), which leave lane group vq with rows 4 i + vq.
+  // Every row of every tile size takes the same sequence of operations, so a
+  // (token, head) row's output does not depend on how many rows share the
+  // launch: a verify row equals the single-token decode of the same position.
+  float acc[RMAX][8];
 #pragma unroll
   for (int r = 0; r < RMAX; r++)
 #pragma unroll
-    for (int d = 0; d < (kWideV ? 8 : 2); d++) acc[r][d] = 0.0f;
-  if constexpr (kWideV) {
+    for (int d = 0; d < 8; d++) acc[r][d] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      // rows past this split's keys (clamped or another split's) are never
-      // weighted, and are zeroed so that stale contents cannot be NaN
-      const uint4 vj = (c0 + vq + 4 * j < kend) ? vw[j] : make_uint4(0, 0, 0, 0);
-      const uint32_t w4[4] = {vj.x, vj.y, vj.z, vj.w};
-      float v[8];
+  for (int j = 0; j < 8; j++) {
+    // rows past this split's keys (clamped or another split's) are never
+    // weighted, and are zeroed so that stale contents cannot be NaN
+    const uint4 vj = (c0 + vq + 4 * j < kend) ? vw[j] : make_uint4(0, 0, 0, 0);
+    const uint32_t w4[4] = {vj.x, vj.y, vj.z, vj.w};
+    float v[8];
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        v[2 * e] = bf2f(w4[e] & 0xffffu);
-        v[2 * e + 1] = bf2f(w4[e] >> 16);
-      }
-#pragma unroll
-      for (int r4 = 0; r4 < RMAX; r4 += 4) {
-        const float4 pv = *reinterpret_cast<const float4*>(&ps[wave][vq + 4 * j][r4]);
-        const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-#pragma unroll
-          for (int d = 0; d < 8; d++) acc[r4 + q][d] += pr[q] * v[d];
-      }
+    for (int e = 0; e < 4; e++) {
+      v[2 * e] = bf2f(w4[e] & 0xffffu);
+      v[2 * e + 1] = bf2f(w4[e] >> 16);
     }
 #pragma unroll
-    for (int i = 0; i < RMAX / 4; i++)
+    for (int r4 = 0; r4 < RMAX; r4 += 4) {
+      const float4 pv = *reinterpret_cast<const float4*>(&ps[wave][vq + 4 * j][r4]);
+      const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
-      for (int d = 0; d < 8; d++) {
-        const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[4 * i][d]),
-                                                        __float_as_uint(acc[4 * i + 2][d]), false, false);
-        const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[4 * i + 1][d]),
-                                                        __float_as_uint(acc[4 * i + 3][d]), false, false);
-        const float r1 = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-        const float r2 = __uint_as_float(b[0]) + __uint_as_float(b[1]);
-        const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(r1), __float_as_uint(r2), false, false);
-        acc[i][d] = __uint_as_float(c[0]) + __uint_as_float(c[1]);  // row 4 i + vq, dim 8 vc + d
-      }
-  } else {
+      for (int q = 0; q < 4; q++)
 #pragma unroll
-    for (int k = 0; k < kDecWaveKeys; k++) {
-      const uint32_t vk = (c0 + k < kend) ? vr[k] : 0u;
-      const float v0 = bf2f(vk & 0xffffu), v1 = bf2f(vk >> 16);
-#pragma unroll
-      for (int r4 = 0; r4 < RMAX; r4 += 4) {
-        if (r4 >= RT) break;
-        const float4 pv = *reinterpret_cast<const float4*>(&ps[wave][k][r4]);
-        const float pr[4] = {pv.x, pv.y, pv.z, pv.w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          acc[r4 + q][0] += pr[q] * v0;
-          acc[r4 + q][1] += pr[q] * v1;
-        }
-      }
+        for (int d = 0; d < 8; d++) acc[r4 + q][d] += pr[q] * v[d];
     }
   }
+#pragma unroll
+  for (int i = 0; i < RMAX / 4; i++)
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+      const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[4 * i][d]),
+                                                      __float_as_uint(acc[4 * i + 2][d]), false, false);
+      const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[4 * i + 1][d]),
+                                                      __float_as_uint(acc[4 * i + 3][d]), false, false);
+      const float r1 = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+      const float r2 = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+      const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(r1), __float_as_uint(r2), false, false);
+      acc[i][d] = __uint_as_float(c[0]) + __uint_as_float(c[1]);  // row 4 i + vq, dim 8 vc + d
+    }
   // ---- merge the waves kMergeRows rows at a time; thread = (row, 4 dims) ----
 #pragma unroll
   for (int h0 = 0; h0 < RMAX; h0 += kMergeRows) {
     if (h0 >= RT) break;
     if (h0 > 0) __syncthreads();  // the previous pass has read os
-    if constexpr (kWideV) {  // RMAX <= kMergeRows: one pass
+    // rows h0 .. h0 + kMergeRows - 1 are the lane groups' rows of i = h0 / 4 ..
 #pragma unroll
-      for (int i = 0; i < RMAX / 4; i++) {
-        float* dst = &os[wave][4 * i + vq][8 * vc];
+    for (int i2 = 0; i2 < kMergeRows / 4; i2++) {
+      const int i = h0 / 4 + i2;
+      if (i < RMAX / 4) {
+        float* dst = &os[wave][4 * i2 + vq][8 * vc];
         *reinterpret_cast<float4*>(dst) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
         *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < kMergeRows && r < RMAX; r++) {
-        if (h0 + r >= RT) break;
-        *reinterpret_cast<float2*>(&os[wave][r][2 * lane]) = make_float2(acc[h0 + r][0], acc[h0 + r][1]);
       }
     }
     __syncthreads();
@@ -475,15 +434,18 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
   __syncthreads();
   if (threadIdx.x == 0) {
-    // wraps to 0 on the ns-th arrival, ready for the next call
-    last = atomicInc(p.cnt + kvh * gridDim.z + blockIdx.z, static_cast<unsigned>(p.ns - 1)) ==
-           static_cast<unsigned>(p.ns - 1);
+    // Arrival: an agent-scope acquire-release increment that wraps to 0 on
+    // the ns-th arrival (ready for the next call).  Release publishes this
+    // workgroup's partials (stored by all its threads before the barrier);
+    // the last arrival's acquire makes every other workgroup's partials
+    // visible to the merge below (its threads read after the next barrier).
+    last = __builtin_amdgcn_atomic_inc32(p.cnt + kvh * gridDim.z + blockIdx.z, static_cast<unsigned>(p.ns - 1),
+                                         __ATOMIC_ACQ_REL, "agent") == static_cast<unsigned>(p.ns - 1);
   }
   __syncthreads();
   if (!last) return;
-  // every partial of the pair completed before its workgroup's arrival.  (Two
-  // waves per row, each folding half of the splits and merged through LDS,
-  // measured 2% slower end to end.)
+  // (Two waves per row, each folding half of the splits and merged through
+  // LDS, measured 2% slower end to end.)
   for (int r = wave; r < RT; r += kDecWaves)
     store_pair(p, kvh * R + r0 + r, lane, combine_range(p, kvh * R + r0 + r, lane, 0, p.ns));
 }

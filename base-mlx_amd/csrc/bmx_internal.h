@@ -101,6 +101,21 @@ size_t qmvx_workspace_floats(int N, int K);
 // (device, stream) pair, grown on demand (growing synchronizes the stream);
 // work on one stream runs in order, so its launches may share it.
 int stream_scratch(size_t floats, hipStream_t stream, float** out);
+// Split-K partials of `need` floats: the caller's workspace ws when given
+// (an error when it holds fewer than `need`), else -- unless a NoAllocScope
+// is active on this thread, which makes it an error -- stream_scratch.
+int split_scratch(size_t need, float* ws, size_t ws_floats, hipStream_t stream, float** out);
+// While an object of this type lives, split_scratch never allocates on the
+// calling thread (entry points that must not allocate).
+struct NoAllocScope {
+  NoAllocScope();
+  ~NoAllocScope();
+  NoAllocScope(const NoAllocScope&) = delete;
+  NoAllocScope& operator=(const NoAllocScope&) = delete;
+};
+// Split-K partial floats one GEMM call of this epilogue and shape uses (0
+// when K is not split).
+size_t qmm_need_floats(QmmEpilogue epi, int M, int N, int K);
 int launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t rows, int dim, float eps,
                     hipStream_t stream);
 struct RopeTable {

@@ -262,6 +262,26 @@ int stream_scratch(size_t floats, hipStream_t stream, float** out) {
 }
 
 namespace {
+thread_local int g_no_alloc_depth = 0;
+}
+
+NoAllocScope::NoAllocScope() { g_no_alloc_depth++; }
+NoAllocScope::~NoAllocScope() { g_no_alloc_depth--; }
+
+int split_scratch(size_t need, float* ws, size_t ws_floats, hipStream_t stream, float** out) {
+  if (ws) {
+    if (ws_floats < need)
+      return set_error(BMX_E_ARG, "workspace of %zu bytes is too small: this shape needs %zu",
+                       ws_floats * sizeof(float), need * sizeof(float));
+    *out = ws;
+    return BMX_OK;
+  }
+  if (g_no_alloc_depth > 0)
+    return set_error(BMX_E_ARG, "this shape needs a workspace of %zu bytes", need * sizeof(float));
+  return stream_scratch(need, stream, out);
+}
+
+namespace {
 
 // K splits of an M x N x K product: split while the tiles leave most of the
 // device idle (splits of at least 8 groups, a multiple of 8 groups each).
@@ -277,6 +297,13 @@ void qmm_split(int M, int N, int K, int* splits_out, int* gps_out, int cols_per_
 }
 
 }  // namespace
+
+size_t qmm_need_floats(QmmEpilogue epi, int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  int splits, gps;
+  qmm_split(M, N, K, &splits, &gps, epi == QMM_SWIGLU ? QBN / 2 : QBN);
+  return splits > 1 ? static_cast<size_t>(splits) * M * N : 0;
+}
 
 size_t qmm_workspace_floats(int max_M, int N, int K) {
   size_t need = 0;
@@ -305,12 +332,7 @@ int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const 
   if (epi == QMM_SWIGLU && splits > 1) return kNoFit;
   QmmParams p{x, w, s, b, w2, s2, b2, res, y, nullptr, M, N, K, gps};
   if (splits > 1) {
-    const size_t need = static_cast<size_t>(splits) * M * N;
-    if (ws && ws_floats >= need) {
-      p.part = ws;
-    } else if (int rc = stream_scratch(need, stream, &p.part)) {
-      return rc;
-    }
+    if (int rc = split_scratch(static_cast<size_t>(splits) * M * N, ws, ws_floats, stream, &p.part)) return rc;
   }
   const dim3 grid((N + cols - 1) / cols, (M + QBM - 1) / QBM, splits);
   auto launch = [&](auto kern) {

@@ -629,10 +629,10 @@ int launch_qmv1_ni(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_
 // within kXU1 units per thread, s|b within one unit per thread); returns -1
 // otherwise.
 int try_launch_qmv1(QmvEpilogue epi, int S, const QmvParams& p, int blocks, hipStream_t st) {
-  if (p.m != 1 || p.kp < p.K || !p.sb_vec || p.K / 8 > kThreads * kXU1) return -1;
+  if (p.m != 1 || p.kp < p.K || !p.sb_vec || p.K / 8 > kThreads * kXU1) return kNoFit;
   const int C = p.K / 32, G = p.K / 64;
   const int RB = 4 * (64 / S);
-  if (RB * (G / 8) > kThreads) return -1;
+  if (RB * (G / 8) > kThreads) return kNoFit;
   const int ni = (C + S - 1) / S;
   const int nh = epi == QMV_SWIGLU ? 2 : 1;
   const size_t lds = static_cast<size_t>(C) * (kChunkBytes + 4) + static_cast<size_t>(nh) * RB * G * 4 + 16 +
@@ -643,7 +643,7 @@ int try_launch_qmv1(QmvEpilogue epi, int S, const QmvParams& p, int blocks, hipS
   if (ni <= 8) return launch_qmv1_ni<8>(epi, S, p, blocks, lds, st);
   if (nh == 1 && ni <= 10) return launch_qmv1_ni<10>(epi, S, p, blocks, lds, st);
   if (nh == 1 && ni <= 16) return launch_qmv1_ni<16>(epi, S, p, blocks, lds, st);
-  return -1;
+  return kNoFit;
 }
 
 // Persistent GEMV for M <= 8 rows of x with the whole K in LDS.  About two
@@ -1021,7 +1021,7 @@ int launch_qmvp_ni(int ni, int nh, QmvEpilogue epi, int S, const QmvParams& p, i
   if (ni <= 3) return launch_qmvp_epi<MT, 3>(epi, S, p, ntiles, grid, lds, st);
   if (ni <= 5) return launch_qmvp_epi<MT, 5>(epi, S, p, ntiles, grid, lds, st);
   if (nh == 1 && ni <= 10) return launch_qmvp_epi<MT, 10>(epi, S, p, ntiles, grid, lds, st);
-  return -1;
+  return kNoFit;
 }
 
 // Launches the persistent GEMV when it applies (whole K in LDS, 16-byte s|b
@@ -1032,18 +1032,17 @@ int launch_qmvp_ni(int ni, int nh, QmvEpilogue epi, int S, const QmvParams& p, i
 constexpr int kPersistentRows = 65536;
 
 int try_launch_qmvp(QmvEpilogue epi, int mt, int S, const QmvParams& p, int ntiles, hipStream_t st) {
-  if (!p.sb_vec) return -1;
-  if (mt == 1 && p.K / 8 > kThreads * 5) return -1;
+  if (!p.sb_vec) return kNoFit;
+  if (mt == 1 && p.K / 8 > kThreads * 5) return kNoFit;
   const int C = p.K / 32, G = p.K / 64;
   const int RB = 4 * (64 / S);
-  if (RB * (G / 8) > kThreads) return -1;
+  if (RB * (G / 8) > kThreads) return kNoFit;
   const int ni = (C + S - 1) / S;
   const int nh = epi == QMV_SWIGLU ? 2 : 1;
   const size_t lds = static_cast<size_t>(mt) * C * (kChunkBytes + 4) + 2ull * nh * RB * G * 4 +
                      4ull * mt * 4 + 32;
-  if (lds > 150 * 1024) return -1;
-  static const int env_grid = getenv("BMX_QMV_GRID") ? std::max(1, atoi(getenv("BMX_QMV_GRID"))) : 0;
-  int grid = env_grid ? env_grid : (mt == 1 ? 512 : 256);
+  if (lds > 150 * 1024) return kNoFit;
+  int grid = mt == 1 ? 512 : 256;
   grid = std::min(grid, ntiles);
   switch (mt) {
     case 1: return launch_qmvp_ni<1>(ni, nh, epi, S, p, ntiles, grid, lds, st);
@@ -1109,19 +1108,14 @@ struct QmvGrid {
   int blk0[3];
 };
 
-// Tile shape and grid of one launch: lanes per row S (tuning override
-// BMX_QMV_LANES = 8/16/32/64), rows per workgroup, and the first workgroup of
+// Tile shape and grid of one launch: lanes per row S, rows per workgroup,
+// and the first workgroup of
 // each segment (segments start on workgroup boundaries; SWIGLU's two
 // matrices share every workgroup).
 QmvGrid qmv_grid(const QmvParams& p, QmvEpilogue epi) {
   QmvGrid g{};
   g.mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : p.m <= 5 ? 5 : 8;
   g.S = (g.mt == 1) ? pick_lanes_per_row(p.N, p.K) : (p.K / 32 >= 64 ? 64 : 16);
-  static const int env_lanes = getenv("BMX_QMV_LANES") ? atoi(getenv("BMX_QMV_LANES")) : 0;
-  {
-    const int v = env_lanes;
-    if (v == 16 || v == 64 || (g.mt == 1 && (v == 8 || v == 32))) g.S = v;
-  }
   g.rows_per_block = (kThreads / 64) * (64 / g.S);
   if (epi == QMV_SWIGLU) {
     g.blocks = (p.N + g.rows_per_block - 1) / g.rows_per_block;
@@ -1176,23 +1170,20 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
     p.sb_vec = p.sb_vec && aligned(p.seg[i].s, 16) && aligned(p.seg[i].b, 16);
   // kernel choice: matrix cores for 2..8 rows of x; for one row the
   // persistent kernel on the vocabulary-sized projection, the single-phase
-  // GEMV elsewhere (BMX_QMV_NO_MFMA / BMX_QMV_NO_PERSISTENT switch the first
-  // two off for comparison)
-  static const bool no_mfma = getenv("BMX_QMV_NO_MFMA") != nullptr;
-  static const bool no_persistent = getenv("BMX_QMV_NO_PERSISTENT") != nullptr;
-  if (mt >= 2 && !no_mfma) {
+  // GEMV elsewhere
+  if (mt >= 2) {
     const int rc = try_launch_qmvx(p, epi, stream);
-    if (rc >= 0) return rc;
+    if (rc != kNoFit) return rc;
   }
   int rows_total = 0;
   for (int i = 0; i < p.nseg; i++) rows_total += p.seg[i].rows;
-  if (mt == 1 && !no_persistent && rows_total >= kPersistentRows) {
+  if (mt == 1 && rows_total >= kPersistentRows) {
     const int rc = try_launch_qmvp(epi, mt, S, p, blocks, stream);
-    if (rc >= 0) return rc;
+    if (rc != kNoFit) return rc;
   }
   if (mt == 1) {
     const int rc = try_launch_qmv1(epi, S, p, blocks, stream);
-    if (rc >= 0) return rc;
+    if (rc != kNoFit) return rc;
   }
   switch (mt) {
     case 1: return launch_epi<1>(epi, S, p, blocks, lds, stream);

@@ -93,17 +93,16 @@ size_t qmvx_workspace_floats(int N, int K) {
 }
 
 int try_launch_qmvx(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
-  if (p.m < 2 || p.m > 8 || p.amax) return -1;
-  if (p.K % 512 || !p.sb_vec) return -1;  // s|b in 16-byte units of 8 groups
+  if (p.m < 2 || p.m > 8 || p.amax) return kNoFit;
+  if (p.K % 512 || !p.sb_vec) return kNoFit;  // s|b in 16-byte units of 8 groups
   const int mt = p.m <= 2 ? 2 : p.m <= 4 ? 4 : p.m <= 5 ? 5 : 8;
   const int G = p.K / 64;
   const int nh = epi == QMV_SWIGLU ? 2 : 1;
 
   // ---- K split over workgroups: no fused norm, no SwiGLU, long rows of a
   // large matrix -- below that the x restaging it saves costs less than its
-  // reduction launch (tuning switch BMX_QMVX_NO_SPLIT turns it off) ----
-  static const bool no_split = getenv("BMX_QMVX_NO_SPLIT") != nullptr;
-  if (!no_split && epi != QMV_SWIGLU && !p.norm_w && p.K >= kSplitMinK &&
+  // reduction launch ----
+  if (epi != QMV_SWIGLU && !p.norm_w && p.K >= kSplitMinK &&
       static_cast<int64_t>(p.N) * p.K >= kSplitMinWeights) {
     int tiles = 0;
     for (int i = 0; i < p.nseg; i++) {
@@ -114,9 +113,7 @@ int try_launch_qmvx(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
     if (split_shape(tiles, G, &sh)) {
       const size_t lds = shape_lds(mt, 1, sh);
       const size_t need = static_cast<size_t>(sh.nkc) * p.m * sh.nts * 16;
-      if (!(p.part && p.part_floats >= need)) {
-        if (int rc = stream_scratch(need, stream, &p.part)) return rc;
-      }
+      if (int rc = split_scratch(need, p.part, p.part_floats, stream, &p.part)) return rc;
       if (int rc = launch_mt_any(mt, kSplit, epi, p, sh, lds, stream)) return rc;
       const int ntr = sh.nts * 16;
       hipLaunchKernelGGL(qmvx_reduce_kernel, dim3((p.m * ntr + 255) / 256), dim3(256), 0, stream, p, sh.nkc, ntr,
@@ -133,7 +130,7 @@ int try_launch_qmvx(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
     nkc = std::max((mt * G * 8 + kXU * kThreads - 1) / (kXU * kThreads), (G + kMaxChunkKC - 1) / kMaxChunkKC);
   const int KC = ((G + nkc - 1) / nkc + 7) / 8 * 8;
   nkc = (G + KC - 1) / KC;
-  if (nkc > 1 && (p.norm_w || epi == QMV_SWIGLU)) return -1;
+  if (nkc > 1 && (p.norm_w || epi == QMV_SWIGLU)) return kNoFit;
   auto tile_sets = [&](int tb) {
     if (epi == QMV_SWIGLU) return (p.N + 16 * tb - 1) / (16 * tb);
     int n = 0;
@@ -153,9 +150,9 @@ int try_launch_qmvx(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   sh.KC = KC;
   sh.nkc = nkc;
   sh.npc = (KC / 2 + SK - 1) / SK;
-  if (sh.npc > np_max) return -1;
+  if (sh.npc > np_max) return kNoFit;
   const int RW = 16 * sh.TB;
-  if (nh * 2 * RW * (KC / 8) > kSBU * kThreads) return -1;
+  if (nh * 2 * RW * (KC / 8) > kSBU * kThreads) return kNoFit;
   // tile-sets; segments start on tile-set boundaries
   if (epi == QMV_SWIGLU) {
     sh.nts = tile_sets(sh.TB);
@@ -168,7 +165,7 @@ int try_launch_qmvx(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
     }
   }
   const size_t lds = shape_lds(mt, nh, sh);
-  if (lds > 160 * 1024) return -1;
+  if (lds > 160 * 1024) return kNoFit;
   return launch_mt_any(mt, nkc > 1 ? kChunked : kOneChunk, epi, p, sh, lds, stream);
 }
 

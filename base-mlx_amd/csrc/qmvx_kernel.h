@@ -505,7 +505,7 @@ int launch_epi(QmvEpilogue epi, const QmvParams& p, const Shape& sh, size_t lds,
     case QMV_RESIDUAL: k = reinterpret_cast<const void*>(qmvx_kernel<MT, NP, QMV_RESIDUAL, CHUNK, SPLIT>); break;
     default:
       // SwiGLU carries the norm (one chunk) and two matrices (at most 8 pairs)
-      if constexpr (CHUNK || SPLIT || NP > 8) return -1;
+      if constexpr (CHUNK || SPLIT || NP > 8) return kNoFit;
       else k = reinterpret_cast<const void*>(qmvx_kernel<MT, NP, QMV_SWIGLU, false, false>);
   }
   if (int rc = allow_lds_ptr(k, lds)) return rc;

@@ -705,8 +705,12 @@ extern "C" int bmx_speculative_generate(bmx_qwen3* target, bmx_kv_cache* tc, bmx
   *n_out = 0;
   if (draft->cfg.vocab != target->cfg.vocab)  // check_compatible, speculative.rs:40-54
     return set_error(BMX_E_ARG, "draft/target vocab mismatch: target=%d draft=%d", target->cfg.vocab, draft->cfg.vocab);
+  if (P <= 0 || max_new <= 0) return set_error(BMX_E_ARG, "speculative: P=%d max_new=%d", P, max_new);
   if (spec_k < 2 || spec_k > 8) return set_error(BMX_E_ARG, "speculative: spec_k=%d outside 2..8", spec_k);
   if (spec_k > target->max_tokens) return set_error(BMX_E_SHAPE, "speculative: spec_k > target max_tokens");
+  // the caches may already hold context (a continued conversation): every
+  // rewind below is relative to where each one starts
+  const int t0 = tc->seq_len, d0 = dc->seq_len;
   hipStream_t st = pick_stream(target, stream);
   int64_t iters = 0, proposed = 0, accepted = 0;
   int n = 0, rc = BMX_OK;
@@ -773,8 +777,8 @@ extern "C" int bmx_speculative_generate(bmx_qwen3* target, bmx_kv_cache* tc, bmx
     if (stop || n >= max_new || is_eos(bonus, eos, n_eos)) break;
     out[n++] = bonus;
     // rewind both caches to prompt + emitted - 1 (:227, :234), keeping the buffers
-    bmx_kv_truncate(tc, P + n - 1);
-    bmx_kv_truncate(dc, P + n - 1);
+    bmx_kv_truncate(tc, t0 + P + n - 1);
+    bmx_kv_truncate(dc, d0 + P + n - 1);
     leader = bonus;
     if ((rc = graph_step(draft, dc, st, leader, &dnext))) goto done;  // :238-239
   }

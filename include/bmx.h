@@ -49,23 +49,46 @@ int bmx_abi_version(void);
 /* Quantized matmul                                                    */
 /* ------------------------------------------------------------------ */
 
-/* y[M,N] = x[M,K] . dequant(w, scales, biases)^T   (transpose = true)
+/* y[M,N] = x[M,K] . dequant(w, scales, biases)^T   (transpose != 0)
  * w: [N, K*bits/32] uint32; scales, biases: [N, K/group_size] bf16;
- * x, y bf16; fp32 accumulation.  bits must be 4 and group_size 64.
- * M <= 8 runs the streaming GEMV (qmv); larger M the MFMA GEMM (qmm).
- * x and w must be 16-byte aligned.
+ * x, y bf16; fp32 accumulation.  bits must be 4 and group_size 64;
+ * transpose = 0 (W stored [K, N]) is BMX_E_UNSUPPORTED -- every call of the
+ * reference passes true.  M <= 8 runs the streaming GEMV (qmv); larger M
+ * the MFMA GEMM (qmm).  x and w must be 16-byte aligned.
  * Shapes that split K over workgroups (small GEMM grids; GEMVs of 2..8 rows
  * with K >= 8192) keep fp32 partials in a device buffer the library owns
  * per (device, stream), allocated or grown on first use of a larger shape
  * on that stream (which synchronizes the stream): the first call of a
- * shape on a stream must not be inside graph capture.
- * Replaces: mlx_rs::ops::quantized_matmul(x, w, scales, biases, true, 64, 4)
- *   as called by QLinear::forward (crates/base-mlx-core/src/model/qwen3.rs:30-41),
+ * shape on a stream must not be inside graph capture.  Callers that must
+ * not allocate use bmx_qmatmul_affine_ws.
+ * Replaces: mlx_rs::ops::quantized_matmul(x, w, scales, biases, transpose,
+ *   group_size, bits) -- mlx-c's mlx_quantized_matmul(res, x, w, scales,
+ *   biases, transpose, group_size, bits, stream) -- as called by
+ *   QLinear::forward (crates/base-mlx-core/src/model/qwen3.rs:30-41),
  *   QEmbedding::lm_head (qwen3.rs:80-91) and qkv_block / mlp_block
  *   (crates/base-mlx-core/src/model/kernels.rs:42-44, 69-75). */
 int bmx_qmatmul_affine(const bmx_bf16 *x, const uint32_t *w, const bmx_bf16 *scales,
                        const bmx_bf16 *biases, bmx_bf16 *y, int64_t M, int64_t N, int64_t K,
-                       int group_size, int bits, void *stream);
+                       int transpose, int group_size, int bits, void *stream);
+
+/* Bytes of split-K workspace bmx_qmatmul_affine_ws needs for an M x N x K
+ * call (0: the shape does not split K, any workspace or NULL will do).
+ * Host only.
+ * Replaces: nothing in the reference (MLX sizes its temporaries itself);
+ *   the companion of bmx_qmatmul_affine_ws. */
+size_t bmx_qmatmul_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/* bmx_qmatmul_affine with the split-K partials in the caller's workspace
+ * (device memory, 16-byte aligned, at least bmx_qmatmul_workspace_bytes(M,
+ * N, K) bytes, else BMX_E_ARG and nothing enqueued).  It never allocates or
+ * synchronizes, so it may be captured into a graph on any call.  Calls that
+ * share a workspace must not run concurrently.
+ * Replaces: the same quantized_matmul calls as bmx_qmatmul_affine
+ *   (crates/base-mlx-core/src/model/qwen3.rs:30-41, 80-91). */
+int bmx_qmatmul_affine_ws(const bmx_bf16 *x, const uint32_t *w, const bmx_bf16 *scales,
+                          const bmx_bf16 *biases, bmx_bf16 *y, int64_t M, int64_t N, int64_t K,
+                          int transpose, int group_size, int bits, void *workspace, size_t workspace_bytes,
+                          void *stream);
 
 /* Routed (MoE expert) quantized matmul: w [n_experts, N, K/8] u32, scales /
  * biases [n_experts, N, K/64] bf16; for route r < n_routes,

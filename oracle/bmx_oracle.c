@@ -853,7 +853,10 @@ int orc_speculative_generate(orc_qwen3 *target, orc_kv *tkv, orc_qwen3 *draft,
   const int V = target->cfg.vocab;
   *n_out = 0;
   if (draft->cfg.vocab != V) return ORC_E_ARG; /* check_compatible, speculative.rs:40-54 */
-  if (spec_k < 2 || spec_k > 16) return ORC_E_ARG;
+  if (spec_k < 2 || spec_k > 16 || P <= 0 || max_new <= 0) return ORC_E_ARG;
+  /* the reference starts from fresh caches (speculative.rs:71-72); caches
+   * that already hold context are rewound relative to where they start */
+  const int t0 = orc_kv_seq_len(tkv), d0 = orc_kv_seq_len(dkv);
   uint16_t *tl = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)V * (size_t)spec_k);
   uint16_t *dl = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)V);
   int64_t iters = 0, proposed = 0, accepted = 0;
@@ -914,8 +917,8 @@ int orc_speculative_generate(orc_qwen3 *target, orc_kv *tkv, orc_qwen3 *draft,
     if (stop || n >= max_new || is_eos(bonus, eos, n_eos)) break;
     out[n++] = bonus;
     /* rewind both caches to prompt + emitted - 1 (:227, :234) */
-    orc_kv_truncate(tkv, P + n - 1);
-    orc_kv_truncate(dkv, P + n - 1);
+    orc_kv_truncate(tkv, t0 + P + n - 1);
+    orc_kv_truncate(dkv, d0 + P + n - 1);
     leader = bonus;
     rc = orc_qwen3_forward(draft, dkv, &leader, 1, 0, dl); /* :238-239 */
     if (rc) goto done;
