@@ -234,3 +234,34 @@ def test_qmm_vs_oracle(gpu, orc, M, N, K):
     # the matrix path of the oracle (bf16-dequantized weights, fp32
     # accumulation): within 2 bf16 ulps of it
     assert _close(yb, orc.qmm_dequant(xb, wq, sb, bb), ulps=2, floor=1e-4) == 1.0
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 1024, 2560), (24, 768, 2048), (5, 5120, 8192), (1, 4096, 2560)])
+def test_qmatmul_ws_matches_qmatmul(gpu, M, N, K):
+    """bmx_qmatmul_affine_ws with a workspace of exactly
+    bmx_qmatmul_workspace_bytes(M, N, K) bytes gives the bits of
+    bmx_qmatmul_affine (same kernels, caller-owned partials), and also when
+    captured into a graph and replayed."""
+    import torch
+
+    print(f"qmatmul_ws M={M} N={N} K={K}", flush=True)
+    w, s, b = gpu.init_qlinear(310 + M, N, K)
+    x = gpu.fill_normal_bf16(410 + M, (M, K))
+    need = gpu.qmatmul_workspace_bytes(M, N, K)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda") if need else None
+    ref = gpu.quantized_matmul(x, w, s, b)
+    got = gpu.quantized_matmul_ws(x, w, s, b, ws)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(torch_bf16_bits(got), torch_bf16_bits(ref))
+    st = torch.cuda.Stream()
+    out = torch.empty_like(ref)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            gpu.quantized_matmul_ws(x, w, s, b, ws, out=out)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(torch_bf16_bits(out), torch_bf16_bits(ref))
