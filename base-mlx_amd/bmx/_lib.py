@@ -59,6 +59,7 @@ SIGNATURES = {
     "bmx_abi_version": (c_int, []),
     "bmx_qmatmul_affine": (c_int, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_p]),
     "bmx_qmatmul_workspace_bytes": (ctypes.c_size_t, [c_i64, c_i64, c_i64]),
+    "bmx_qmatmul_affine_noalloc": (c_int, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_p]),
     "bmx_qmatmul_affine_ws": (c_int, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_p,
                                       ctypes.c_size_t, c_p]),
     "bmx_dequantize_affine": (c_int, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_int, c_int, c_p]),

@@ -126,3 +126,56 @@ extern "C" int bmx_qmatmul_affine_ws(const bmx_bf16* x, const uint32_t* w, const
   return qmatmul(x, w, scales, biases, y, M, N, K, transpose, group_size, bits, static_cast<float*>(workspace),
                  workspace_bytes / sizeof(float), as_stream(stream));
 }
+
+// ---------------------------------------------------------------------------
+// bmx_qmatmul_affine_noalloc: the split-K partials live in `scratch`, a
+// file-scope device array of kScratchBytes that every device the library
+// runs on holds from module load until the process ends.  Host code never
+// uses the array's name as an address: its per-device address comes from
+// hipGetSymbolAddress, taken once per device (with that device current) at
+// the entry point's first call there.  Every split-K launch writes each
+// partial it later reads, so nothing in the array needs clearing between
+// calls; calls that overlap on one device share the array and race.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kScratchBytes = size_t{16} << 20;  // 16 MiB
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+int device_scratch(float** out) {
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "noalloc: hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return set_error(BMX_E_ARG, "noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (int rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "noalloc: hipGetSymbolAddress")) return rc;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return BMX_OK;
+}
+
+}  // namespace
+
+extern "C" int bmx_qmatmul_affine_noalloc(const bmx_bf16* x, const uint32_t* w, const bmx_bf16* scales,
+                                          const bmx_bf16* biases, bmx_bf16* y, int64_t M, int64_t N, int64_t K,
+                                          int transpose, int group_size, int bits, void* stream) {
+  const size_t need = bmx_qmatmul_workspace_bytes(M, N, K);
+  if (need > kScratchBytes)
+    return set_error(BMX_E_SHAPE, "qmatmul_noalloc: M=%lld N=%lld K=%lld needs %zu bytes of split-K scratch, "
+                     "above the %zu-byte maximum",
+                     (long long)M, (long long)N, (long long)K, need, kScratchBytes);
+  float* ptr = nullptr;
+  if (need > 0) {
+    if (int rc = device_scratch(&ptr)) return rc;
+  }
+  NoAllocScope no_alloc;
+  return qmatmul(x, w, scales, biases, y, M, N, K, transpose, group_size, bits, ptr,
+                 ptr ? kScratchBytes / sizeof(float) : 0, as_stream(stream));
+}

@@ -90,6 +90,20 @@ int bmx_qmatmul_affine_ws(const bmx_bf16 *x, const uint32_t *w, const bmx_bf16 *
                           int transpose, int group_size, int bits, void *workspace, size_t workspace_bytes,
                           void *stream);
 
+/* bmx_qmatmul_affine with the split-K partials in a scratch array of the
+ * library's own (a file-scope device array of 16 MiB that each GPU the
+ * library runs on holds until the process ends): no allocation, no caller
+ * workspace, no synchronization.  A shape whose partials need more than
+ * 16 MiB (bmx_qmatmul_workspace_bytes) is BMX_E_SHAPE.  All calls on one
+ * GPU share the array, so calls that overlap on one GPU (concurrent
+ * streams, threads) race; serialise them.
+ * No counterpart in the reference: for callers that cannot allocate or
+ * manage a workspace (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). */
+int bmx_qmatmul_affine_noalloc(const bmx_bf16 *x, const uint32_t *w, const bmx_bf16 *scales,
+                               const bmx_bf16 *biases, bmx_bf16 *y, int64_t M, int64_t N, int64_t K,
+                               int transpose, int group_size, int bits, void *stream);
+
 /* Routed (MoE expert) quantized matmul: w [n_experts, N, K/8] u32, scales /
  * biases [n_experts, N, K/64] bf16; for route r < n_routes,
  *   out[r] [M, N] = x[r / x_bcast] [M, K] . W[rhs_indices[r]]^T

@@ -1,0 +1,56 @@
+"""bmx_qmatmul_affine_noalloc (split-K partials in the library's static
+device scratch) against bmx_qmatmul_affine (the same kernels with a
+library-allocated buffer): bit-identical outputs on two calls in a row,
+the second smaller, through the C ABI."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from _util import torch_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _call(gpu, name, x, w, s, b, M, N, K):
+    import torch
+
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    gpu.call(name, x.data_ptr(), w.data_ptr(), s.data_ptr(), b.data_ptr(), y.data_ptr(), M, N, K, 1, 64, 4,
+             ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    return y
+
+
+@pytest.mark.parametrize("shapes", [
+    # split-K GEMMs (small tile grids), the second call smaller
+    [(64, 1024, 2560), (24, 768, 2048)],
+    # GEMVs of 5 rows with K >= 8192, then a GEMM that splits K
+    [(5, 5120, 8192), (16, 512, 1024)],
+])
+def test_noalloc_matches_qmatmul(gpu, shapes):
+    import torch
+
+    lib = gpu.load()
+    for i, (M, N, K) in enumerate(shapes):
+        print(f"noalloc case M={M} N={N} K={K}", flush=True)
+        need = lib.bmx_qmatmul_workspace_bytes(M, N, K)
+        assert 0 < need <= 16 << 20, need
+        w, s, b = gpu.init_qlinear(300 + i, N, K)
+        x = gpu.fill_normal_bf16(400 + i, (M, K))
+        ref = _call(gpu, "bmx_qmatmul_affine", x, w, s, b, M, N, K)
+        got = _call(gpu, "bmx_qmatmul_affine_noalloc", x, w, s, b, M, N, K)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(torch_bf16_bits(got), torch_bf16_bits(ref))
+
+
+def test_noalloc_rejects_shapes_beyond_its_scratch(gpu):
+    """A shape whose split-K partials exceed the 16 MiB scratch is refused
+    before anything is enqueued (the pointers below are never read)."""
+    lib = gpu.load()
+    M, N, K = 8, 66048, 32768
+    need = lib.bmx_qmatmul_workspace_bytes(M, N, K)
+    if need <= 16 << 20:
+        pytest.skip(f"M={M} N={N} K={K} needs only {need} bytes of partials")
+    fake = ctypes.c_void_p(0x1000)
+    rc = lib.bmx_qmatmul_affine_noalloc(fake, fake, fake, fake, fake, M, N, K, 1, 64, 4, ctypes.c_void_p(0))
+    assert rc == gpu.BMX_E_SHAPE and "16777216" in gpu.last_error()
