@@ -462,8 +462,9 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
 //     as its 8-wide k slice in that order;
 //   O += P V with B = V^T from LDS, staged transposed (4 keys x 8 dims per
 //     thread, transposed in registers) so that the same 8 keys are two
-//     8-byte reads.  p is rounded to bf16 for the product (and the row sums
-//     add the rounded values); O and the softmax statistics stay fp32.  The
+//     8-byte reads.  p stays fp32: it enters the product as three bf16
+//     terms (three MFMAs), and the row sums add it unrounded; O and the
+//     softmax statistics are fp32.  The
 //     softmax runs in base 2 (v_exp_f32 on scores pre-multiplied by log2 e),
 //     and O is rescaled only in blocks where some row's running max moved.
 // The K and V^T tiles are double-buffered: the loads of key block j+1 are
@@ -629,20 +630,34 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     // row with nothing visible yet keeps m = -inf and is skipped
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    // p in fp32, carried to the matrix cores as three bf16 terms p = hi + mid
+    // + lo (each the bf16 rounding of what the terms before it leave; every
+    // difference is exact in fp32), so P V sees p to ~2^-27 of itself -- as
+    // if p stayed fp32 -- and the row sum adds the unrounded p.  (Two terms
+    // leave ~2^-18 of p, which through softmax cancellation flips ~0.2% of
+    // the bf16 outputs against an fp32 reference.)
     float sum = 0.0f;
-    bf16x8_t pa[2];
+    bf16x8_t pa[3][2];
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-      uint32_t pw[4];
+      uint32_t pw[3][4];
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int kt = 2 * c + (u >> 1), i0 = 2 * (u & 1);
-        const uint16_t b0 = f2bf(__builtin_amdgcn_exp2f(sc[kt][i0] - m_use));
-        const uint16_t b1 = f2bf(__builtin_amdgcn_exp2f(sc[kt][i0 + 1] - m_use));
-        sum += bf2f(b0) + bf2f(b1);
-        pw[u] = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
+        float r0 = __builtin_amdgcn_exp2f(sc[kt][i0] - m_use);
+        float r1 = __builtin_amdgcn_exp2f(sc[kt][i0 + 1] - m_use);
+        sum += r0 + r1;
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+          const uint16_t b0 = f2bf(r0), b1 = f2bf(r1);
+          pw[t][u] = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
+          r0 -= bf2f(b0);
+          r1 -= bf2f(b1);
+        }
       }
-      pa[c] = __builtin_bit_cast(bf16x8_t, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+#pragma unroll
+      for (int t = 0; t < 3; t++)
+        pa[t][c] = __builtin_bit_cast(bf16x8_t, make_uint4(pw[t][0], pw[t][1], pw[t][2], pw[t][3]));
     }
     sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
@@ -670,7 +685,8 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
         const uint2 v0 = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * c + g) ^ sw));
         const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * c + 4 + g) ^ sw));
         const bf16x8_t bv = __builtin_bit_cast(bf16x8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
-        o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[c], bv, o[j], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 3; t++) o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[t][c], bv, o[j], 0, 0, 0);
       }
     if (more) store_block(P == 0 ? sg1 : sg0, buf ^ 1);
     __syncthreads();

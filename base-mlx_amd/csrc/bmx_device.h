@@ -69,6 +69,71 @@ __device__ __forceinline__ float word_dot(uint32_t w, uint4 xp, float acc, const
   return acc;
 }
 
+// ---- Per-row arithmetic of the GEMV kernels (qmv.hip) --------------------
+// Every GEMV kernel of 1..8 rows of x (single-phase, persistent, phased)
+// computes each row with exactly these operations, in this order, written
+// with explicit fused multiply-adds so that no kernel's code generation can
+// contract them differently.  With the same lanes per weight row (a
+// function of N and K only) and the same chunk -> lane assignment (chunk c
+// to lane c mod S, in increasing c), a row's output is therefore the same
+// bits whatever the number of rows of x in the launch: a speculative-verify
+// row equals the single-token decode of that position.
+
+// Sum of squares of 8 bf16 values (one 16-byte unit of x), added to ss.
+__device__ __forceinline__ float gemv_ss_unit(uint4 d, float ss) {
+  const uint32_t v[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const float lo = bf2f(v[q] & 0xffffu), hi = bf2f(v[q] >> 16);
+    ss = __builtin_fmaf(lo, lo, ss);
+    ss = __builtin_fmaf(hi, hi, ss);
+  }
+  return ss;
+}
+// 1 / rms from the four waves' sums of squares (fast::rms_norm,
+// crates/base-mlx-core/src/model/qwen3.rs:50-55)
+__device__ __forceinline__ float gemv_norm_inv(float r0, float r1, float r2, float r3, int K, float eps) {
+  return 1.0f / sqrtf((((r0 + r1) + r2) + r3) / static_cast<float>(K) + eps);
+}
+// h = w * bf16(x * inv), 8 values, bf16 result
+__device__ __forceinline__ uint4 gemv_norm_unit(uint4 d, uint4 wn, float inv) {
+  uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+  const uint32_t wq[4] = {wn.x, wn.y, wn.z, wn.w};
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const float lo = bf2f(wq[q] & 0xffffu) * round_bf(bf2f(dv[q] & 0xffffu) * inv);
+    const float hi = bf2f(wq[q] >> 16) * round_bf(bf2f(dv[q] >> 16) * inv);
+    dv[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+  }
+  return make_uint4(dv[0], dv[1], dv[2], dv[3]);
+}
+// Sum of 8 bf16 values (a quarter of a chunk's x sum), in a fixed order
+__device__ __forceinline__ float gemv_unit_sum(uint4 d) {
+  const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+  float part = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) part += bf2f(dv[q] & 0xffffu) + bf2f(dv[q] >> 16);
+  return part;
+}
+// s and b - 128 s of a group from its interleaved (s | b << 16) word
+__device__ __forceinline__ void gemv_sb(uint32_t sb, float& sv, float& bb) {
+  sv = bf2f(sb & 0xffffu);
+  bb = __builtin_fmaf(-128.0f, sv, bf2f(sb >> 16));
+}
+// One 16-byte chunk (32 nibbles, half a group) of one weight row against
+// the pair-permuted x chunk (x0..x3) with chunk sum sx:
+//   acc += s * D + (b - 128 s) * sx,   D = sum (128 + q) x  (two dot2 chains)
+__device__ __forceinline__ float gemv_chunk(uint4 w, uint4 x0, uint4 x1, uint4 x2, uint4 x3, float sv, float bb,
+                                            float sx, float acc, const NibbleK& nk) {
+  float d0 = 0.0f, d1 = 0.0f;
+  d0 = word_dot(w.x, x0, d0, nk);
+  d1 = word_dot(w.y, x1, d1, nk);
+  d0 = word_dot(w.z, x2, d0, nk);
+  d1 = word_dot(w.w, x3, d1, nk);
+  acc = __builtin_fmaf(sv, d0 + d1, acc);
+  return __builtin_fmaf(bb, sx, acc);
+}
+
 // Per-head RMSNorm (fp32 inside, bf16 result) followed by rotate-half RoPE
 // at angle pos * freq, for one head row of 128 held by a whole wave: lane
 // holds dims lane and lane + 64 (values a, b and norm weights wa, wb on

@@ -52,10 +52,6 @@ struct QmvParams {
   // QMV_STORE with one segment: optional per-workgroup argmax partials of
   // the bf16 outputs, (value bits, row) at [m * qmv_blocks(...) + workgroup]
   uint2* amax;
-  // optional workspace for the K-split matrix-core GEMV (fp32 partials);
-  // without one the library's buffer of the stream is used
-  float* part;
-  size_t part_floats;
 };
 
 // Raises a kernel's dynamic-LDS limit to `bytes` (launches above 64 KB need
@@ -72,8 +68,6 @@ int allow_lds(F* kernel, size_t bytes) {
 
 // Validates shapes/alignment and launches the qmv kernel family.
 int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream);
-// 2..8 rows of x on the matrix cores; -1 when the shape does not fit.
-int try_launch_qmvx(QmvParams p, QmvEpilogue epi, hipStream_t stream);
 // Workgroups launch_qmv uses for these parameters (the count of argmax
 // partials per x row).
 int qmv_blocks(const QmvParams& p, QmvEpilogue epi);
@@ -94,9 +88,6 @@ int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const 
                    int N, int K, float* ws, size_t ws_floats, hipStream_t stream);
 // Split-K partial floats the GEMM needs for any M up to max_M (0 if none).
 size_t qmm_workspace_floats(int max_M, int N, int K);
-// Partial floats the K-split GEMV of 2..8 rows of x needs for an N x K
-// weight (0 if it never splits that shape).
-size_t qmvx_workspace_floats(int N, int K);
 // A device buffer of at least `floats` floats owned by the library for the
 // (device, stream) pair, grown on demand (growing synchronizes the stream);
 // work on one stream runs in order, so its launches may share it.

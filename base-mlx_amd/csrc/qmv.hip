@@ -42,16 +42,41 @@ constexpr int kThreads = 256;
 constexpr int kChunkBytes = 80;  // 64 data bytes + 16 pad per 32 x values
 constexpr int kLdsBudget = 40 * 1024;
 
-template <int MT, int S, int EPI>
-__global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
+// The epilogue of output (m, row): y, y = res + y (o / down projections,
+// qwen3.rs:520-521, 541) or SwiGLU silu(gate) * up (kernels.rs:73-74), each
+// MLX op rounding to bf16.  g / u are the fp32 sums of the (first, second)
+// weight matrix.
+template <int EPI>
+__device__ __forceinline__ void gemv_store(const QmvParams& p, int seg, int m, int rows, int row, float g, float u) {
+  if constexpr (EPI == QMV_STORE) {
+    p.seg[seg].y[static_cast<int64_t>(m) * rows + row] = f2bf(g);
+  } else if constexpr (EPI == QMV_RESIDUAL) {
+    const int64_t o = static_cast<int64_t>(m) * p.N + row;
+    p.seg[0].y[o] = f2bf(bf2f(p.res[o]) + round_bf(g));
+  } else {
+    const float gr = round_bf(g);
+    const float ur = round_bf(u);
+    const float sg = round_bf(1.0f / (1.0f + expf(-gr)));
+    p.seg[0].y[static_cast<int64_t>(m) * p.N + row] = f2bf(round_bf(gr * sg) * ur);
+  }
+}
+
+// Phased GEMV: any K, s / b in 16-byte units or one group at a time.  x and
+// the workgroup's s|b are staged in LDS one phase of p.kp columns at a time
+// (p.kp a multiple of 32 S, so lane sl still meets its chunks c = sl mod S
+// in increasing order, as in the single-phase kernels); W streams U chunks
+// ahead in a register ring.  S (lanes per row) is a launch parameter.
+template <int MT, int EPI>
+__global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p, const int S) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NH = (EPI == QMV_SWIGLU) ? 2 : 1;  // weight rows per lane
-  constexpr int SLOTS = 64 / S;
-  constexpr int RB = (kThreads / 64) * SLOTS;  // rows per workgroup
+  const int lshift = __builtin_ctz(S);
+  const int SLOTS = 64 >> lshift;
+  const int RB = 4 * SLOTS;  // rows per workgroup
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int slot = lane / S;
-  const int sl = lane % S;
+  const int slot = lane >> lshift;
+  const int sl = lane & (S - 1);
   const int M = p.m;
   const int K = p.K;
   const int G = K / 64;
@@ -107,37 +132,27 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
       if (u < n_i0) load_chunk(u, sl + S * u);
   }
 
-  // Optional fused RMSNorm of x (fast::rms_norm, qwen3.rs:50-55):
-  //   h = w * bf16(x * rsqrt(mean(x^2) + eps))
+  // Optional fused RMSNorm of each x row (fast::rms_norm, qwen3.rs:50-55):
+  //   h = w * bf16(x * rsqrt(mean(x^2) + eps)); thread t sums units t,
+  //   t + 256, ... of the row (the single-phase kernels' assignment)
   float inv[MT];
 #pragma unroll
   for (int m = 0; m < MT; m++) inv[m] = 1.0f;
   if (p.norm_w != nullptr) {
-    float ss[MT];
 #pragma unroll
     for (int m = 0; m < MT; m++) {
-      ss[m] = 0.0f;
+      float ss = 0.0f;
       if (m < M) {
         const uint16_t* xr = p.x + m * p.ldx;
-        for (int k = threadIdx.x * 8; k < K; k += kThreads * 8) {
-          uint4 d = *reinterpret_cast<const uint4*>(xr + k);
-          uint32_t v[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            float lo = bf2f(v[i] & 0xffffu), hi = bf2f(v[i] >> 16);
-            ss[m] += lo * lo + hi * hi;
-          }
-        }
+        for (int k = threadIdx.x * 8; k < K; k += kThreads * 8)
+          ss = gemv_ss_unit(*reinterpret_cast<const uint4*>(xr + k), ss);
       }
-      ss[m] = wave_sum_xor(ss[m], 64);
-      if (lane == 0) red[wave * MT + m] = ss[m];
+      ss = lanes_sum(ss, 64);
+      if (lane == 0) red[wave * MT + m] = ss;
     }
     __syncthreads();
 #pragma unroll
-    for (int m = 0; m < MT; m++) {
-      float t = red[m] + red[MT + m] + red[2 * MT + m] + red[3 * MT + m];
-      inv[m] = 1.0f / sqrtf(t / static_cast<float>(K) + p.eps);
-    }
+    for (int m = 0; m < MT; m++) inv[m] = gemv_norm_inv(red[m], red[MT + m], red[2 * MT + m], red[3 * MT + m], K, p.eps);
   }
 
   float acc[NH][MT];
@@ -206,24 +221,14 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
         uint4 d = xr[i];
         float part = 0.0f;
         if (act && m < M) {
-          if (p.norm_w != nullptr) {
-            const uint4 wn = *reinterpret_cast<const uint4*>(p.norm_w + k0 + j * 8);
-            uint32_t dv[4] = {d.x, d.y, d.z, d.w}, wq[4] = {wn.x, wn.y, wn.z, wn.w};
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-              float lo = bf2f(wq[q] & 0xffffu) * round_bf(bf2f(dv[q] & 0xffffu) * inv[m]);
-              float hi = bf2f(wq[q] >> 16) * round_bf(bf2f(dv[q] >> 16) * inv[m]);
-              dv[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
-            }
-            d = make_uint4(dv[0], dv[1], dv[2], dv[3]);
-          }
-          const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-          for (int q = 0; q < 4; q++) part += bf2f(dv[q] & 0xffffu) + bf2f(dv[q] >> 16);
+          if (p.norm_w != nullptr)
+            d = gemv_norm_unit(d, *reinterpret_cast<const uint4*>(p.norm_w + k0 + j * 8), inv[m]);
+          part = gemv_unit_sum(d);
         }
-        // chunk of 32 values = 4 consecutive words = 4 consecutive lanes
-        part += __shfl_xor(part, 1, 64);
-        part += __shfl_xor(part, 2, 64);
+        // a chunk of 32 values = 4 consecutive words = 4 consecutive lanes
+        // (words is a multiple of 8, so j and threadIdx.x agree mod 4)
+        part += dpp_f32<0xB1>(part);
+        part += dpp_f32<0x4E>(part);
         if (act) {
           *reinterpret_cast<uint4*>(xs + (m * CP + (j >> 2)) * kChunkBytes + (j & 3) * 16) = permute_pairs(d);
           if ((j & 3) == 0) sxs[m * CP + (j >> 2)] = part;
@@ -267,11 +272,7 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
           const int c = sl + S * i;  // chunk within the phase
           float sv[NH], bb[NH];
 #pragma unroll
-          for (int h = 0; h < NH; h++) {
-            const uint32_t sb = sbs[(h * RB + rl) * GP + (c >> 1)];
-            sv[h] = bf2f(sb & 0xffffu);
-            bb[h] = bf2f(sb >> 16) - 128.0f * sv[h];
-          }
+          for (int h = 0; h < NH; h++) gemv_sb(sbs[(h * RB + rl) * GP + (c >> 1)], sv[h], bb[h]);
 #pragma unroll
           for (int m = 0; m < MT; m++) {
             if (m < M) {
@@ -279,15 +280,7 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
               const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
               const float sx = sxs[m * CP + c];
 #pragma unroll
-              for (int h = 0; h < NH; h++) {
-                float d = 0.0f;
-                d = word_dot(wv[u][h].x, x0, d, nk);
-                d = word_dot(wv[u][h].y, x1, d, nk);
-                d = word_dot(wv[u][h].z, x2, d, nk);
-                d = word_dot(wv[u][h].w, x3, d, nk);
-                acc[h][m] += sv[h] * d;
-                acc[h][m] += bb[h] * sx;
-              }
+              for (int h = 0; h < NH; h++) acc[h][m] = gemv_chunk(wv[u][h], x0, x1, x2, x3, sv[h], bb[h], sx, acc[h][m], nk);
             }
           }
           if (i + U < n_i) load_chunk(u, cbase + c + S * U);
@@ -300,27 +293,13 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
 #pragma unroll
   for (int h = 0; h < NH; h++)
 #pragma unroll
-    for (int m = 0; m < MT; m++) acc[h][m] = wave_sum_xor(acc[h][m], S);
+    for (int m = 0; m < MT; m++) acc[h][m] = lanes_sum(acc[h][m], S);
 
   if (sl == 0 && valid) {
 #pragma unroll
     for (int m = 0; m < MT; m++) {
       if (m >= M) break;
-      if constexpr (EPI == QMV_STORE) {
-        p.seg[seg].y[static_cast<int64_t>(m) * rows + row] = f2bf(acc[0][m]);
-      } else if constexpr (EPI == QMV_RESIDUAL) {
-        // x = x + o_proj(attn) in bf16 (qwen3.rs:520-521, 541)
-        const int64_t o = static_cast<int64_t>(m) * p.N + row;
-        const float r = bf2f(p.res[o]);
-        p.seg[0].y[o] = f2bf(r + round_bf(acc[0][m]));
-      } else {
-        // silu(gate) * up, each MLX op rounding to bf16 (kernels.rs:73-74)
-        const float g = round_bf(acc[0][m]);
-        const float u = round_bf(acc[NH - 1][m]);
-        const float sg = round_bf(1.0f / (1.0f + expf(-g)));
-        const float a = round_bf(g * sg);
-        p.seg[0].y[static_cast<int64_t>(m) * p.N + row] = f2bf(a * u);
-      }
+      gemv_store<EPI>(p, seg, m, rows, row, acc[0][m], acc[NH - 1][m]);
     }
   }
   if constexpr (EPI == QMV_STORE) {
@@ -353,21 +332,21 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p) {
   }
 }
 
-// M = 1 with the whole K in one LDS phase (the decode shapes).  Every load
-// of the workgroup is unconditional (indices are clamped; duplicate
-// addresses coalesce inside an instruction): first x, the norm weight, s|b
-// and the lane's first 16-byte W chunk; then, once x and s|b are staged in
-// LDS, the remaining NI - 1 chunks.  With the count of loads in flight
-// fixed, the compiler waits for each W chunk on its own, so the dot products
-// of chunk u overlap the arrival of the later ones.
+// Single-phase GEMV, the decode shapes: 1..8 rows of x (MT) with the whole K
+// in one LDS phase.  Every load of the workgroup is unconditional (indices
+// are clamped; duplicate addresses coalesce inside an instruction): first
+// x, the norm weight, s|b and the lane's first 16-byte W chunk; then, once x
+// and s|b are staged in LDS, the remaining NI - 1 chunks.  With the count of
+// loads in flight fixed, the compiler waits for each W chunk on its own, so
+// the dot products of chunk u overlap the arrival of the later ones.
 // S (lanes per row) is a launch parameter; NI = ceil(K/32 / S) rounded up to
 // an instantiated value.
 constexpr int kXU1 = 5;  // x units (8 values) per thread: K <= 256 * 8 * 5
 
-// XU: x units per thread the launch needs (2 up to K = 4096, else kXU1), so
-// that no thread issues loads of clamped duplicates; NORM: the RMSNorm
-// prologue (p.norm_w set), whose weight loads are issued only then
-template <int NI, int EPI, int XU, bool NORM>
+// XU: x units per thread and row the launch needs (2 up to K = 4096, else
+// kXU1), so that no thread issues loads of clamped duplicates; NORM: the
+// RMSNorm prologue (p.norm_w set), whose weight loads are issued only then
+template <int NI, int EPI, int XU, bool NORM, int MT>
 __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const int S) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NH = (EPI == QMV_SWIGLU) ? 2 : 1;
@@ -378,14 +357,15 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   const int wave = threadIdx.x >> 6;
   const int slot = lane >> lshift;
   const int sl = lane & (S - 1);
+  const int M = p.m;
   const int K = p.K;
   const int G = K / 64, C = K / 32, W8 = K / 8, GU = G / 8;
-  unsigned char* xs = smem;                                        // [C] x 80 B
-  float* sxs = reinterpret_cast<float*>(smem + C * kChunkBytes);   // [C]
-  uint32_t* sbs = reinterpret_cast<uint32_t*>(sxs + C);            // [NH][RB][G]
-  float* red = reinterpret_cast<float*>(sbs + NH * RB * G);        // [4]
-  float* amv = red + 4;                                            // [RB]
-  uint32_t* ami = reinterpret_cast<uint32_t*>(amv + RB);           // [RB]
+  unsigned char* xs = smem;                                             // [MT][C] x 80 B
+  float* sxs = reinterpret_cast<float*>(smem + MT * C * kChunkBytes);   // [MT][C]
+  uint32_t* sbs = reinterpret_cast<uint32_t*>(sxs + MT * C);            // [NH][RB][G]
+  float* red = reinterpret_cast<float*>(sbs + NH * RB * G);             // [4][MT]
+  float* amv = red + 4 * MT;                                            // [RB]
+  uint32_t* ami = reinterpret_cast<uint32_t*>(amv + RB);                // [RB]
 
   int seg = 0;
   if constexpr (EPI != QMV_SWIGLU) {
@@ -397,15 +377,15 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   const int rl = wave * SLOTS + slot;
   const int row = row0 + rl;
   const bool valid = row < rows;
-  constexpr bool has_norm = NORM;
   const uint16_t* nw = p.norm_w;
 
   // ---- 1. staging loads (unconditional, clamped) ----
-  uint4 xr[XU], nr[XU];
+  uint4 xr[MT][XU], nr[XU];
 #pragma unroll
   for (int i = 0; i < XU; i++) {
     const int idx = min(i * kThreads + static_cast<int>(threadIdx.x), W8 - 1);
-    xr[i] = *reinterpret_cast<const uint4*>(p.x + idx * 8);
+#pragma unroll
+    for (int m = 0; m < MT; m++) xr[m][i] = *reinterpret_cast<const uint4*>(p.x + min(m, M - 1) * p.ldx + idx * 8);
     if constexpr (NORM) nr[i] = *reinterpret_cast<const uint4*>(nw + idx * 8);
   }
   uint4 sr[NH], br[NH];
@@ -443,58 +423,51 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
     }
   };
   issue_w(0);
-  // ---- 3. fused RMSNorm (fast::rms_norm, qwen3.rs:50-55) from the staged x:
-  //      h = w * bf16(x * rsqrt(mean(x^2) + eps)) ----
-  float inv = 1.0f;
-  if (has_norm) {
-    float ss = 0.0f;
+  // ---- 3. fused RMSNorm (fast::rms_norm, qwen3.rs:50-55) of each x row
+  //      from the staged x: h = w * bf16(x * rsqrt(mean(x^2) + eps)) ----
+  float inv[MT];
 #pragma unroll
-    for (int i = 0; i < XU; i++) {
-      if (i * kThreads >= W8) break;  // uniform: the remaining units are clamped copies
-      if (i * kThreads + static_cast<int>(threadIdx.x) < W8) {
-        const uint32_t v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+  for (int m = 0; m < MT; m++) inv[m] = 1.0f;
+  if constexpr (NORM) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const float lo = bf2f(v[q] & 0xffffu), hi = bf2f(v[q] >> 16);
-          ss += lo * lo + hi * hi;
+    for (int m = 0; m < MT; m++) {
+      float ss = 0.0f;
+      if (m < M) {
+#pragma unroll
+        for (int i = 0; i < XU; i++) {
+          if (i * kThreads >= W8) break;  // uniform: the remaining units are clamped copies
+          if (i * kThreads + static_cast<int>(threadIdx.x) < W8) ss = gemv_ss_unit(xr[m][i], ss);
         }
       }
+      ss = lanes_sum(ss, 64);
+      if (lane == 0) red[wave * MT + m] = ss;
     }
-    ss = lanes_sum(ss, 64);
-    if (lane == 0) red[wave] = ss;
     __syncthreads();
-    inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / static_cast<float>(K) + p.eps);
+#pragma unroll
+    for (int m = 0; m < MT; m++) inv[m] = gemv_norm_inv(red[m], red[MT + m], red[2 * MT + m], red[3 * MT + m], K, p.eps);
   }
   // ---- 4. x (pair-permuted, chunk sums) and s|b into LDS ----
 #pragma unroll
-  for (int i = 0; i < XU; i++) {
-    if (i * kThreads >= W8) break;  // uniform: the remaining units are clamped copies
-    const int idx = i * kThreads + static_cast<int>(threadIdx.x);
-    const bool act = idx < W8;
-    uint4 d = xr[i];
-    float part = 0.0f;
-    if (act) {
-      if (has_norm) {
-        uint32_t dv[4] = {d.x, d.y, d.z, d.w};
-        const uint32_t wq[4] = {nr[i].x, nr[i].y, nr[i].z, nr[i].w};
+  for (int m = 0; m < MT; m++) {
+    if (m >= M) break;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const float lo = bf2f(wq[q] & 0xffffu) * round_bf(bf2f(dv[q] & 0xffffu) * inv);
-          const float hi = bf2f(wq[q] >> 16) * round_bf(bf2f(dv[q] >> 16) * inv);
-          dv[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
-        }
-        d = make_uint4(dv[0], dv[1], dv[2], dv[3]);
+    for (int i = 0; i < XU; i++) {
+      if (i * kThreads >= W8) break;  // uniform: the remaining units are clamped copies
+      const int idx = i * kThreads + static_cast<int>(threadIdx.x);
+      const bool act = idx < W8;
+      uint4 d = xr[m][i];
+      float part = 0.0f;
+      if (act) {
+        if constexpr (NORM) d = gemv_norm_unit(d, nr[i], inv[m]);
+        part = gemv_unit_sum(d);
       }
-      const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-      for (int q = 0; q < 4; q++) part += bf2f(dv[q] & 0xffffu) + bf2f(dv[q] >> 16);
-    }
-    // a chunk of 32 values = 4 consecutive words = 4 consecutive lanes
-    part += dpp_f32<0xB1>(part);
-    part += dpp_f32<0x4E>(part);
-    if (act) {
-      *reinterpret_cast<uint4*>(xs + (idx >> 2) * kChunkBytes + (idx & 3) * 16) = permute_pairs(d);
-      if ((idx & 3) == 0) sxs[idx >> 2] = part;
+      // a chunk of 32 values = 4 consecutive words = 4 consecutive lanes
+      part += dpp_f32<0xB1>(part);
+      part += dpp_f32<0x4E>(part);
+      if (act) {
+        *reinterpret_cast<uint4*>(xs + (m * C + (idx >> 2)) * kChunkBytes + (idx & 3) * 16) = permute_pairs(d);
+        if ((idx & 3) == 0) sxs[m * C + (idx >> 2)] = part;
+      }
     }
   }
   if (static_cast<int>(threadIdx.x) < sb_units && row0 + r_sb < rows) {
@@ -516,28 +489,26 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   __syncthreads();
   // ---- 5. dot products, chunk by chunk as the W stream arrives ----
   const NibbleK nk = nibble_consts();
-  float acc[NH];
+  float acc[NH][MT];
 #pragma unroll
-  for (int h = 0; h < NH; h++) acc[h] = 0.0f;
+  for (int h = 0; h < NH; h++)
+#pragma unroll
+    for (int m = 0; m < MT; m++) acc[h][m] = 0.0f;
 #pragma unroll
   for (int u = 0; u < NI; u++) {
     const int c = sl + (u << lshift);
     if (c < C) {
-      const uint4* xp = reinterpret_cast<const uint4*>(xs + c * kChunkBytes);
-      const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
-      const float sx = sxs[c];
+      float sv[NH], bb[NH];
 #pragma unroll
-      for (int h = 0; h < NH; h++) {
-        const uint32_t sb = sbs[(h * RB + rl) * G + (c >> 1)];
-        const float sv = bf2f(sb & 0xffffu);
-        const float bb = bf2f(sb >> 16) - 128.0f * sv;
-        float d0 = 0.0f, d1 = 0.0f;  // two independent dot2 chains
-        d0 = word_dot(wv[u][h].x, x0, d0, nk);
-        d1 = word_dot(wv[u][h].y, x1, d1, nk);
-        d0 = word_dot(wv[u][h].z, x2, d0, nk);
-        d1 = word_dot(wv[u][h].w, x3, d1, nk);
-        acc[h] += sv * (d0 + d1);
-        acc[h] += bb * sx;
+      for (int h = 0; h < NH; h++) gemv_sb(sbs[(h * RB + rl) * G + (c >> 1)], sv[h], bb[h]);
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        if (m >= M) break;
+        const uint4* xp = reinterpret_cast<const uint4*>(xs + (m * C + c) * kChunkBytes);
+        const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+        const float sx = sxs[m * C + c];
+#pragma unroll
+        for (int h = 0; h < NH; h++) acc[h][m] = gemv_chunk(wv[u][h], x0, x1, x2, x3, sv[h], bb[h], sx, acc[h][m], nk);
       }
     }
     // consume the chunks in issue order (each waits only for its own loads)
@@ -545,28 +516,21 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   }
   // ---- 6. reduce the S lanes of each row, epilogue ----
 #pragma unroll
-  for (int h = 0; h < NH; h++) acc[h] = lanes_sum(acc[h], S);
+  for (int h = 0; h < NH; h++)
+#pragma unroll
+    for (int m = 0; m < MT; m++) acc[h][m] = lanes_sum(acc[h][m], S);
   if (sl == 0 && valid) {
-    if constexpr (EPI == QMV_STORE) {
-      p.seg[seg].y[row] = f2bf(acc[0]);
-    } else if constexpr (EPI == QMV_RESIDUAL) {
-      // x = x + o_proj(attn) in bf16 (qwen3.rs:520-521, 541)
-      const float r = bf2f(p.res[row]);
-      p.seg[0].y[row] = f2bf(r + round_bf(acc[0]));
-    } else {
-      // silu(gate) * up, each MLX op rounding to bf16 (kernels.rs:73-74)
-      const float g = round_bf(acc[0]);
-      const float u = round_bf(acc[NH - 1]);
-      const float sg = round_bf(1.0f / (1.0f + expf(-g)));
-      const float a = round_bf(g * sg);
-      p.seg[0].y[row] = f2bf(a * u);
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+      if (m >= M) break;
+      gemv_store<EPI>(p, seg, m, rows, row, acc[0][m], acc[NH - 1][m]);
     }
   }
-  if constexpr (EPI == QMV_STORE) {
+  if constexpr (EPI == QMV_STORE && MT == 1) {
     if (p.amax != nullptr) {
       // argmax partial of the workgroup's rows (first index on ties): across
       // the row slots of each wave with shuffles, then the 4 waves in LDS
-      float bv = valid ? bf2f(f2bf(acc[0])) : -INFINITY;
+      float bv = valid ? bf2f(f2bf(acc[0][0])) : -INFINITY;
       uint32_t bi = valid ? static_cast<uint32_t>(row) : 0xffffffffu;
       for (int off = S; off < 64; off <<= 1) {
         const float ov = __shfl_xor(bv, off, 64);
@@ -594,56 +558,76 @@ __global__ void __launch_bounds__(kThreads) qmv1_kernel(const QmvParams p, const
   }
 }
 
-template <int NI, int XU>
+template <int NI, int XU, int MT>
 int launch_qmv1_xu(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
   const bool norm = p.norm_w != nullptr;
+  auto go = [&](auto kern) {
+    if (int rc = allow_lds(kern, lds)) return rc;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, st, p, S);
+    return check_launch("qmv1");
+  };
+  // the combinations the library uses: store with or without the fused
+  // norm (q|k|v, lm_head; plain projections), residual without it (o,
+  // down), SwiGLU with it (gate|up); others go to the phased kernel
   switch (epi) {
     case QMV_STORE:
-      if (norm)
-        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_STORE, XU, true>), dim3(blocks), dim3(kThreads), lds, st, p, S);
-      else
-        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_STORE, XU, false>), dim3(blocks), dim3(kThreads), lds, st, p, S);
-      break;
+      return norm ? go(qmv1_kernel<NI, QMV_STORE, XU, true, MT>) : go(qmv1_kernel<NI, QMV_STORE, XU, false, MT>);
     case QMV_RESIDUAL:
-      if (norm)
-        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_RESIDUAL, XU, true>), dim3(blocks), dim3(kThreads), lds, st, p, S);
-      else
-        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_RESIDUAL, XU, false>), dim3(blocks), dim3(kThreads), lds, st, p, S);
-      break;
+      return norm ? kNoFit : go(qmv1_kernel<NI, QMV_RESIDUAL, XU, false, MT>);
     default:
-      if (norm)
-        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_SWIGLU, XU, true>), dim3(blocks), dim3(kThreads), lds, st, p, S);
-      else
-        hipLaunchKernelGGL((qmv1_kernel<NI, QMV_SWIGLU, XU, false>), dim3(blocks), dim3(kThreads), lds, st, p, S);
+      return norm ? go(qmv1_kernel<NI, QMV_SWIGLU, XU, true, MT>) : kNoFit;
   }
-  return check_launch("qmv1");
 }
 
-template <int NI>
+// x units per thread and row: 2 up to K = 4096, else kXU1; several rows stay
+// within 12 units per thread in all
+constexpr int qmv1_xu(int K) { return K / 8 <= 2 * kThreads ? 2 : kXU1; }
+constexpr bool qmv1_fits(int mt, int xu) { return mt == 1 || mt * xu <= 12; }
+
+template <int NI, int MT>
 int launch_qmv1_ni(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
-  if (p.K / 8 <= 2 * kThreads) return launch_qmv1_xu<NI, 2>(epi, S, p, blocks, lds, st);
-  return launch_qmv1_xu<NI, kXU1>(epi, S, p, blocks, lds, st);
+  if (qmv1_xu(p.K) == 2) {
+    if constexpr (qmv1_fits(MT, 2)) return launch_qmv1_xu<NI, 2, MT>(epi, S, p, blocks, lds, st);
+  } else {
+    if constexpr (qmv1_fits(MT, kXU1)) return launch_qmv1_xu<NI, kXU1, MT>(epi, S, p, blocks, lds, st);
+  }
+  return kNoFit;
 }
 
-// Launches qmv1 when it applies (M = 1, one phase, 16-byte s|b staging, x
-// within kXU1 units per thread, s|b within one unit per thread); returns -1
-// otherwise.
-int try_launch_qmv1(QmvEpilogue epi, int S, const QmvParams& p, int blocks, hipStream_t st) {
-  if (p.m != 1 || p.kp < p.K || !p.sb_vec || p.K / 8 > kThreads * kXU1) return kNoFit;
+template <int MT>
+int launch_qmv1_mt(int ni, int nh, QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds,
+                   hipStream_t st) {
+  if (ni <= 2) return launch_qmv1_ni<2, MT>(epi, S, p, blocks, lds, st);
+  if (ni <= 3) return launch_qmv1_ni<3, MT>(epi, S, p, blocks, lds, st);
+  if (ni <= 5) return launch_qmv1_ni<5, MT>(epi, S, p, blocks, lds, st);
+  if (ni <= 8) return launch_qmv1_ni<8, MT>(epi, S, p, blocks, lds, st);
+  if (nh == 1 && ni <= 10) return launch_qmv1_ni<10, MT>(epi, S, p, blocks, lds, st);
+  if (nh == 1 && ni <= 16) return launch_qmv1_ni<16, MT>(epi, S, p, blocks, lds, st);
+  return kNoFit;
+}
+
+// Launches the single-phase GEMV when it applies (one phase, 16-byte s|b
+// staging, x within kXU1 units per thread and row -- with several rows at
+// most 12 units per thread in all, so the staging stays in registers -- and
+// the workgroup's s|b within one unit per thread); returns kNoFit otherwise.
+int try_launch_qmv1(QmvEpilogue epi, int mt, int S, const QmvParams& p, int blocks, hipStream_t st) {
+  if (!p.sb_vec || p.K / 8 > kThreads * kXU1) return kNoFit;
+  if (!qmv1_fits(mt, qmv1_xu(p.K))) return kNoFit;
   const int C = p.K / 32, G = p.K / 64;
   const int RB = 4 * (64 / S);
   if (RB * (G / 8) > kThreads) return kNoFit;
   const int ni = (C + S - 1) / S;
   const int nh = epi == QMV_SWIGLU ? 2 : 1;
-  const size_t lds = static_cast<size_t>(C) * (kChunkBytes + 4) + static_cast<size_t>(nh) * RB * G * 4 + 16 +
-                     static_cast<size_t>(RB) * 8;
-  if (ni <= 2) return launch_qmv1_ni<2>(epi, S, p, blocks, lds, st);
-  if (ni <= 3) return launch_qmv1_ni<3>(epi, S, p, blocks, lds, st);
-  if (ni <= 5) return launch_qmv1_ni<5>(epi, S, p, blocks, lds, st);
-  if (ni <= 8) return launch_qmv1_ni<8>(epi, S, p, blocks, lds, st);
-  if (nh == 1 && ni <= 10) return launch_qmv1_ni<10>(epi, S, p, blocks, lds, st);
-  if (nh == 1 && ni <= 16) return launch_qmv1_ni<16>(epi, S, p, blocks, lds, st);
-  return kNoFit;
+  const size_t lds = static_cast<size_t>(mt) * C * (kChunkBytes + 4) + static_cast<size_t>(nh) * RB * G * 4 +
+                     16ull * mt + static_cast<size_t>(RB) * 8;
+  if (lds > 160 * 1024) return kNoFit;
+  switch (mt) {
+    case 1: return launch_qmv1_mt<1>(ni, nh, epi, S, p, blocks, lds, st);
+    case 2: return launch_qmv1_mt<2>(ni, nh, epi, S, p, blocks, lds, st);
+    case 4: return launch_qmv1_mt<4>(ni, nh, epi, S, p, blocks, lds, st);
+    case 5: return launch_qmv1_mt<5>(ni, nh, epi, S, p, blocks, lds, st);
+    default: return kNoFit;  // 8 rows exceed the staging registers
+  }
 }
 
 // Persistent GEMV for M <= 8 rows of x with the whole K in LDS.  About two
@@ -730,10 +714,7 @@ __global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const
 
   // ---- x into LDS once: pair-permuted, chunk sums; RMSNorm fused for M = 1 ----
   // 1 / rms of x row m from the per-wave sums of squares in red [4][MT]
-  auto inv_of = [&](int m) {
-    const float t = red[m] + red[MT + m] + red[2 * MT + m] + red[3 * MT + m];
-    return 1.0f / sqrtf(t / static_cast<float>(K) + p.eps);
-  };
+  auto inv_of = [&](int m) { return gemv_norm_inv(red[m], red[MT + m], red[2 * MT + m], red[3 * MT + m], K, p.eps); };
   auto stage_unit = [&](int idx, uint4 d, const uint4& wn, float inv) {
     const bool act = idx < MT * W8;
     float part = 0.0f;
@@ -742,20 +723,8 @@ __global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const
       m = (MT == 1) ? 0 : idx / W8;
       j = idx - m * W8;
       if (MT > 1 && has_norm) inv = inv_of(m);
-      if (has_norm) {
-        uint32_t dv[4] = {d.x, d.y, d.z, d.w};
-        const uint32_t wq[4] = {wn.x, wn.y, wn.z, wn.w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const float lo = bf2f(wq[q] & 0xffffu) * round_bf(bf2f(dv[q] & 0xffffu) * inv);
-          const float hi = bf2f(wq[q] >> 16) * round_bf(bf2f(dv[q] >> 16) * inv);
-          dv[q] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
-        }
-        d = make_uint4(dv[0], dv[1], dv[2], dv[3]);
-      }
-      const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
-#pragma unroll
-      for (int q = 0; q < 4; q++) part += bf2f(dv[q] & 0xffffu) + bf2f(dv[q] >> 16);
+      if (has_norm) d = gemv_norm_unit(d, wn, inv);
+      part = gemv_unit_sum(d);
     }
     // a chunk of 32 values = 4 consecutive words = 4 consecutive lanes
     part += dpp_f32<0xB1>(part);
@@ -784,19 +753,12 @@ __global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const
 #pragma unroll
       for (int i = 0; i < XU; i++) {
         if (i * kThreads >= W8) break;
-        if (i * kThreads + static_cast<int>(threadIdx.x) < W8) {
-          const uint32_t v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const float lo = bf2f(v[q] & 0xffffu), hi = bf2f(v[q] >> 16);
-            ss += lo * lo + hi * hi;
-          }
-        }
+        if (i * kThreads + static_cast<int>(threadIdx.x) < W8) ss = gemv_ss_unit(xr[i], ss);
       }
       ss = lanes_sum(ss, 64);
       if (lane == 0) red[wave] = ss;
       __syncthreads();
-      inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / static_cast<float>(K) + p.eps);
+      inv = inv_of(0);
     }
 #pragma unroll
     for (int i = 0; i < XU; i++) {
@@ -806,40 +768,17 @@ __global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const
   } else {
     if (has_norm) {
       // fast::rms_norm (qwen3.rs:50-55) of each x row: a first pass for the
-      // sums of squares, then the staging pass normalises
-      float ss[MT];
-#pragma unroll
-      for (int m = 0; m < MT; m++) ss[m] = 0.0f;
-      for (int b0 = 0; b0 < MT * W8; b0 += kThreads * XU) {
-        uint4 xr[XU];
-#pragma unroll
-        for (int i = 0; i < XU; i++) {
-          const int idx = min(b0 + i * kThreads + static_cast<int>(threadIdx.x), MT * W8 - 1);
-          const int m = idx / W8;
-          xr[i] = *reinterpret_cast<const uint4*>(p.x + min(m, M - 1) * p.ldx + (idx - m * W8) * 8);
-        }
-#pragma unroll
-        for (int i = 0; i < XU; i++) {
-          const int idx = b0 + i * kThreads + static_cast<int>(threadIdx.x);
-          if (idx < MT * W8) {
-            const int m = idx / W8;
-            const uint32_t v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-            float q2 = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-              const float lo = bf2f(v[q] & 0xffffu), hi = bf2f(v[q] >> 16);
-              q2 += lo * lo + hi * hi;
-            }
-#pragma unroll
-            for (int mm = 0; mm < MT; mm++)
-              if (m == mm) ss[mm] += q2;
-          }
-        }
-      }
+      // sums of squares (thread t sums units t, t + 256, ... of the row, as
+      // for one row), then the staging pass normalises
 #pragma unroll
       for (int m = 0; m < MT; m++) {
-        const float v = lanes_sum(ss[m], 64);
-        if (lane == 0) red[wave * MT + m] = v;
+        float ss = 0.0f;
+        if (m < M) {
+          for (int j = threadIdx.x; j < W8; j += kThreads)
+            ss = gemv_ss_unit(*reinterpret_cast<const uint4*>(p.x + m * p.ldx + j * 8), ss);
+        }
+        ss = lanes_sum(ss, 64);
+        if (lane == 0) red[wave * MT + m] = ss;
       }
       __syncthreads();
     }
@@ -896,11 +835,7 @@ __global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const
       if (c < C) {
         float sv[NH], bb[NH];
 #pragma unroll
-        for (int h = 0; h < NH; h++) {
-          const uint32_t w = sb[(h * RB + rl) * G + (c >> 1)];
-          sv[h] = bf2f(w & 0xffffu);
-          bb[h] = bf2f(w >> 16) - 128.0f * sv[h];
-        }
+        for (int h = 0; h < NH; h++) gemv_sb(sb[(h * RB + rl) * G + (c >> 1)], sv[h], bb[h]);
 #pragma unroll
         for (int m = 0; m < MT; m++) {
           if (m >= M) break;
@@ -908,15 +843,8 @@ __global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const
           const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
           const float sx = sxs[m * C + c];
 #pragma unroll
-          for (int h = 0; h < NH; h++) {
-            float d0 = 0.0f, d1 = 0.0f;
-            d0 = word_dot(cur.w[u][h].x, x0, d0, nk);
-            d1 = word_dot(cur.w[u][h].y, x1, d1, nk);
-            d0 = word_dot(cur.w[u][h].z, x2, d0, nk);
-            d1 = word_dot(cur.w[u][h].w, x3, d1, nk);
-            acc[h][m] += sv[h] * (d0 + d1);
-            acc[h][m] += bb[h] * sx;
-          }
+          for (int h = 0; h < NH; h++)
+            acc[h][m] = gemv_chunk(cur.w[u][h], x0, x1, x2, x3, sv[h], bb[h], sx, acc[h][m], nk);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -931,19 +859,7 @@ __global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const
 #pragma unroll
       for (int m = 0; m < MT; m++) {
         if (m >= M) break;
-        if constexpr (EPI == QMV_STORE) {
-          p.seg[sg].y[static_cast<int64_t>(m) * rows + row] = f2bf(acc[0][m]);
-        } else if constexpr (EPI == QMV_RESIDUAL) {
-          // x = x + o_proj(attn) in bf16 (qwen3.rs:520-521, 541)
-          const int64_t o = static_cast<int64_t>(m) * p.N + row;
-          p.seg[0].y[o] = f2bf(bf2f(p.res[o]) + round_bf(acc[0][m]));
-        } else {
-          // silu(gate) * up, each MLX op rounding to bf16 (kernels.rs:73-74)
-          const float g = round_bf(acc[0][m]);
-          const float u = round_bf(acc[NH - 1][m]);
-          const float sgm = round_bf(1.0f / (1.0f + expf(-g)));
-          p.seg[0].y[static_cast<int64_t>(m) * p.N + row] = f2bf(round_bf(g * sgm) * u);
-        }
+        gemv_store<EPI>(p, sg, m, rows, row, acc[0][m], acc[NH - 1][m]);
       }
     }
     if constexpr (EPI == QMV_STORE && MT == 1) {
@@ -998,19 +914,10 @@ __global__ void __launch_bounds__(kThreads) qmvp_kernel(const QmvParams p, const
 
 template <int MT, int NI>
 int launch_qmvp_epi(QmvEpilogue epi, int S, const QmvParams& p, int ntiles, int grid, size_t lds, hipStream_t st) {
-  switch (epi) {
-    case QMV_STORE:
-      if (int rc = allow_lds(qmvp_kernel<MT, NI, QMV_STORE>, lds)) return rc;
-      hipLaunchKernelGGL((qmvp_kernel<MT, NI, QMV_STORE>), dim3(grid), dim3(kThreads), lds, st, p, S, ntiles);
-      break;
-    case QMV_RESIDUAL:
-      if (int rc = allow_lds(qmvp_kernel<MT, NI, QMV_RESIDUAL>, lds)) return rc;
-      hipLaunchKernelGGL((qmvp_kernel<MT, NI, QMV_RESIDUAL>), dim3(grid), dim3(kThreads), lds, st, p, S, ntiles);
-      break;
-    default:
-      if (int rc = allow_lds(qmvp_kernel<MT, NI, QMV_SWIGLU>, lds)) return rc;
-      hipLaunchKernelGGL((qmvp_kernel<MT, NI, QMV_SWIGLU>), dim3(grid), dim3(kThreads), lds, st, p, S, ntiles);
-  }
+  // the vocabulary-sized projections are plain stores (the lm_head)
+  if (epi != QMV_STORE) return kNoFit;
+  if (int rc = allow_lds(qmvp_kernel<MT, NI, QMV_STORE>, lds)) return rc;
+  hipLaunchKernelGGL((qmvp_kernel<MT, NI, QMV_STORE>), dim3(grid), dim3(kThreads), lds, st, p, S, ntiles);
   return check_launch("qmvp");
 }
 
@@ -1025,10 +932,9 @@ int launch_qmvp_ni(int ni, int nh, QmvEpilogue epi, int S, const QmvParams& p, i
 }
 
 // Launches the persistent GEMV when it applies (whole K in LDS, 16-byte s|b
-// staging, the workgroup's s|b in one unit per thread, norm only with one x
-// row); returns -1 otherwise.
-// one-row GEMVs with at least this many weight rows (the vocabulary
-// projection) go to the persistent kernel
+// staging, the workgroup's s|b in one unit per thread); returns kNoFit
+// otherwise.  GEMVs with at least this many weight rows (the vocabulary
+// projection) go to the persistent kernel.
 constexpr int kPersistentRows = 65536;
 
 int try_launch_qmvp(QmvEpilogue epi, int mt, int S, const QmvParams& p, int ntiles, hipStream_t st) {
@@ -1053,33 +959,17 @@ int try_launch_qmvp(QmvEpilogue epi, int mt, int S, const QmvParams& p, int ntil
   }
 }
 
-template <int MT, int EPI>
-int launch_s(int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
-  if constexpr (MT == 1) {
-    if (S == 8) {
-      hipLaunchKernelGGL((qmv_kernel<MT, 8, EPI>), dim3(blocks), dim3(kThreads), lds, st, p);
-      return check_launch("qmv");
-    }
-    if (S == 32) {
-      hipLaunchKernelGGL((qmv_kernel<MT, 32, EPI>), dim3(blocks), dim3(kThreads), lds, st, p);
-      return check_launch("qmv");
-    }
-  }
-  if (S == 16) {
-    hipLaunchKernelGGL((qmv_kernel<MT, 16, EPI>), dim3(blocks), dim3(kThreads), lds, st, p);
-  } else {
-    hipLaunchKernelGGL((qmv_kernel<MT, 64, EPI>), dim3(blocks), dim3(kThreads), lds, st, p);
-  }
-  return check_launch("qmv");
-}
-
 template <int MT>
-int launch_epi(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds,
-               hipStream_t st) {
+int launch_epi(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
+  auto go = [&](auto kern) {
+    if (int rc = allow_lds(kern, lds)) return rc;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, st, p, S);
+    return check_launch("qmv");
+  };
   switch (epi) {
-    case QMV_STORE: return launch_s<MT, QMV_STORE>(S, p, blocks, lds, st);
-    case QMV_RESIDUAL: return launch_s<MT, QMV_RESIDUAL>(S, p, blocks, lds, st);
-    default: return launch_s<MT, QMV_SWIGLU>(S, p, blocks, lds, st);
+    case QMV_STORE: return go(qmv_kernel<MT, QMV_STORE>);
+    case QMV_RESIDUAL: return go(qmv_kernel<MT, QMV_RESIDUAL>);
+    default: return go(qmv_kernel<MT, QMV_SWIGLU>);
   }
 }
 
@@ -1108,14 +998,14 @@ struct QmvGrid {
   int blk0[3];
 };
 
-// Tile shape and grid of one launch: lanes per row S, rows per workgroup,
-// and the first workgroup of
-// each segment (segments start on workgroup boundaries; SWIGLU's two
-// matrices share every workgroup).
+// Tile shape and grid of one launch: lanes per row S (a function of N and K
+// only, so that every row count shares one chunk -> lane assignment), rows
+// per workgroup, and the first workgroup of each segment (segments start on
+// workgroup boundaries; SWIGLU's two matrices share every workgroup).
 QmvGrid qmv_grid(const QmvParams& p, QmvEpilogue epi) {
   QmvGrid g{};
   g.mt = p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : p.m <= 5 ? 5 : 8;
-  g.S = (g.mt == 1) ? pick_lanes_per_row(p.N, p.K) : (p.K / 32 >= 64 ? 64 : 16);
+  g.S = pick_lanes_per_row(p.N, p.K);
   g.rows_per_block = (kThreads / 64) * (64 / g.S);
   if (epi == QMV_SWIGLU) {
     g.blocks = (p.N + g.rows_per_block - 1) / g.rows_per_block;
@@ -1151,10 +1041,13 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   const int nh = epi == QMV_SWIGLU ? 2 : 1;
   const int rows_per_block = gr.rows_per_block;
   // LDS per phase: x chunks (80 B + 4 B sum per 32 columns per x row) and
-  // the workgroup's s|b words (4 B per 64 columns per weight row).
+  // the workgroup's s|b words (4 B per 64 columns per weight row).  A phase
+  // is a multiple of 32 S columns (whole rounds of the S lanes over the
+  // chunks), so the phase split never changes which lane adds which chunk.
   const double per_col = mt * (kChunkBytes + 4) / 32.0 + nh * rows_per_block * 4 / 64.0;
+  const int unit = std::max(512, 32 * S);
   int kp = static_cast<int>(kLdsBudget / per_col);
-  kp = std::max(512, (kp / 512) * 512);
+  kp = std::max(unit, (kp / unit) * unit);
   p.kp = std::min(kp, p.K);
   const int CP = p.kp / 32, GP = p.kp / 64;
   const size_t lds = static_cast<size_t>(mt) * CP * (kChunkBytes + 4) +
@@ -1168,21 +1061,21 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   p.sb_vec = (p.K % 512) == 0;
   for (int i = 0; i < p.nseg; i++)
     p.sb_vec = p.sb_vec && aligned(p.seg[i].s, 16) && aligned(p.seg[i].b, 16);
-  // kernel choice: matrix cores for 2..8 rows of x; for one row the
-  // persistent kernel on the vocabulary-sized projection, the single-phase
-  // GEMV elsewhere
-  if (mt >= 2) {
-    const int rc = try_launch_qmvx(p, epi, stream);
-    if (rc != kNoFit) return rc;
-  }
+  // Kernel choice: the persistent kernel on vocabulary-sized projections,
+  // the single-phase kernel where x and s|b fit it, the phased kernel
+  // otherwise.  All three compute every row with the same operations in the
+  // same order (bmx_device.h, gemv_*), so which one runs -- and how many
+  // rows of x share the launch -- never changes a row's bits.  Argmax
+  // partials of several rows come from the phased kernel.
   int rows_total = 0;
   for (int i = 0; i < p.nseg; i++) rows_total += p.seg[i].rows;
-  if (mt == 1 && rows_total >= kPersistentRows) {
+  const bool amax_multi = p.amax != nullptr && mt > 1;
+  if (rows_total >= kPersistentRows && !amax_multi) {
     const int rc = try_launch_qmvp(epi, mt, S, p, blocks, stream);
     if (rc != kNoFit) return rc;
   }
-  if (mt == 1) {
-    const int rc = try_launch_qmv1(epi, S, p, blocks, stream);
+  if (!amax_multi) {
+    const int rc = try_launch_qmv1(epi, mt, S, p, blocks, stream);
     if (rc != kNoFit) return rc;
   }
   switch (mt) {

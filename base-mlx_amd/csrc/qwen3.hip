@@ -90,8 +90,8 @@ struct bmx_qwen3 {
            *o = nullptr, *g = nullptr, *u = nullptr, *a = nullptr, *logits1 = nullptr;
   float* attn_ws = nullptr;
   size_t attn_ws_floats = 0;
-  float* qmm_ws = nullptr;  // split-K partials of the prefill GEMMs and of the K-split
-  size_t qmm_ws_floats = 0;  // verify GEMVs (per model: models on different streams never share one)
+  float* qmm_ws = nullptr;  // split-K partials of the prefill GEMMs (per model: models on
+  size_t qmm_ws_floats = 0;  // different streams never share one)
   int32_t* ids = nullptr;     // [max_tokens] token ids for the embedding gather
   uint32_t* tok_u = nullptr;  // [max(max_tokens, 64)] token staging
   uint32_t* next_tok = nullptr;  // argmax output of the decode step
@@ -231,8 +231,6 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       p.N = H;
       p.K = qd;
       p.res = m->x;
-      p.part = m->qmm_ws;
-      p.part_floats = m->qmm_ws_floats;
       if (int rc = launch_qmv(p, QMV_RESIDUAL, st)) return rc;
     } else {
       if (int rc = launch_qmm_epi(QMM_RESIDUAL, m->att, L.p[SLOT_O].w, L.p[SLOT_O].s, L.p[SLOT_O].b, nullptr, nullptr,
@@ -262,8 +260,6 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       d.N = H;
       d.K = I;
       d.res = m->x;
-      d.part = m->qmm_ws;
-      d.part_floats = m->qmm_ws_floats;
       if (int rc = launch_qmv(d, QMV_RESIDUAL, st)) return rc;
     } else {
       if (int rc = launch_rms_norm(m->x, L.post_norm, m->h, M, H, cf.eps, st)) return rc;
@@ -417,9 +413,6 @@ int qwen3_alloc(const bmx_qwen3_config* cfg, int max_tokens, bmx_qwen3** out) {
   for (int sl = 0; sl < NSLOT; sl++)
     m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmm_workspace_floats(max_tokens, dims[sl][0], dims[sl][1]));
   m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmm_workspace_floats(max_tokens, cfg->vocab, H));
-  // the o and down GEMVs of up to 8 tokens may split K (no fused norm)
-  m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmvx_workspace_floats(H, cfg->n_heads * cfg->head_dim));
-  m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmvx_workspace_floats(H, cfg->inter));
   if (!rc && m->qmm_ws_floats) rc = dalloc_t(m, &m->qmm_ws, m->qmm_ws_floats);
   if (!rc) rc = dalloc_t(m, &m->ids, T);
   if (!rc) rc = dalloc_t(m, &m->tok_u, T < 64 ? 64 : T);

@@ -16,7 +16,13 @@ rotating over >= 1 GiB of distinct weights so no launch reads from the
 
 `cpu_baseline`: the C restatement of the same decode step (oracle/, OpenMP)
 on this host's cores, timed over a bounded sample of decode tokens at context
-4096 (KV positions filled synthetically instead of a CPU prefill).
+4096 (KV positions filled synthetically instead of a CPU prefill), with the
+host's CPU model, the threads used and a STREAM-triad bandwidth beside it.
+
+The other configurations run in the default invocation too and are reported
+under `config`: the qmm sweep (M = 5, 128, 512, 2048 over the eleven
+Qwen3-4B / 8B projection shapes) and greedy speculative decoding with a
+Qwen3-32B-shaped target and a Qwen3-0.6B-shaped draft.
 """
 import argparse
 import json
@@ -37,18 +43,48 @@ QMM_M = [5, 128, 512, 2048]
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
+def _profile_value(name, key):
+    """A `key: value` line of a committed profiles/ summary; None if absent."""
+    try:
+        for line in open(os.path.join(ROOT, "profiles", name)):
+            if line.startswith(key + ":"):
+                return float(line.split(":", 1)[1].split()[0])
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
 def measured_traffic():
     """HBM bytes per launch of the roofline GEMV, from the committed
     rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE scaled by a copy of
     known size); None when that summary is absent."""
-    path = os.path.join(ROOT, "profiles", "qmv_9728x2560_pmc.md")
+    v = _profile_value("qmv_9728x2560_pmc.md", "traffic_bytes_per_launch")
+    return None if v is None else int(v)
+
+
+def traced_duration_us():
+    """Average duration of the roofline GEMV in the committed rocprofv3
+    kernel trace of the default bench command (the tracer's per-dispatch
+    timestamps; the line's `achieved` uses HIP events around graph replays
+    instead); None when that summary is absent."""
+    return _profile_value("bench_default_qwen3_4b_decode.md", "roofline_kernel_trace_avg_us")
+
+
+def host_info():
+    """CPU model, logical CPUs in this process's affinity mask, OpenMP
+    threads of the oracle, and a STREAM-triad bandwidth of the host."""
+    import oracle
+
+    model = "unknown"
     try:
-        for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":")[1])
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
     except OSError:
         pass
-    return None
+    return {"cpu_model": model, "affinity_cpus": len(os.sched_getaffinity(0)), "threads": oracle.num_threads(),
+            "stream_triad_GBps": round(oracle.stream_triad_gbs(), 1)}
 
 
 def log(*a):
@@ -292,8 +328,7 @@ def cpu_baseline(tokens, ctx=4096, seed=42):
         tok = np.array([int(np.argmax(oracle.bf16_to_f32(logits)))], np.uint32)
     dt = time.time() - t0
     m.close()
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return tokens / dt, cores
+    return tokens / dt
 
 
 def main():
@@ -304,11 +339,11 @@ def main():
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--cpu-tokens", type=int, default=8, help="decode tokens in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-sweep", action="store_true")
-    ap.add_argument("--qmm-sweep", action="store_true",
-                    help="also time the quantized GEMM at M = 5, 128, 512, 2048 (4B and 8B projection shapes)")
-    ap.add_argument("--speculative", action="store_true",
-                    help="also run 32B-target / 0.6B-draft greedy speculative decoding (M = 5 verify)")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the qmv sweep")
+    ap.add_argument("--no-qmm-sweep", action="store_true",
+                    help="skip the quantized GEMM sweep at M = 5, 128, 512, 2048 (4B and 8B projection shapes)")
+    ap.add_argument("--no-speculative", action="store_true",
+                    help="skip 32B-target / 0.6B-draft greedy speculative decoding (M = 5 verify)")
     ap.add_argument("--moe", action="store_true",
                     help="also time gather_qmm on Qwen3-30B-A3B-shaped routed experts (decode, top-8 of 128)")
     ap.add_argument("--profile-roofline", action="store_true",
@@ -378,21 +413,26 @@ def main():
                           "frac": round(gbs / HBM_PEAK_GBS, 4)})
             log(f"qmv N={N} K={K}: {us:.2f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
             if (N, K) == ROOF_SHAPE:
+                tr = traced_duration_us()
                 roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                        "kernel": f"qmv M=1 N={N} K={K}", "avg_launch_us": round(us, 3), "bytes_per_launch": nb}
+                        "kernel": f"qmv M=1 N={N} K={K}", "avg_launch_us": round(us, 3), "bytes_per_launch": nb,
+                        "trace_avg_us": tr,
+                        "frac_trace": None if tr is None else round(nb / tr / 1e3 / HBM_PEAK_GBS, 4)}
 
-    qmm = qmm_sweep(bmx, torch) if args.qmm_sweep else []
-    spec = speculative_bench(bmx, torch) if args.speculative else None
+    qmm = [] if args.no_qmm_sweep else qmm_sweep(bmx, torch)
+    spec = None if args.no_speculative else speculative_bench(bmx, torch)
     moe = moe_bench(bmx, torch) if args.moe else []
 
     cpu = None
     if not args.no_cpu:
-        v, cores = cpu_baseline(args.cpu_tokens)
-        cpu = {"value": round(v, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+        host = host_info()
+        v = cpu_baseline(args.cpu_tokens)
+        cpu = {"value": round(v, 3), "unit": "tok/s", "cores": host["threads"], "kind": "port",
                "sample": f"{args.cpu_tokens} greedy decode tokens of the same Qwen3-4B shape at context 4096 "
-                         f"(KV positions 0..4095 filled synthetically), oracle/ C restatement, OpenMP"}
-        log(f"cpu baseline: {v:.3f} tok/s on {cores} threads")
+                         f"(KV positions 0..4095 filled synthetically), oracle/ C restatement, OpenMP",
+               "host": host}
+        log(f"cpu baseline: {v:.3f} tok/s on {host['threads']} threads ({host})")
 
     out = {
         "metric": "decode tok/s Qwen3-4B-shape 4-bit bs1; qmv GB/s as % of HBM peak",

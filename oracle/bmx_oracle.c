@@ -218,6 +218,15 @@ int orc_dequant_gather(const uint32_t *ids, int64_t M, int64_t rows,
   return ORC_OK;
 }
 
+/* Accumulation-order variant, for measuring the end-to-end spread that fp32
+ * summation order alone causes (a test measures the oracle against itself
+ * with this on): every fp32 reduction runs in the opposite order -- the
+ * GEMV adds its groups last to first, the GEMM its 8-wide k blocks, SDPA its
+ * keys and RMSNorm (incl. the per-head QK-norm) its squares.  Off by
+ * default; not thread-safe to toggle while a call runs. */
+static int g_reverse = 0;
+void orc_set_reverse_accumulation(int on) { g_reverse = on ? 1 : 0; }
+
 /* quantized_matmul(x, W, s, b, transpose=true, gs, 4) [MLX upstream]:
  *   y[m, n] = sum_g ( s[n,g] * sum_{k in g} q[n,k] x[m,k]
  *                    + b[n,g] * sum_{k in g} x[m,k] )
@@ -251,7 +260,8 @@ int orc_qmatmul(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
     float qrow[64];
     for (int64_t m = 0; m < M; m++) {
       float acc = 0.0f;
-      for (int64_t g = 0; g < G; g++) {
+      for (int64_t gi = 0; gi < G; gi++) {
+        const int64_t g = g_reverse ? G - 1 - gi : gi;
         const uint32_t *wg = row + g * 8;
         for (int i = 0; i < 8; i++) {
           uint32_t w = wg[i];
@@ -305,8 +315,10 @@ int orc_qmm_dequant(const uint16_t *x, const uint32_t *wq, const uint16_t *s,
         for (int64_t m = 0; m < M; m++) {
           const float *xp = xf + m * K;
           float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-          for (int64_t k = 0; k < K; k += 8)
+          for (int64_t ki = 0; ki < K; ki += 8) {
+            const int64_t k = g_reverse ? K - 8 - ki : ki;
             for (int j = 0; j < 8; j++) a[j] += wrow[k + j] * xp[k + j];
+          }
           y[m * N + n] = f2bf(((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7])));
         }
       }
@@ -383,7 +395,8 @@ void orc_rms_norm(const uint16_t *x, const uint16_t *w, uint16_t *y,
   for (int64_t r = 0; r < rows; r++) {
     const uint16_t *xr = x + r * dim;
     float ss = 0.0f;
-    for (int64_t i = 0; i < dim; i++) {
+    for (int64_t ii = 0; ii < dim; ii++) {
+      const int64_t i = g_reverse ? dim - 1 - ii : ii;
       float v = bf2f(xr[i]);
       ss += v * v;
     }
@@ -491,7 +504,8 @@ void orc_sdpa(const uint16_t *q, const uint16_t *k, const uint16_t *v,
         mx = a > mx ? a : mx;
       }
       float l = 0.0f;
-      for (int64_t j = 0; j < nk; j++) {
+      for (int64_t ji = 0; ji < nk; ji++) {
+        const int64_t j = g_reverse ? nk - 1 - ji : ji;
         float p = expf(sc[j] - mx);
         l += p;
         for (int64_t d = 0; d < D; d++) acc[d] += p * bf2f(vh[j * D + d]);
@@ -933,4 +947,57 @@ done:
   free(tl);
   free(dl);
   return rc;
+}
+
+/* ------------------------------------------------------------------ */
+/* Host measurement helpers for the CPU baseline (not part of the path): */
+/* the OpenMP thread count the oracle runs with, and a STREAM-style      */
+/* triad a[i] = b[i] + s * c[i] over n doubles (24 n bytes moved per     */
+/* pass), best of `reps` passes, in GB/s.                                */
+/* ------------------------------------------------------------------ */
+int orc_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+double orc_stream_triad_gbs(int64_t n, int reps) {
+  double *a = (double *)malloc(sizeof(double) * (size_t)n);
+  double *b = (double *)malloc(sizeof(double) * (size_t)n);
+  double *c = (double *)malloc(sizeof(double) * (size_t)n);
+  if (!a || !b || !c) {
+    free(a);
+    free(b);
+    free(c);
+    return 0.0;
+  }
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; i++) {
+    a[i] = 0.0;
+    b[i] = 1.0;
+    c[i] = 2.0;
+  }
+  double best = 0.0;
+  for (int r = 0; r < reps; r++) {
+#ifdef _OPENMP
+    const double t0 = omp_get_wtime();
+#endif
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; i++) a[i] = b[i] + 3.0 * c[i];
+#ifdef _OPENMP
+    const double dt = omp_get_wtime() - t0;
+#else
+    const double dt = 1.0;
+#endif
+    const double gbs = 24.0 * (double)n / dt / 1e9;
+    if (gbs > best) best = gbs;
+  }
+  volatile double sink = a[n / 2];
+  (void)sink;
+  free(a);
+  free(b);
+  free(c);
+  return best;
 }

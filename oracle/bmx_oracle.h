@@ -94,6 +94,9 @@ void orc_sdpa(const uint16_t *q, const uint16_t *k, const uint16_t *v,
 void orc_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *y, int64_t n);
 void orc_add(const uint16_t *a, const uint16_t *b, uint16_t *y, int64_t n);
 void orc_argmax_rows(const uint16_t *x, int64_t rows, int64_t n, uint32_t *out);
+/* Test knob: reverse the order of every fp32 reduction (GEMV, GEMM, SDPA,
+ * RMSNorm): measures the spread summation order alone causes.  Default off. */
+void orc_set_reverse_accumulation(int on);
 
 /* ---- Qwen3 model ----------------------------------------------------- */
 typedef struct {
@@ -131,6 +134,10 @@ int orc_speculative_generate(orc_qwen3 *target, orc_kv *tkv, orc_qwen3 *draft,
                              int max_new, int spec_k, const uint32_t *eos,
                              int n_eos, uint32_t *out, int *n_out,
                              int64_t *stats);
+
+/* host measurement helpers for the CPU baseline */
+int orc_num_threads(void);
+double orc_stream_triad_gbs(int64_t n, int reps);
 
 /* error codes shared with the HIP library */
 #define ORC_OK 0

@@ -64,6 +64,9 @@ _SIGS = {
     "orc_qwen3_forward": (INT, [P, P, P, INT, INT, P]),
     "orc_generate_greedy": (INT, [P, P, P, INT, INT, P, INT, P, P]),
     "orc_speculative_generate": (INT, [P, P, P, P, P, INT, INT, INT, P, INT, P, P, P]),
+    "orc_set_reverse_accumulation": (None, [INT]),
+    "orc_num_threads": (INT, []),
+    "orc_stream_triad_gbs": (ctypes.c_double, [I64, INT]),
 }
 
 
@@ -87,6 +90,30 @@ def lib():
 
 def _p(a):
     return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def num_threads():
+    """OpenMP threads the oracle's parallel loops use."""
+    return int(lib().orc_num_threads())
+
+
+def stream_triad_gbs(n=1 << 26, reps=5):
+    """Host memory bandwidth: best-of-`reps` STREAM triad over n doubles."""
+    return float(lib().orc_stream_triad_gbs(n, reps))
+
+
+class reversed_accumulation:
+    """Context manager: inside it every fp32 reduction of the oracle (GEMV,
+    GEMM, SDPA, RMSNorm) adds its terms in reverse order (the spread fp32
+    summation order alone causes)."""
+
+    def __enter__(self):
+        lib().orc_set_reverse_accumulation(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_reverse_accumulation(0)
+        return False
 
 
 def _chk(rc):

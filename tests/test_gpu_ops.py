@@ -236,7 +236,8 @@ def test_qmm_vs_oracle(gpu, orc, M, N, K):
     assert _close(yb, orc.qmm_dequant(xb, wq, sb, bb), ulps=2, floor=1e-4) == 1.0
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 1024, 2560), (24, 768, 2048), (5, 5120, 8192), (1, 4096, 2560)])
+@pytest.mark.parametrize("M,N,K", [(64, 1024, 2560), (24, 768, 2048), (16, 2048, 4096), (5, 5120, 8192),
+                                   (1, 4096, 2560)])
 def test_qmatmul_ws_matches_qmatmul(gpu, M, N, K):
     """bmx_qmatmul_affine_ws with a workspace of exactly
     bmx_qmatmul_workspace_bytes(M, N, K) bytes gives the bits of

@@ -134,3 +134,22 @@ def test_qmv_linearity_full_lm_head(gpu, orc):
     yo = gpu.quantized_matmul(odd, w, s, b).float()
     torch.cuda.synchronize()
     assert max_rel_err((ye + yo).cpu().numpy(), y1.float().cpu().numpy()) < 1e-2
+
+
+@pytest.mark.parametrize("N,K", [(4096, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (2560, 9728),
+                                 (151936, 2560), (10240, 5120), (5120, 8192), (5120, 25600), (576, 320)])
+def test_gemv_rows_independent_of_row_count(gpu, N, K):
+    """Each row of an M-row GEMV (M = 2..8) has the bits of the same row
+    computed alone: the single-phase, persistent and phased kernels share one
+    per-row arithmetic, and the lanes per weight row depend on N and K only
+    (this is what makes greedy speculative decoding exact)."""
+    import torch
+
+    print(f"row invariance N={N} K={K}", flush=True)
+    w, s, b = gpu.init_qlinear(4000 + N % 97, N, K)
+    x = gpu.fill_normal_bf16(4100 + K % 89, (8, K))
+    singles = [torch_bf16_bits(gpu.quantized_matmul(x[i:i + 1], w, s, b)) for i in range(8)]
+    for M in range(2, 9):
+        y = torch_bf16_bits(gpu.quantized_matmul(x[:M].contiguous(), w, s, b))
+        for i in range(M):
+            np.testing.assert_array_equal(y[i], singles[i][0], err_msg=f"M={M} row {i}")

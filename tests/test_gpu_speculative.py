@@ -1,0 +1,169 @@
+"""Greedy speculative decoding is exact on the GPU.
+
+The reference's algorithm is "greedy variant -- exact, no quality loss"
+(crates/base-mlx-core/src/speculative.rs:3-6).  It holds here bit for bit
+because a verify forward of M tokens computes every row with the same
+operations as a single-token decode of that position: the GEMVs share one
+per-row arithmetic whatever M (tests/test_gpu_qmv.py), and decode attention
+reduces every query row the same way whatever the tile of rows.  So:
+  * the rows of an M-token forward equal M single-token decode steps, logits
+    and KV cache rows, bit for bit;
+  * speculative output equals greedy output token for token (any draft);
+  * against the oracle, the GPU's tokens are the oracle's argmax at every
+    step except where the oracle's own top-2 logits are a rounding tie.
+"""
+import numpy as np
+import pytest
+
+from _util import bf16_to_f32, torch_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(hidden=512, inter=1536, layers=3, n_heads=8, n_kv_heads=2, head_dim=128, vocab=4096)
+QWEN3_0_6B = dict(hidden=1024, inter=3072, layers=28, n_heads=16, n_kv_heads=8, head_dim=128, vocab=151936)
+QWEN3_4B = dict(hidden=2560, inter=9728, layers=36, n_heads=32, n_kv_heads=8, head_dim=128, vocab=151936)
+QWEN3_32B = dict(hidden=5120, inter=25600, layers=64, n_heads=64, n_kv_heads=8, head_dim=128, vocab=151936, tied=0)
+
+
+def _gpu(gpu, shape, seed, max_tokens=64, **kw):
+    return gpu.Qwen3(gpu.qwen3_config(**{**shape, **kw}), seed, 0.02, max_tokens=max_tokens)
+
+
+def _verify_rows_equal_decode_steps(gpu, model, prefill, toks, cap, fill=0):
+    """Logits and KV rows of one forward over `toks` == those of len(toks)
+    single-token graph decode steps, after the same prefill (or the same
+    synthetic fill of `fill` positions)."""
+    a, b = model.new_cache(cap), model.new_cache(cap)
+    for c in (a, b):
+        if fill:
+            c.fill_synthetic(77, fill)
+        else:
+            model.forward(c, prefill)
+    p0 = a.seq_len
+    steps = [torch_bf16_bits(model.decode_step(a, int(t), want_logits=True)[1]) for t in toks]
+    rows = torch_bf16_bits(model.forward(b, toks, all_logits=True))
+    for i in range(len(toks)):
+        np.testing.assert_array_equal(rows[i], steps[i], err_msg=f"row {i}")
+    n = model.cfg.layers
+    for layer in sorted({0, n // 2, n - 1}):
+        for kv in (0, 1):
+            np.testing.assert_array_equal(a.layer_numpy(layer, kv)[:, p0:p0 + len(toks)],
+                                          b.layer_numpy(layer, kv)[:, p0:p0 + len(toks)])
+
+
+@pytest.mark.parametrize("M", [2, 3, 5, 8])
+def test_small_verify_rows_equal_decode_steps(gpu, orc, M):
+    m = _gpu(gpu, SMALL, 21)
+    prompt = orc.fill_tokens(31, 17, SMALL["vocab"])
+    _verify_rows_equal_decode_steps(gpu, m, prompt, orc.fill_tokens(32 + M, M, SMALL["vocab"]), 64)
+
+
+def test_4b_verify_rows_equal_decode_steps(gpu, orc):
+    """The Qwen3-4B shape (36 layers): a 5-token verify forward at context
+    300 equals five decode steps."""
+    m = _gpu(gpu, QWEN3_4B, 42, max_tokens=16)
+    _verify_rows_equal_decode_steps(gpu, m, None, orc.fill_tokens(40, 5, QWEN3_4B["vocab"]), 512, fill=300)
+
+
+def test_32b_shape_verify_rows_equal_decode_steps(gpu, orc):
+    """The Qwen3-32B shape (2 of its layers, untied head; K = 25600 down
+    projection on the phased GEMV): verify at context 2048 == decode."""
+    m = _gpu(gpu, QWEN3_32B, 13, max_tokens=16, layers=2)
+    _verify_rows_equal_decode_steps(gpu, m, None, orc.fill_tokens(41, 5, QWEN3_32B["vocab"]), 2304, fill=2048)
+
+
+def _spec_equals_greedy(gpu, target, draft, prompt, n, spec_k=5):
+    greedy = target.generate_greedy(target.new_cache(len(prompt) + n + 16), prompt, n, eos=())
+    spec, stats = gpu.speculative_generate(target, target.new_cache(len(prompt) + n + 16), draft,
+                                           draft.new_cache(len(prompt) + n + 16), prompt, n, spec_k=spec_k, eos=())
+    print(f"speculative: {len(spec)} tokens, iterations {stats[0]}, drafted {stats[1]}, accepted {stats[2]}",
+          flush=True)
+    np.testing.assert_array_equal(spec, greedy)
+    return greedy, stats
+
+
+def test_small_speculative_equals_greedy_token_for_token(gpu, orc):
+    """3-layer target, 128 tokens, with three drafts: an unrelated 1-layer
+    model (nothing accepted), the target's own first layer (a truncated copy:
+    some accepted) and an identical twin (all accepted)."""
+    target = _gpu(gpu, SMALL, 7)
+    prompt = orc.fill_tokens(14, 10, SMALL["vocab"])
+    for draft, spec_k in ((_gpu(gpu, SMALL, 8, layers=1), 5), (_gpu(gpu, SMALL, 7, layers=1), 5),
+                          (_gpu(gpu, SMALL, 7), 5), (_gpu(gpu, SMALL, 7, layers=2), 3)):
+        _, stats = _spec_equals_greedy(gpu, target, draft, prompt, 128, spec_k)
+    assert stats[2] > 0
+
+
+def test_speculative_continues_a_filled_cache(gpu, orc):
+    """Caches that already hold context: the rewinds are relative to where
+    each cache starts (the oracle does the same), and the result equals
+    greedy decoding from that context."""
+    target, draft = _gpu(gpu, SMALL, 7), _gpu(gpu, SMALL, 7, layers=1)
+    ctx = orc.fill_tokens(50, 20, SMALL["vocab"])
+    prompt = orc.fill_tokens(51, 6, SMALL["vocab"])
+    tc, dc, gc = target.new_cache(256), draft.new_cache(256), target.new_cache(256)
+    target.forward(tc, ctx)
+    draft.forward(dc, ctx)
+    target.forward(gc, ctx)
+    spec, _ = gpu.speculative_generate(target, tc, draft, dc, prompt, 48, spec_k=5, eos=())
+    greedy = target.generate_greedy(gc, prompt, 48, eos=())
+    np.testing.assert_array_equal(spec, greedy)
+    om, odm = orc.Qwen3(orc.make_config(**SMALL), 7, 0.02), orc.Qwen3(orc.make_config(**{**SMALL, "layers": 1}), 7, 0.02)
+    otc, odc = om.new_cache(256), odm.new_cache(256)
+    om.forward(otc, ctx)
+    odm.forward(odc, ctx)
+    ospec, _ = orc.speculative_generate(om, otc, odm, odc, prompt, 48, spec_k=5, eos=())
+    ogc = om.new_cache(256)
+    om.forward(ogc, ctx)
+    np.testing.assert_array_equal(ospec, orc.generate_greedy(om, ogc, prompt, 48, eos=()))
+
+
+def _agree_with_oracle_greedy(orc, om, tokens, prompt, cap):
+    """The oracle replays `tokens` (teacher forcing): each must be its
+    argmax, except where its top-2 logits are within 2 bf16 ulps (a tie that
+    rounding decides); returns the count of such ties taken differently."""
+    oc = om.new_cache(cap)
+    logits = om.forward(oc, prompt)
+    ties = 0
+    for i, t in enumerate(tokens):
+        o = bf16_to_f32(logits).astype(np.float64)
+        if int(np.argmax(o)) != int(t):
+            top = np.sort(o)[-2:]
+            assert top[1] - top[0] <= 2 * abs(top[1]) * 2.0 ** -7, (i, int(t), int(np.argmax(o)))
+            ties += 1
+        logits = om.forward(oc, [int(t)])
+    return ties
+
+
+def test_small_speculative_vs_oracle(gpu, orc):
+    target, draft = _gpu(gpu, SMALL, 7), _gpu(gpu, SMALL, 7, layers=1)
+    om = orc.Qwen3(orc.make_config(**SMALL), 7, 0.02)
+    odm = orc.Qwen3(orc.make_config(**{**SMALL, "layers": 1}), 7, 0.02)
+    prompt = orc.fill_tokens(14, 10, SMALL["vocab"])
+    spec, _ = gpu.speculative_generate(target, target.new_cache(256), draft, draft.new_cache(256), prompt, 128,
+                                       spec_k=5, eos=())
+    ospec, ostats = orc.speculative_generate(om, om.new_cache(256), odm, odm.new_cache(256), prompt, 128, spec_k=5,
+                                             eos=())
+    print(f"oracle speculative: drafted {ostats[1]}, accepted {ostats[2]}", flush=True)
+    # the oracle's own speculative output is its greedy output
+    np.testing.assert_array_equal(ospec, orc.generate_greedy(om, om.new_cache(256), prompt, 128, eos=()))
+    assert _agree_with_oracle_greedy(orc, om, spec, prompt, 256) <= 2
+
+
+def test_4b_target_0_6b_draft_speculative(gpu, orc):
+    """The Qwen3-4B-shaped target with a Qwen3-0.6B-shaped draft (config 4's
+    draft; the 4B shape keeps the oracle side fast): 128 speculative tokens
+    equal 128 greedy tokens exactly, and agree with the oracle's greedy
+    decode except at rounding ties.  Through 36 random-init layers such ties
+    are common: the oracle against itself with its summation order reversed
+    agrees on 88-94% of greedy tokens, so up to 15% may be taken the other
+    way (each one must be a tie)."""
+    print("building 4B target + 0.6B draft", flush=True)
+    target = _gpu(gpu, QWEN3_4B, 42, max_tokens=16)
+    draft = _gpu(gpu, QWEN3_0_6B, 43, max_tokens=16)
+    prompt = orc.fill_tokens(60, 12, QWEN3_4B["vocab"])
+    greedy, _ = _spec_equals_greedy(gpu, target, draft, prompt, 128)
+    om = orc.Qwen3(orc.make_config(**QWEN3_4B), 42, 0.02)
+    ties = _agree_with_oracle_greedy(orc, om, greedy, prompt, 256)
+    print(f"4B: {ties} of 128 greedy tokens took the other side of a rounding tie", flush=True)
+    assert ties <= 0.15 * 128
