@@ -61,7 +61,8 @@ struct FuseParams {
 // The split partials travel between workgroups on different XCDs (each with
 // its own L2) through agent-scope atomic loads and stores (relaxed, issued
 // with sc1: coherent across the XCDs); the arrival counter's agent-scope
-// acquire-release increment orders them (one per workgroup, not per wave).
+// release increment and the last arrival's acquire fence order them (one
+// per workgroup, not per wave).
 // Pairs of floats move as one 8-byte access (8-byte aligned addresses).
 __device__ __forceinline__ void store_agent2(float* a, float x, float y) {
   const uint64_t v = static_cast<uint64_t>(__float_as_uint(x)) | (static_cast<uint64_t>(__float_as_uint(y)) << 32);
@@ -434,13 +435,16 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
   __syncthreads();
   if (threadIdx.x == 0) {
-    // Arrival: an agent-scope acquire-release increment that wraps to 0 on
-    // the ns-th arrival (ready for the next call).  Release publishes this
-    // workgroup's partials (stored by all its threads before the barrier);
-    // the last arrival's acquire makes every other workgroup's partials
-    // visible to the merge below (its threads read after the next barrier).
+    // Arrival: an agent-scope release increment that wraps to 0 on the
+    // ns-th arrival (ready for the next call); the release publishes this
+    // workgroup's partials (stored by all its threads before the barrier).
+    // Only the last arrival acquires -- an agent-scope acquire fence after
+    // reading the final count synchronizes with every release before it --
+    // so only that workgroup pays the cache invalidation; its threads read
+    // the partials after the next barrier.
     last = __builtin_amdgcn_atomic_inc32(p.cnt + kvh * gridDim.z + blockIdx.z, static_cast<unsigned>(p.ns - 1),
-                                         __ATOMIC_ACQ_REL, "agent") == static_cast<unsigned>(p.ns - 1);
+                                         __ATOMIC_RELEASE, "agent") == static_cast<unsigned>(p.ns - 1);
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (!last) return;

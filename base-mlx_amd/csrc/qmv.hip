@@ -64,9 +64,11 @@ __device__ __forceinline__ void gemv_store(const QmvParams& p, int seg, int m, i
 // Phased GEMV: any K, s / b in 16-byte units or one group at a time.  x and
 // the workgroup's s|b are staged in LDS one phase of p.kp columns at a time
 // (p.kp a multiple of 32 S, so lane sl still meets its chunks c = sl mod S
-// in increasing order, as in the single-phase kernels); W streams U chunks
-// ahead in a register ring.  S (lanes per row) is a launch parameter.
-template <int MT, int EPI>
+// in increasing order, as in the single-phase kernels).  W streams U chunks
+// ahead in a register ring that runs across phase boundaries (W does not
+// wait for x): lane chunk i sits in slot i mod U.  S (lanes per row) is a
+// launch parameter.
+template <int MT, int EPI, int U>
 __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p, const int S) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NH = (EPI == QMV_SWIGLU) ? 2 : 1;  // weight rows per lane
@@ -110,8 +112,6 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p, const 
     for (int h = 0; h < NH; h++) wrow[h] = p.seg[EPI == QMV_SWIGLU ? h : seg].w + rr * (K / 8);
   }
 
-  // Register ring of U chunks (see header).
-  constexpr int U = (NH == 1 && MT == 1) ? 8 : 4;
   constexpr int XU = 4;  // x words per thread per staging batch
   constexpr int SU = 2;  // s|b units per thread per staging batch
   uint4 wv[U][NH];
@@ -123,14 +123,13 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p, const 
       wv[u][h] = make_uint4(t.x, t.y, t.z, t.w);
     }
   };
-  // the first phase's loads go out before anything else
-  {
-    const int nc0 = min(p.kp, K) / 32;
-    const int n_i0 = sl < nc0 ? (nc0 - sl + S - 1) / S : 0;
+  // the lane's chunks over all of K: c = sl + S i, i < n_all; the first U
+  // go out before anything else
+  const int C = K / 32;
+  const int n_all = sl < C ? (C - sl + S - 1) / S : 0;
 #pragma unroll
-    for (int u = 0; u < U; u++)
-      if (u < n_i0) load_chunk(u, sl + S * u);
-  }
+  for (int u = 0; u < U; u++)
+    if (u < n_all) load_chunk(u, sl + S * u);
 
   // Optional fused RMSNorm of each x row (fast::rms_norm, qwen3.rs:50-55):
   //   h = w * bf16(x * rsqrt(mean(x^2) + eps)); thread t sums units t,
@@ -161,20 +160,16 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p, const 
 #pragma unroll
     for (int m = 0; m < MT; m++) acc[h][m] = 0.0f;
 
-  for (int k0 = 0; k0 < K; k0 += p.kp) {
+  for (int k0 = 0, i0 = 0; k0 < K; k0 += p.kp) {
     const int kpp = min(p.kp, K - k0);
     const int words = kpp / 8;  // multiple of 8
     const int total = MT * words;
     const int ncp = kpp / 32;   // chunks in this phase
     const int gpp = kpp / 64;   // groups in this phase
-    const int cbase = k0 / 32;
+    const int cbase = k0 / 32;  // a multiple of S
     const int gbase = k0 / 64;
-    const int n_i = sl < ncp ? (ncp - sl + S - 1) / S : 0;  // chunks of this lane
-    if (k0 > 0) {
-#pragma unroll
-      for (int u = 0; u < U; u++)
-        if (u < n_i) load_chunk(u, cbase + sl + S * u);
-    }
+    // this lane's chunks of the phase: i in [i0, i1)
+    const int i1 = sl < cbase + ncp ? (cbase + ncp - sl + S - 1) / S : 0;
     __syncthreads();  // previous phase finished reading LDS
     // ---- stage x[:, k0:k0+kpp] (pair-permuted, chunk sums) and the
     //      workgroup's s|b words.  Each batch issues all of its loads before
@@ -262,14 +257,15 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p, const 
     }
     __syncthreads();
 
-    // ---- stream W over this phase's chunks ----
+    // ---- stream W over this phase's chunks (slot u = i mod U; the
+    // unrolled rounds start at the ring-aligned chunk at or below i0) ----
     const NibbleK nk = nibble_consts();
-    for (int i0 = 0; i0 < n_i; i0 += U) {
+    for (int ib = (i0 / U) * U; ib < i1; ib += U) {
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        const int i = i0 + u;
-        if (i < n_i) {
-          const int c = sl + S * i;  // chunk within the phase
+        const int i = ib + u;
+        if (i >= i0 && i < i1) {
+          const int c = sl + S * i - cbase;  // chunk within the phase
           float sv[NH], bb[NH];
 #pragma unroll
           for (int h = 0; h < NH; h++) gemv_sb(sbs[(h * RB + rl) * GP + (c >> 1)], sv[h], bb[h]);
@@ -283,10 +279,11 @@ __global__ void __launch_bounds__(kThreads) qmv_kernel(const QmvParams p, const 
               for (int h = 0; h < NH; h++) acc[h][m] = gemv_chunk(wv[u][h], x0, x1, x2, x3, sv[h], bb[h], sx, acc[h][m], nk);
             }
           }
-          if (i + U < n_i) load_chunk(u, cbase + c + S * U);
+          if (i + U < n_all) load_chunk(u, sl + S * (i + U));
         }
       }
     }
+    i0 = i1;
   }
 
   // ---- reduce the S lanes of each row and write ----
@@ -959,6 +956,9 @@ int try_launch_qmvp(QmvEpilogue epi, int mt, int S, const QmvParams& p, int ntil
   }
 }
 
+// W chunks in flight per lane in the phased kernel (its register ring)
+constexpr int kRing = 8;
+
 template <int MT>
 int launch_epi(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t lds, hipStream_t st) {
   auto go = [&](auto kern) {
@@ -967,9 +967,9 @@ int launch_epi(QmvEpilogue epi, int S, const QmvParams& p, int blocks, size_t ld
     return check_launch("qmv");
   };
   switch (epi) {
-    case QMV_STORE: return go(qmv_kernel<MT, QMV_STORE>);
-    case QMV_RESIDUAL: return go(qmv_kernel<MT, QMV_RESIDUAL>);
-    default: return go(qmv_kernel<MT, QMV_SWIGLU>);
+    case QMV_STORE: return go(qmv_kernel<MT, QMV_STORE, kRing>);
+    case QMV_RESIDUAL: return go(qmv_kernel<MT, QMV_RESIDUAL, kRing>);
+    default: return go(qmv_kernel<MT, QMV_SWIGLU, kRing>);
   }
 }
 
@@ -1040,19 +1040,6 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   const int mt = gr.mt, S = gr.S;
   const int nh = epi == QMV_SWIGLU ? 2 : 1;
   const int rows_per_block = gr.rows_per_block;
-  // LDS per phase: x chunks (80 B + 4 B sum per 32 columns per x row) and
-  // the workgroup's s|b words (4 B per 64 columns per weight row).  A phase
-  // is a multiple of 32 S columns (whole rounds of the S lanes over the
-  // chunks), so the phase split never changes which lane adds which chunk.
-  const double per_col = mt * (kChunkBytes + 4) / 32.0 + nh * rows_per_block * 4 / 64.0;
-  const int unit = std::max(512, 32 * S);
-  int kp = static_cast<int>(kLdsBudget / per_col);
-  kp = std::max(unit, (kp / unit) * unit);
-  p.kp = std::min(kp, p.K);
-  const int CP = p.kp / 32, GP = p.kp / 64;
-  const size_t lds = static_cast<size_t>(mt) * CP * (kChunkBytes + 4) +
-                     static_cast<size_t>(nh) * rows_per_block * GP * 4 + 4 * static_cast<size_t>(mt) * 4 +
-                     (p.amax ? static_cast<size_t>(mt) * rows_per_block * 8 : 0);
   // every segment starts on a workgroup boundary (the kernel reads its
   // segment's fields with scalar loads)
   const int blocks = gr.blocks;
@@ -1078,6 +1065,20 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
     const int rc = try_launch_qmv1(epi, mt, S, p, blocks, stream);
     if (rc != kNoFit) return rc;
   }
+  // the phased kernel.  LDS per phase: x chunks (80 B + 4 B sum per 32
+  // columns per x row) and the workgroup's s|b words (4 B per 64 columns per
+  // weight row).  A phase is a multiple of 32 S columns (whole rounds of the
+  // S lanes over the chunks), so the phase split never changes which lane
+  // adds which chunk.
+  const double per_col = mt * (kChunkBytes + 4) / 32.0 + nh * rows_per_block * 4 / 64.0;
+  const int unit = std::max(512, 32 * S);
+  int kp = static_cast<int>(kLdsBudget / per_col);
+  kp = std::max(unit, (kp / unit) * unit);
+  p.kp = std::min(kp, p.K);
+  const int CP = p.kp / 32, GP = p.kp / 64;
+  const size_t lds = static_cast<size_t>(mt) * CP * (kChunkBytes + 4) +
+                     static_cast<size_t>(nh) * rows_per_block * GP * 4 + 4 * static_cast<size_t>(mt) * 4 +
+                     (p.amax ? static_cast<size_t>(mt) * rows_per_block * 8 : 0);
   switch (mt) {
     case 1: return launch_epi<1>(epi, S, p, blocks, lds, stream);
     case 2: return launch_epi<2>(epi, S, p, blocks, lds, stream);

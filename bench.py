@@ -308,6 +308,29 @@ def profile_roofline(bmx, torch, launches=200):
         f"10 copies of {256 << 20} bytes")
 
 
+def profile_mfma(bmx, torch, launches=20):
+    """Counter-collection workload for the matrix-core kernels: the GEMM at
+    M = 2048 on the 4B gate/up (9728 x 2560) and 8B (12288 x 4096) shapes,
+    and causal prefill attention over 4096 tokens at the Qwen3-4B head layout
+    (32 q / 8 kv heads, head_dim 128), each launched `launches` times."""
+    for (N, K) in [(9728, 2560), (12288, 4096)]:
+        w, s, b = bmx.init_qlinear(7, N, K)
+        x = bmx.fill_normal_bf16(8, (2048, K))
+        y = torch.empty(2048, N, dtype=torch.bfloat16, device="cuda")
+        for _ in range(launches):
+            bmx.quantized_matmul(x, w, s, b, out=y)
+        torch.cuda.synchronize()
+        log(f"profile-mfma: {launches} GEMMs M=2048 N={N} K={K} ({2 * 2048 * N * K:.3e} flop each)")
+    T = 4096
+    q = bmx.fill_normal_bf16(9, (32, T, 128))
+    k = bmx.fill_normal_bf16(10, (8, T, 128))
+    v = bmx.fill_normal_bf16(11, (8, T, 128))
+    for _ in range(launches):
+        bmx.attention(q, k, v, 0, use_workspace=False)
+    torch.cuda.synchronize()
+    log(f"profile-mfma: {launches} causal prefill attentions, 4096 tokens, 32 q / 8 kv heads")
+
+
 def cpu_baseline(tokens, ctx=4096, seed=42):
     """Oracle decode of `tokens` tokens at context `ctx` on the host cores."""
     import numpy as np
@@ -348,6 +371,8 @@ def main():
                     help="also time gather_qmm on Qwen3-30B-A3B-shaped routed experts (decode, top-8 of 128)")
     ap.add_argument("--profile-roofline", action="store_true",
                     help="only run the roofline GEMV and a copy of known size (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-mfma", action="store_true",
+                    help="only run the M = 2048 GEMMs and a 4096-token prefill attention (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)", file=sys.stderr)
@@ -361,6 +386,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.profile_roofline:
         profile_roofline(bmx, torch)
+        return
+    if args.profile_mfma:
+        profile_mfma(bmx, torch)
         return
     cap = args.prompt + args.steps
     assert args.prompt + max(args.steps, args.warmup) <= cap
