@@ -97,6 +97,8 @@ int qmatmul(const bmx_bf16* x, const uint32_t* w, const bmx_bf16* scales, const 
   p.seg[0] = QmvSegment{w, scales, biases, y, static_cast<int>(N), 0};
   p.x = x;
   p.m = static_cast<int>(M);
+  p.part = ws;  // the K-split matrix-core GEMV's partials
+  p.part_floats = ws_floats;
   return launch_qmv(p, QMV_STORE, stream);
 }
 
@@ -110,9 +112,9 @@ extern "C" int bmx_qmatmul_affine(const bmx_bf16* x, const uint32_t* w, const bm
 
 extern "C" size_t bmx_qmatmul_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64 || N > INT32_MAX || K > INT32_MAX || M > INT32_MAX) return 0;
-  // the GEMV (M <= 8) never splits K
   if (M > 8) return qmm_need_floats(QMM_STORE, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)) * 4;
-  return 0;
+  // the GEMV splits K only on the matrix-core path (large N x K)
+  return qmvx_workspace_floats(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)) * 4;
 }
 
 extern "C" int bmx_qmatmul_affine_ws(const bmx_bf16* x, const uint32_t* w, const bmx_bf16* scales,

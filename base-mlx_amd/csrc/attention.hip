@@ -166,11 +166,11 @@ constexpr int kFuseMaxM = 16;    // new tokens of the fused prologue
 constexpr int kQS = kD + 8;      // LDS row stride of the prologue's q / k rows
 constexpr int kCounters = 1024;  // arrival counters at the head of the workspace
 
-template <int RMAX, bool FUSED>
-__global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnParams p, const FuseParams f) {
-  __shared__ __align__(16) float ps[kDecWaves][kDecWaveKeys][RMAX];
-  __shared__ __align__(16) float os[kDecWaves][kMergeRows][kD];
-  __shared__ float ms[kDecWaves][RMAX], ls[kDecWaves][RMAX];
+template <int RMAX, bool FUSED, int NW>
+__global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p, const FuseParams f) {
+  __shared__ __align__(16) float ps[NW][kDecWaveKeys][RMAX];
+  __shared__ __align__(16) float os[NW][kMergeRows][kD];
+  __shared__ float ms[NW][RMAX], ls[NW][RMAX];
   __shared__ __align__(16) uint16_t qs[FUSED ? RMAX : 1][kQS];
   __shared__ __align__(16) uint16_t kn[FUSED ? kFuseMaxM : 1][kQS];
   __shared__ __align__(16) uint16_t vn[FUSED ? kFuseMaxM : 1][kD];
@@ -193,7 +193,7 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   // ---- fused prologue, part 1: raw rows of this wave's items (issued first,
   // so that waiting for them does not wait for the K / V loads) ----
   // items: it < RT: q row r0 + it; else new token t_lo + it - RT
-  constexpr int kItems = FUSED ? (RMAX + kFuseMaxM + kDecWaves - 1) / kDecWaves : 0;
+  constexpr int kItems = FUSED ? (RMAX + kFuseMaxM + NW - 1) / NW : 0;
   const int t_lo = max(0, kbase - offset);
   const int t_hi = min(p.M, kbase + p.kps - offset);
   const int n_items = RT + max(0, t_hi - t_lo);
@@ -206,7 +206,7 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
     freq = f.tab.inv_freq[lane];
 #pragma unroll
     for (int u = 0; u < kItems; u++) {
-      const int it = wave + u * kDecWaves;
+      const int it = wave + u * NW;
       const bool is_q = it < RT;
       const int rg = r0 + min(it, RT - 1), j = rg / tn, i = rg - j * tn;
       const int64_t krow = static_cast<int64_t>(min(max(t_lo + it - RT, 0), p.M - 1)) * p.Hkv + kvh;
@@ -249,7 +249,7 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
     // ---- fused prologue, part 2: norm + rope into LDS (and the caches) ----
 #pragma unroll
     for (int u = 0; u < kItems; u++) {
-      const int it = wave + u * kDecWaves;
+      const int it = wave + u * NW;
       if (it < n_items) {
         const bool is_q = it < RT;
         const int t = is_q ? (r0 + it) % tn : t_lo + it - RT;
@@ -402,17 +402,17 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
     }
     __syncthreads();
     const int nr = min(kMergeRows, RT - h0);
-    for (int e = threadIdx.x; e < nr * (kD / 4); e += 64 * kDecWaves) {
+    for (int e = threadIdx.x; e < nr * (kD / 4); e += 64 * NW) {
       const int rr = e / (kD / 4), d4 = e - rr * (kD / 4);
       const int r = h0 + rr;
       float m = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < kDecWaves; w++) m = fmaxf(m, ms[w][r]);
+      for (int w = 0; w < NW; w++) m = fmaxf(m, ms[w][r]);
       float l = 0.0f;
       float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if (m != -INFINITY) {
 #pragma unroll
-        for (int w = 0; w < kDecWaves; w++) {
+        for (int w = 0; w < NW; w++) {
           if (ms[w][r] == -INFINITY) continue;
           const float a = expf(ms[w][r] - m);
           const float4 ow = *reinterpret_cast<const float4*>(&os[w][rr][d4 * 4]);
@@ -450,7 +450,7 @@ __global__ void __launch_bounds__(64 * kDecWaves) attn_decode_kernel(const AttnP
   if (!last) return;
   // (Two waves per row, each folding half of the splits and merged through
   // LDS, measured 2% slower end to end.)
-  for (int r = wave; r < RT; r += kDecWaves)
+  for (int r = wave; r < RT; r += NW)
     store_pair(p, kvh * R + r0 + r, lane, combine_range(p, kvh * R + r0 + r, lane, 0, p.ns));
 }
 
@@ -757,9 +757,9 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
 #define BMX_DECODE_LAUNCH(RM)                                                                   \
   do {                                                                                          \
     if (fuse)                                                                                   \
-      hipLaunchKernelGGL((attn_decode_kernel<RM, true>), grid, block, 0, stream, p, f);         \
+      hipLaunchKernelGGL((attn_decode_kernel<RM, true, kDecWaves>), grid, block, 0, stream, p, f);  \
     else                                                                                        \
-      hipLaunchKernelGGL((attn_decode_kernel<RM, false>), grid, block, 0, stream, p, f);        \
+      hipLaunchKernelGGL((attn_decode_kernel<RM, false, kDecWaves>), grid, block, 0, stream, p, f); \
   } while (0)
   if (rmax == 4)
     BMX_DECODE_LAUNCH(4);

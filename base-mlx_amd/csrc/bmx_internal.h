@@ -52,6 +52,10 @@ struct QmvParams {
   // QMV_STORE with one segment: optional per-workgroup argmax partials of
   // the bf16 outputs, (value bits, row) at [m * qmv_blocks(...) + workgroup]
   uint2* amax;
+  // optional workspace for the K-split matrix-core GEMV (fp32 partials);
+  // without one the library's buffer of the stream is used
+  float* part;
+  size_t part_floats;
 };
 
 // Raises a kernel's dynamic-LDS limit to `bytes` (launches above 64 KB need
@@ -68,6 +72,16 @@ int allow_lds(F* kernel, size_t bytes) {
 
 // Validates shapes/alignment and launches the qmv kernel family.
 int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream);
+// Matrices (N output rows, K columns) the matrix-core GEMV takes for every
+// row count 1..8; all other shapes take the dot2 GEMV kernels.  Argmax
+// partials come from the dot2 kernels only.
+bool qmv_mfma_family(int N, int K);
+// The matrix-core GEMV; kNoFit when the shape does not fit it (a function of
+// the shape, never of the row count).
+int try_launch_qmvx(QmvParams p, QmvEpilogue epi, hipStream_t stream);
+// Partial floats the K-split matrix-core GEMV needs for M rows of x and an
+// N x K weight (0 if it never splits that shape).
+size_t qmvx_workspace_floats(int M, int N, int K);
 // Workgroups launch_qmv uses for these parameters (the count of argmax
 // partials per x row).
 int qmv_blocks(const QmvParams& p, QmvEpilogue epi);

@@ -1048,6 +1048,14 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   p.sb_vec = (p.K % 512) == 0;
   for (int i = 0; i < p.nseg; i++)
     p.sb_vec = p.sb_vec && aligned(p.seg[i].s, 16) && aligned(p.seg[i].b, 16);
+  // The large matrices take the matrix-core GEMV for every row count (a
+  // function of the shape only, like every choice below).
+  if (qmv_mfma_family(p.N, p.K)) {
+    if (p.amax)
+      return set_error(BMX_E_ARG, "qmv: no argmax partials from the matrix-core GEMV (%d x %d)", p.N, p.K);
+    const int rc = try_launch_qmvx(p, epi, stream);
+    if (rc != kNoFit) return rc;
+  }
   // Kernel choice: the persistent kernel on vocabulary-sized projections,
   // the single-phase kernel where x and s|b fit it, the phased kernel
   // otherwise.  All three compute every row with the same operations in the

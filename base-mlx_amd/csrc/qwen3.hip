@@ -148,6 +148,12 @@ int qmv(const bmx_qwen3* m, const uint16_t* x, int M, const QLin& w, uint16_t* y
   p.K = w.K;
   p.norm_w = norm;
   p.eps = m->cfg.eps;
+  // the matrix-core GEMV (large heads) writes no argmax partials: the
+  // caller then reduces the logits row itself (*amax_nblk = 0)
+  if (amax && qmv_mfma_family(w.N, w.K)) {
+    amax = nullptr;
+    if (amax_nblk) *amax_nblk = 0;
+  }
   p.amax = amax;
   if (amax) {
     const int nblk = qmv_blocks(p, QMV_STORE);
@@ -231,6 +237,8 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       p.N = H;
       p.K = qd;
       p.res = m->x;
+      p.part = m->qmm_ws;
+      p.part_floats = m->qmm_ws_floats;
       if (int rc = launch_qmv(p, QMV_RESIDUAL, st)) return rc;
     } else {
       if (int rc = launch_qmm_epi(QMM_RESIDUAL, m->att, L.p[SLOT_O].w, L.p[SLOT_O].s, L.p[SLOT_O].b, nullptr, nullptr,
@@ -260,6 +268,8 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       d.N = H;
       d.K = I;
       d.res = m->x;
+      d.part = m->qmm_ws;
+      d.part_floats = m->qmm_ws_floats;
       if (int rc = launch_qmv(d, QMV_RESIDUAL, st)) return rc;
     } else {
       if (int rc = launch_rms_norm(m->x, L.post_norm, m->h, M, H, cf.eps, st)) return rc;
@@ -297,7 +307,9 @@ int decode_step_device(bmx_qwen3* m, bmx_kv_cache* c, hipStream_t st) {
   int nblk = 0;
   if (int rc = forward_device(m, c, 1, 0, m->step_io + 1, false, m->logits1, st, m->step_io, m->amax, &nblk))
     return rc;
-  return launch_argmax_partials(m->amax, 1, nblk, reinterpret_cast<uint32_t*>(m->step_io + 2), st);
+  uint32_t* next = reinterpret_cast<uint32_t*>(m->step_io + 2);
+  if (nblk == 0) return launch_argmax(m->logits1, 1, m->cfg.vocab, next, st);
+  return launch_argmax_partials(m->amax, 1, nblk, next, st);
 }
 
 void drop_graph(bmx_qwen3* m) {
@@ -413,6 +425,9 @@ int qwen3_alloc(const bmx_qwen3_config* cfg, int max_tokens, bmx_qwen3** out) {
   for (int sl = 0; sl < NSLOT; sl++)
     m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmm_workspace_floats(max_tokens, dims[sl][0], dims[sl][1]));
   m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmm_workspace_floats(max_tokens, cfg->vocab, H));
+  // the o and down GEMVs of up to 8 tokens may split K (matrix-core GEMV)
+  m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmvx_workspace_floats(8, H, cfg->n_heads * cfg->head_dim));
+  m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmvx_workspace_floats(8, H, cfg->inter));
   if (!rc && m->qmm_ws_floats) rc = dalloc_t(m, &m->qmm_ws, m->qmm_ws_floats);
   if (!rc) rc = dalloc_t(m, &m->ids, T);
   if (!rc) rc = dalloc_t(m, &m->tok_u, T < 64 ? 64 : T);

@@ -53,9 +53,11 @@ int bmx_abi_version(void);
  * w: [N, K*bits/32] uint32; scales, biases: [N, K/group_size] bf16;
  * x, y bf16; fp32 accumulation.  bits must be 4 and group_size 64;
  * transpose = 0 (W stored [K, N]) is BMX_E_UNSUPPORTED -- every call of the
- * reference passes true.  M <= 8 runs the streaming GEMV (qmv); larger M
- * the MFMA GEMM (qmm).  x and w must be 16-byte aligned.
- * Shapes that split K over workgroups (small GEMM grids; GEMVs of 2..8 rows
+ * reference passes true.  M <= 8 runs the streaming GEMV (qmv: dot2 on
+ * the VALU, or the matrix cores when N and K are both >= 5120 -- chosen by
+ * the shape alone, so a row's result never depends on M); larger M the
+ * MFMA GEMM (qmm).  x and w must be 16-byte aligned.
+ * Shapes that split K over workgroups (small GEMM grids; matrix-core GEMVs
  * with K >= 8192) keep fp32 partials in a device buffer the library owns
  * per (device, stream), allocated or grown on first use of a larger shape
  * on that stream (which synchronizes the stream): the first call of a
