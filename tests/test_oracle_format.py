@@ -234,3 +234,36 @@ def test_gather_qmm_vs_float64(orc, M, x_bcast):
     clamp = rhs.copy()
     clamp[5] = E - 1
     np.testing.assert_array_equal(orc.gather_qmm(x, wq, s, b, hi, x_bcast), orc.gather_qmm(x, wq, s, b, clamp, x_bcast))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8192, 2560), (5, 2048, 4096), (12, 1024, 1024)])
+def test_reversed_accumulation_is_a_pure_reordering(orc, M, N, K):
+    """The reordered oracle (the summation-order floor of the end-to-end
+    bar) must change nothing but the order of fp32 additions: on sums that
+    are exact in fp32 it gives the forward bits, on random data it differs
+    from the forward order somewhere (it is on) but only by rounding, and it
+    switches off again on leaving the context.  (Enough outputs that some
+    bf16 rounding flips with the order.)"""
+    rng = np.random.default_rng(M * 7 + K)
+    # exact sums: s = 1, b = 1, x in {-1, 0, 1}
+    q = rng.integers(0, 16, (N, K))
+    wq = _pack(q)
+    one = np.full((N, K // 64), 0x3F80, np.uint16)
+    xi = orc.f32_to_bf16(rng.integers(-1, 2, (M, K)).astype(np.float32))
+    fwd = orc.qlinear(xi, wq, one, one)
+    with orc.reversed_accumulation():
+        rev = orc.qlinear(xi, wq, one, one)
+    np.testing.assert_array_equal(rev, fwd)
+    # random data: rounding-level differences only
+    wq, s, b = orc.init_qlinear(300 + M, N, K)
+    x = orc.fill_normal_bf16(400 + M, M * K).reshape(M, K)
+    fwd = orc.qlinear(x, wq, s, b)
+    with orc.reversed_accumulation():
+        rev = orc.qlinear(x, wq, s, b)
+    after = orc.qlinear(x, wq, s, b)
+    np.testing.assert_array_equal(after, fwd)
+    f, r = bf16_to_f32(fwd), bf16_to_f32(rev)
+    ref = orc.qmatmul_f64(x, wq, s, b)
+    assert np.any(f != r)
+    assert np.max(np.abs(f - r)) <= 2 * 2.0 ** -7 * np.max(np.abs(ref))
+    assert np.max(np.abs(r - ref)) / np.max(np.abs(ref)) < 1e-2

@@ -146,3 +146,34 @@ def test_argmax_first_index_on_ties(orc):
     ref = np.argmax(bf16_to_f32(x), axis=1)  # numpy: first index of the max
     np.testing.assert_array_equal(got, ref)
     assert got[1] == 100 and got[2] == 0
+
+
+def test_reversed_accumulation_sdpa_and_rms_norm(orc):
+    """Reversed key and square orders: closed forms stay exact (one visible
+    key returns v; constant rows normalise to the weight), random inputs
+    move by rounding only."""
+    rng = np.random.default_rng(5)
+    Hq, Hkv, D, L = 8, 2, 128, 300
+    q = bf16_of(rng.standard_normal((Hq, 1, D)), orc)
+    k = bf16_of(rng.standard_normal((Hkv, L, D)), orc)
+    v = bf16_of(rng.standard_normal((Hkv, L, D)), orc)
+    scale = 1.0 / np.sqrt(D)
+    with orc.reversed_accumulation():
+        one = orc.sdpa(q, k, v, 1, 0, False, scale)
+        rev = orc.sdpa(q, k, v, L, 0, False, scale)
+    np.testing.assert_array_equal(one.reshape(Hq, D), np.repeat(v[:, 0], Hq // Hkv, axis=0))
+    fwd = orc.sdpa(q, k, v, L, 0, False, scale)
+    f, r = bf16_to_f32(fwd), bf16_to_f32(rev)
+    assert np.any(f != r)
+    assert np.max(np.abs(f - r)) <= 4 * 2.0 ** -8 * np.max(np.abs(f))
+    x = bf16_of(np.array([[3.0] * 256]), orc)
+    w = bf16_of(np.linspace(0.5, 2.0, 256), orc)
+    with orc.reversed_accumulation():
+        yc = orc.rms_norm(x, w)
+    np.testing.assert_array_equal(yc, orc.rms_norm(x, w))
+    x = bf16_of(rng.standard_normal((16, 2560)) * 3, orc)
+    w = bf16_of(rng.uniform(0.5, 1.5, 2560), orc)
+    fwd = bf16_to_f32(orc.rms_norm(x, w))
+    with orc.reversed_accumulation():
+        rev = bf16_to_f32(orc.rms_norm(x, w))
+    assert np.max(np.abs(fwd - rev) / np.maximum(np.abs(fwd), 1e-3)) <= 2 * 2.0 ** -8
