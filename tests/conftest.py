@@ -8,6 +8,19 @@ for p in (os.path.join(ROOT, "base-mlx_amd"), os.path.join(ROOT, "oracle"), os.p
     if p not in sys.path:
         sys.path.insert(0, p)
 
+# tests/test_sanitizers.py runs CPU tests in child processes against the
+# AddressSanitizer / UndefinedBehaviorSanitizer builds: "lib" swaps in the
+# library's, "oracle" the oracle's (one sanitizer runtime per process).
+_SAN = os.environ.get("BMX_TEST_SANITIZED", "")
+if _SAN == "lib":
+    import bmx._lib as _bmx_lib
+
+    _bmx_lib.LIB_PATH = os.path.join(ROOT, "base-mlx_amd", "lib", "libbmx_san.so")
+elif _SAN == "oracle":
+    import oracle as _oracle
+
+    _oracle.LIB_PATH = os.path.join(ROOT, "oracle", "_build", "liboracle_san.so")
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP library)")
