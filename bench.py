@@ -21,8 +21,10 @@ host's CPU model, the threads used and a STREAM-triad bandwidth beside it.
 
 The other configurations run in the default invocation too and are reported
 under `config`: the qmm sweep (M = 5, 128, 512, 2048 over the eleven
-Qwen3-4B / 8B projection shapes) and greedy speculative decoding with a
-Qwen3-32B-shaped target and a Qwen3-0.6B-shaped draft.
+Qwen3-4B / 8B projection shapes), greedy speculative decoding with a
+Qwen3-32B-shaped target and a Qwen3-0.6B-shaped draft, and the
+Qwen3-0.6B-shaped prompt-32 / 64-token greedy run on the GPU and, beside it,
+on the host cores through the oracle.
 """
 import argparse
 import json
@@ -285,6 +287,71 @@ def speculative_bench(bmx, torch, new_tokens=512, prompt_len=2048, spec_k=5):
     return res
 
 
+def small_model_bench(bmx, torch, prompt_len=32, new_tokens=64, seed=7, cpu=True):
+    """The Qwen3-0.6B-shaped model (28 layers, hidden 1024, tied head): a
+    32-token seeded prompt, then 64 greedy decode tokens -- on the GPU
+    (prefill forward, then one graph replay per token) and, as the reference
+    runs this configuration on its CPU path, with the oracle on the host
+    cores (prefill forward, then one forward per token).  Also reports how
+    many leading greedy tokens the two agree on (random-init logits have
+    near-ties, where fp32 summation order alone can flip a token)."""
+    import numpy as np
+
+    shape = dict(bmx.QWEN3_0_6B, head_dim=128, vocab=151936)
+    prompt = np.array([int(v) for v in np.random.default_rng(seed).integers(0, 151936, prompt_len)], np.uint32)
+    m = bmx.Qwen3(bmx.qwen3_config(**shape), seed, 0.02, max_tokens=prompt_len)
+    c = m.new_cache(prompt_len + new_tokens + 8)
+    m.forward(c, prompt)  # first use: one-time setup
+    c.reset()
+    for _ in range(4):  # captures the decode graph
+        m.decode_step(c, 1)
+    c.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = m.forward(c, prompt)
+    tok = int(torch.argmax(logits.float()).item())
+    torch.cuda.synchronize()
+    gpu_prefill = time.perf_counter() - t0
+    gpu_toks = [tok]
+    t0 = time.perf_counter()
+    for _ in range(new_tokens - 1):
+        tok = m.decode_step(c, tok)
+        gpu_toks.append(tok)
+    torch.cuda.synchronize()
+    gpu_decode = time.perf_counter() - t0
+    m.close()
+    del c
+    res = {"workload": "Qwen3-0.6B-shape 4-bit, 32-token prompt, 64 greedy tokens, batch 1",
+           "gpu_prefill_ms": round(gpu_prefill * 1000, 2),
+           "gpu_decode_tok_s": round((new_tokens - 1) / gpu_decode, 1)}
+    if cpu:
+        import oracle
+
+        om = oracle.Qwen3(oracle.make_config(**shape), seed, 0.02)
+        oc = om.new_cache(prompt_len + new_tokens + 8)
+        t0 = time.perf_counter()
+        ol = om.forward(oc, prompt)
+        cpu_prefill = time.perf_counter() - t0
+        t = int(np.argmax(oracle.bf16_to_f32(ol)))
+        cpu_toks = [t]
+        t0 = time.perf_counter()
+        for _ in range(new_tokens - 1):
+            t = int(np.argmax(oracle.bf16_to_f32(om.forward(oc, np.array([t], np.uint32)))))
+            cpu_toks.append(t)
+        cpu_decode = time.perf_counter() - t0
+        om.close()
+        agree = 0
+        while agree < new_tokens and gpu_toks[agree] == cpu_toks[agree]:
+            agree += 1
+        res.update({"cpu_prefill_ms": round(cpu_prefill * 1000, 1),
+                    "cpu_decode_tok_s": round((new_tokens - 1) / cpu_decode, 2),
+                    "cpu_threads": oracle.num_threads(), "cpu_kind": "port (oracle/, OpenMP)",
+                    "greedy_tokens_agreeing": agree})
+    log(f"0.6B shape: {res}")
+    torch.cuda.empty_cache()
+    return res
+
+
 def profile_roofline(bmx, torch, launches=200):
     """Counter-collection workload: the roofline GEMV shape launched eagerly
     (rotating over >= 1 GiB of weights), then a plain 256 MiB device copy as
@@ -367,6 +434,8 @@ def main():
                     help="skip the quantized GEMM sweep at M = 5, 128, 512, 2048 (4B and 8B projection shapes)")
     ap.add_argument("--no-speculative", action="store_true",
                     help="skip 32B-target / 0.6B-draft greedy speculative decoding (M = 5 verify)")
+    ap.add_argument("--no-small", action="store_true",
+                    help="skip the Qwen3-0.6B-shape prompt-32 / 64-token decode (GPU and oracle on the host)")
     ap.add_argument("--moe", action="store_true",
                     help="also time gather_qmm on Qwen3-30B-A3B-shaped routed experts (decode, top-8 of 128)")
     ap.add_argument("--profile-roofline", action="store_true",
@@ -450,6 +519,7 @@ def main():
 
     qmm = [] if args.no_qmm_sweep else qmm_sweep(bmx, torch)
     spec = None if args.no_speculative else speculative_bench(bmx, torch)
+    small = None if args.no_small else small_model_bench(bmx, torch, cpu=not args.no_cpu)
     moe = moe_bench(bmx, torch) if args.moe else []
 
     cpu = None
@@ -478,7 +548,7 @@ def main():
         "config": {"workload": "Qwen3-4B-shape 4-bit greedy decode, batch 1, after a 4096-token prefill",
                    "prompt_tokens": args.prompt, "kv_cache": [36, 2, 8, max(cap, 4352), 128],
                    "prefill_ms": round(prefill_s * 1000, 1), "qmv_sweep": sweep, "qmm_sweep": qmm,
-                   "speculative": spec, "gather_qmm": moe},
+                   "speculative": spec, "qwen3_0_6b": small, "gather_qmm": moe},
         "roofline": roof,
         "cpu_baseline": cpu,
     }
