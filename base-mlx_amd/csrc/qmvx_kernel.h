@@ -356,13 +356,29 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
   auto step = [&](auto pf, int cts, int ckc, int nts_, int nkc_, WRegs<NP, NH>& cur, WRegs<NP, NH>& nxt) {
     XRegs nx;     // next x chunk (several chunks only)
     SbRegs nsb;  // next s|b
+    // The next step's W goes out pair by pair between this step's products
+    // (pair i after the products of pair i): a wave that issued them all
+    // first stalled ~2 us on the full memory queue before any product.
+    const uint32_t* nrow[NH];
+    int ng0 = 0, nkl = 2;
     if constexpr (decltype(pf)::value) {
       if constexpr (CHUNK) issue_x(nkc_, nx, false);
       issue_sb(nts_, nkc_, nsb);
-      __builtin_amdgcn_sched_barrier(0);
-      issue_w(nts_, nkc_, nxt);
+      const int sg = seg_of(nts_);
+      const int rows = p.seg[sg].rows;
+      ng0 = nkc_ * KC;
+      nkl = min(KC, G - ng0);
+      const int64_t rr = min((nts_ - p.seg[sg].blk0) * RW + tile * 16 + n_l, rows - 1);
+#pragma unroll
+      for (int h = 0; h < NH; h++) nrow[h] = p.seg[EPI == QMV_SWIGLU ? h : sg].w + rr * W8 + 4 * q;
       __builtin_amdgcn_sched_barrier(0);
     }
+    auto issue_next_pair = [&](int i) {
+      const int g = ng0 + 2 * min(slice * npc + i, nkl / 2 - 1);
+#pragma unroll
+      for (int h = 0; h < NH; h++)
+        nxt.w[i][h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(nrow[h] + g * 8));
+    };
     const int kl = min(KC, G - ckc * KC);
 #pragma unroll
     for (int i = 0; i < NP; i++) {
@@ -405,6 +421,7 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
           }
         }
       }
+      if constexpr (decltype(pf)::value) issue_next_pair(i);
       __builtin_amdgcn_sched_barrier(0);
     }
     const bool last_chunk = SPLIT || ckc == nkc - 1;
