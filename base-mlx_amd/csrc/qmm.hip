@@ -41,8 +41,15 @@ typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
 constexpr int QBM = 128, QBN = 128, QT = 256;  // tile rows of x, of W; threads
-constexpr int XP = 72, WP = 72;                // LDS row strides (elements)
-constexpr size_t kQmmLds = (1ull * QBM * XP + 1ull * QBN * WP) * 2;
+// LDS tiles: 64 bf16 (128 bytes, 8 chunks of 16 bytes) per row, unpadded;
+// chunk c of row r sits at chunk c ^ (r & 7).  The swizzle keeps the MFMA
+// operand reads (16 rows x one chunk per ds_read_b128) and both tile stores
+// free of bank conflicts on gfx950; the padded strides tried (144 and 160
+// bytes) left the operand reads or the W stores 4-8 cycles per instruction
+// in conflicts.
+constexpr int RS = 64;  // LDS row stride (elements)
+constexpr size_t kQmmLds = (1ull * QBM * RS + 1ull * QBN * RS) * 2;
+__device__ __forceinline__ int swz(int row, int chunk) { return row * RS + ((chunk ^ (row & 7)) << 3); }
 
 struct QmmParams {
   const uint16_t* x;   // [M, K]
@@ -67,8 +74,8 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 template <int EPI>
 __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [QBM][XP]
-  uint16_t* ws = xs + QBM * XP;                      // [QBN][WP]
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [QBM][RS], swizzled
+  uint16_t* ws = xs + QBM * RS;                      // [QBN][RS], swizzled
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;  // wave sub-tile: x rows 64 wm, W rows 64 wn
   const int li = lane & 15, q = lane >> 4;
@@ -104,14 +111,13 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   };
   // ---- registers -> LDS: x as is, W dequantized to bf16 ----
   auto store = [&]() {
-    auto put_x = [&](int e, const uint4& v) { *reinterpret_cast<uint4*>(xs + (e >> 3) * XP + (e & 7) * 8) = v; };
+    auto put_x = [&](int e, const uint4& v) { *reinterpret_cast<uint4*>(xs + swz(e >> 3, e & 7)) = v; };
     put_x(tid, xr0);
     put_x(tid + QT, xr1);
     put_x(tid + 2 * QT, xr2);
     put_x(tid + 3 * QT, xr3);
     const float sv = bf2f(sr), bv = bf2f(br);
-    uint16_t* dst = ws + wr * WP + wh * 32;
-    auto put_word = [&](uint16_t* d, uint32_t word) {
+    auto put_word = [&](int chunk, uint32_t word) {
       // nibble k of the word is value k: even k in the low nibble of byte
       // k/2, odd k in the high nibble
       uint32_t lo = word & 0x0f0f0f0fu, hi = (word >> 4) & 0x0f0f0f0fu;
@@ -125,12 +131,12 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
       o.z = pk_bf16(fmaf(sv, static_cast<float>((lo >> 16) & 0xffu), bv),
                     fmaf(sv, static_cast<float>((hi >> 16) & 0xffu), bv));
       o.w = pk_bf16(fmaf(sv, static_cast<float>(lo >> 24), bv), fmaf(sv, static_cast<float>(hi >> 24), bv));
-      *reinterpret_cast<uint4*>(d) = o;
+      *reinterpret_cast<uint4*>(ws + swz(wr, chunk)) = o;
     };
-    put_word(dst, wq.x);
-    put_word(dst + 8, wq.y);
-    put_word(dst + 16, wq.z);
-    put_word(dst + 24, wq.w);
+    put_word(wh * 4, wq.x);
+    put_word(wh * 4 + 1, wq.y);
+    put_word(wh * 4 + 2, wq.z);
+    put_word(wh * 4 + 3, wq.w);
   };
 
   f32x4_t acc[4][4];
@@ -150,12 +156,12 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int t = 0; t < 2; t++)
-        af[i][t] = *reinterpret_cast<const bf16x8_t*>(xs + (wm * 64 + i * 16 + li) * XP + t * 32 + q * 8);
+        af[i][t] = *reinterpret_cast<const bf16x8_t*>(xs + swz(wm * 64 + i * 16 + li, t * 4 + q));
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int c = wn * 64 + j * 16 + li;
-      const bf16x8_t b0 = *reinterpret_cast<const bf16x8_t*>(ws + c * WP + q * 8);
-      const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(ws + c * WP + 32 + q * 8);
+      const bf16x8_t b0 = *reinterpret_cast<const bf16x8_t*>(ws + swz(c, q));
+      const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(ws + swz(c, 4 + q));
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i][0], b0, acc[i][j], 0, 0, 0);
