@@ -92,6 +92,13 @@ int qmv_blocks(const QmvParams& p, QmvEpilogue epi);
 // stream) pair that the library keeps.
 int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M,
                int N, int K, float* ws, size_t ws_floats, hipStream_t stream);
+// The same x times up to 3 weights (q, k, v of a layer) with separate
+// outputs y[i] of n[i] columns: one launch when every n[i] is a multiple of
+// 128 and K does not split, else one launch_qmm per weight.  Each output is
+// bit-identical to its own launch_qmm without a K split.
+int launch_qmm_segments(const uint16_t* x, int nseg, const uint32_t* const* w, const uint16_t* const* s,
+                        const uint16_t* const* b, uint16_t* const* y, const int* n, int M, int K, float* ws,
+                        size_t ws_floats, hipStream_t stream);
 // The GEMM with a fused epilogue: store; residual, y = res + bf16(x W^T)
 // (res may alias y); SwiGLU of the gate W and up W2 weights,
 // y = bf16(silu(bf16(x W^T)) * bf16(x W2^T)) with MLX's roundings.  SwiGLU

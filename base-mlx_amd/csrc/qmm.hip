@@ -66,6 +66,16 @@ struct QmmParams {
   int gps;     // groups per split
   int mtiles;  // row tiles of x (the grid's x dimension enumerates mtiles x column tiles)
   int xcd;     // XCD-grouped tile order (vocabulary-sized N), else row-major
+  // Store epilogue over up to 3 column segments (q | k | v of one layer in
+  // one launch): segment i covers output columns [seg_n0[i], seg_n0[i+1])
+  // of the launch (multiples of the tile width) with its own W, s, b and y
+  // (y row stride = the segment's width).  nseg = 0: the plain product.
+  int nseg;
+  int seg_n0[4];
+  const uint32_t* seg_w[3];
+  const uint16_t* seg_s[3];
+  const uint16_t* seg_b[3];
+  uint16_t* seg_y[3];
 };
 
 // two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
@@ -81,7 +91,8 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;  // wave sub-tile: x rows 64 wm, W rows 64 wn
   const int li = lane & 15, q = lane >> 4;
-  const int M = p.M, N = p.N, K = p.K, G = K / 64;
+  const int M = p.M, K = p.K, G = K / 64;
+  int N = p.N;
   // output columns per workgroup: 128, or 64 gate / up pairs for SwiGLU
   constexpr int CN = EPI == QMM_SWIGLU ? QBN / 2 : QBN;
   // Tile of this workgroup.  Row-major (column tiles fastest): the ~768
@@ -108,8 +119,24 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
       nt = blockIdx.x % ntiles;
     }
   }
-  const int m0 = mt * QBM, n0 = nt * CN;
+  const int m0 = mt * QBM;
+  int n0 = nt * CN;
   const int gb = blockIdx.z * p.gps, ge = min(G, gb + p.gps);
+  // the segment holding this workgroup's columns (uniform)
+  const uint32_t* pw = p.w;
+  const uint16_t *ps = p.s, *pb = p.b;
+  uint16_t* py = p.y;
+  if constexpr (EPI == QMM_STORE) {
+    if (p.nseg > 1) {
+      const int si = (n0 >= p.seg_n0[1]) + (p.nseg > 2 && n0 >= p.seg_n0[2]);
+      pw = p.seg_w[si];
+      ps = p.seg_s[si];
+      pb = p.seg_b[si];
+      py = p.seg_y[si];
+      n0 -= p.seg_n0[si];
+      N = p.seg_n0[si + 1] - p.seg_n0[si];
+    }
+  }
 
   // ---- global -> registers for one group (rows clamped: their results are
   // never stored) ----
@@ -121,9 +148,9 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   const int wr = tid >> 1, wh = tid & 1;  // W row of the tile, half of the group
   const bool up_row = EPI == QMM_SWIGLU && wr >= CN;
   const int64_t wrow = min(n0 + (EPI == QMM_SWIGLU ? wr % CN : wr), N - 1);
-  const uint32_t* wp = (up_row ? p.w2 : p.w) + wrow * (K / 8) + wh * 4;
-  const uint16_t* sp = (up_row ? p.s2 : p.s) + wrow * G;
-  const uint16_t* bp = (up_row ? p.b2 : p.b) + wrow * G;
+  const uint32_t* wp = (up_row ? p.w2 : pw) + wrow * (K / 8) + wh * 4;
+  const uint16_t* sp = (up_row ? p.s2 : ps) + wrow * G;
+  const uint16_t* bp = (up_row ? p.b2 : pb) + wrow * G;
   uint4 xr0, xr1, xr2, xr3, wq;
   uint16_t sr, br;
   auto load = [&](int g) {
@@ -232,13 +259,13 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
           const float g = round_bf(acc[i][j][r]);
           const float u = round_bf(reinterpret_cast<const float*>(smem)[(((wm * 4 + i) * 4 + j) * 4 + r) * 64 + lane]);
           const float sg = round_bf(1.0f / (1.0f + expf(-g)));
-          p.y[o] = f2bf(round_bf(g * sg) * u);
+          py[o] = f2bf(round_bf(g * sg) * u);
         } else if (p.part) {
           p.part[static_cast<int64_t>(blockIdx.z) * M * N + o] = acc[i][j][r];
         } else if constexpr (EPI == QMM_RESIDUAL) {
-          p.y[o] = f2bf(bf2f(p.res[o]) + round_bf(acc[i][j][r]));
+          py[o] = f2bf(bf2f(p.res[o]) + round_bf(acc[i][j][r]));
         } else {
-          p.y[o] = f2bf(acc[i][j][r]);
+          py[o] = f2bf(acc[i][j][r]);
         }
       }
     }
@@ -388,6 +415,45 @@ int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const 
     return check_launch("qmm_reduce");
   }
   return BMX_OK;
+}
+
+int launch_qmm_segments(const uint16_t* x, int nseg, const uint32_t* const* w, const uint16_t* const* s,
+                        const uint16_t* const* b, uint16_t* const* y, const int* n, int M, int K, float* ws,
+                        size_t ws_floats, hipStream_t stream) {
+  if (M <= 0) return BMX_OK;
+  if (nseg < 1 || nseg > 3) return set_error(BMX_E_ARG, "qmm: %d segments", nseg);
+  int ntot = 0;
+  bool one = K % 64 == 0 && aligned(x, 16);
+  for (int i = 0; i < nseg; i++) {
+    one = one && n[i] > 0 && n[i] % QBN == 0 && aligned(w[i], 16);
+    ntot += n[i];
+  }
+  int splits = 2, gps = 0;
+  if (one) qmm_split(M, ntot, K, &splits, &gps, QBN);
+  // one launch when every segment is whole tiles and K is not split (the
+  // reduction writes one y); else a launch per segment
+  if (!one || splits > 1 || (M + QBM - 1) / QBM > 65535) {
+    for (int i = 0; i < nseg; i++)
+      if (int rc = launch_qmm(x, w[i], s[i], b[i], y[i], M, n[i], K, ws, ws_floats, stream)) return rc;
+    return BMX_OK;
+  }
+  const int mtiles = (M + QBM - 1) / QBM, ntiles = ntot / QBN;
+  QmmParams p{x, w[0], s[0], b[0], nullptr, nullptr, nullptr, nullptr, y[0], nullptr, M, ntot, K, gps, mtiles, 0};
+  p.nseg = nseg;
+  int c = 0;
+  for (int i = 0; i < nseg; i++) {
+    p.seg_n0[i] = c;
+    p.seg_w[i] = w[i];
+    p.seg_s[i] = s[i];
+    p.seg_b[i] = b[i];
+    p.seg_y[i] = y[i];
+    c += n[i];
+  }
+  for (int i = nseg; i < 4; i++) p.seg_n0[i] = c;
+  if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(qmm_kernel<QMM_STORE>), kQmmLds)) return rc;
+  hipLaunchKernelGGL(qmm_kernel<QMM_STORE>, dim3(static_cast<unsigned>(mtiles) * ntiles, 1, 1), dim3(QT), kQmmLds,
+                     stream, p);
+  return check_launch("qmm");
 }
 
 int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M, int N,

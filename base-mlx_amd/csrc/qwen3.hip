@@ -200,14 +200,13 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       if (int rc = launch_qmv(p, QMV_STORE, st)) return rc;
     } else {
       if (int rc = launch_rms_norm(m->x, L.in_norm, m->h, M, H, cf.eps, st)) return rc;
-      if (int rc = launch_qmm(m->h, L.p[SLOT_Q].w, L.p[SLOT_Q].s, L.p[SLOT_Q].b, m->q, M, qd, H,
-                              m->qmm_ws, m->qmm_ws_floats, st))
-        return rc;
-      if (int rc = launch_qmm(m->h, L.p[SLOT_K].w, L.p[SLOT_K].s, L.p[SLOT_K].b, m->k, M, kvd, H,
-                              m->qmm_ws, m->qmm_ws_floats, st))
-        return rc;
-      if (int rc = launch_qmm(m->h, L.p[SLOT_V].w, L.p[SLOT_V].s, L.p[SLOT_V].b, m->v, M, kvd, H,
-                              m->qmm_ws, m->qmm_ws_floats, st))
+      // q, k and v in one GEMM launch where the shape allows (qwen3.rs:370-390)
+      const uint32_t* w3[3] = {L.p[SLOT_Q].w, L.p[SLOT_K].w, L.p[SLOT_V].w};
+      const uint16_t* s3[3] = {L.p[SLOT_Q].s, L.p[SLOT_K].s, L.p[SLOT_V].s};
+      const uint16_t* b3[3] = {L.p[SLOT_Q].b, L.p[SLOT_K].b, L.p[SLOT_V].b};
+      uint16_t* y3[3] = {m->q, m->k, m->v};
+      const int n3[3] = {qd, kvd, kvd};
+      if (int rc = launch_qmm_segments(m->h, 3, w3, s3, b3, y3, n3, M, H, m->qmm_ws, m->qmm_ws_floats, st))
         return rc;
     }
     // ---- QK-norm, RoPE at the cache offset, KV write (qwen3.rs:392-489) and
