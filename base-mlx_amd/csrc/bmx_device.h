@@ -141,16 +141,29 @@ __device__ __forceinline__ float gemv_chunk(uint4 w, uint4 x0, uint4 x1, uint4 x
 // Qwen3::forward_internal (crates/base-mlx-core/src/model/qwen3.rs:392-413).
 // Every kernel that norms and rotates q or k calls this, so they agree bit
 // for bit.
-__device__ __forceinline__ void qk_norm_rope_lane(float a, float b, float wa, float wb, float freq, float pos,
-                                                  float eps, uint16_t& o1, uint16_t& o2) {
-  const float ss = wave_sum_xor(a * a + b * b, 64);
+// the same with the rotation's cos / sin given (they depend on the position
+// and lane only, so a wave over several heads of one token computes them once)
+__device__ __forceinline__ void qk_norm_rope_lane_cs(float a, float b, float wa, float wb, float c, float s,
+                                                     float eps, uint16_t& o1, uint16_t& o2) {
+  // the fused multiply-adds are written out, so every place this function
+  // is inlined rounds the same way
+  const float ss = wave_sum_xor(__builtin_fmaf(a, a, __fmul_rn(b, b)), 64);
   const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
   const float na = bf2f(f2bf(wa * round_bf(a * inv)));
   const float nb = bf2f(f2bf(wb * round_bf(b * inv)));
+  o1 = f2bf(__builtin_fmaf(na, c, -__fmul_rn(nb, s)));
+  o2 = f2bf(__builtin_fmaf(nb, c, __fmul_rn(na, s)));
+}
+__device__ __forceinline__ void rope_cs(float freq, float pos, float& c, float& s) {
   const float ang = pos * freq;
-  const float c = cosf(ang), s = sinf(ang);
-  o1 = f2bf(na * c - nb * s);
-  o2 = f2bf(na * s + nb * c);
+  c = cosf(ang);
+  s = sinf(ang);
+}
+__device__ __forceinline__ void qk_norm_rope_lane(float a, float b, float wa, float wb, float freq, float pos,
+                                                  float eps, uint16_t& o1, uint16_t& o2) {
+  float c, s;
+  rope_cs(freq, pos, c, s);
+  qk_norm_rope_lane_cs(a, b, wa, wb, c, s, eps, o1, o2);
 }
 
 // DPP lane moves within 16-lane rows (gfx9 dpp_ctrl encodings):

@@ -93,8 +93,13 @@ __global__ void __launch_bounds__(256)
 
 // Fused per-head RMSNorm (QK-norm, qwen3.rs:392-399), RoPE at positions
 // offset + t (qwen3.rs:407-413), KV write at [offset, offset + M)
-// (qwen3.rs:431-489).  One wave per (token, head) with head_dim 128: lane i
-// holds the rotate-half pair (i, i + 64).
+// (qwen3.rs:431-489), head_dim 128.  One wave per (token, group of up to
+// kQkHeads q heads or kv heads): the rotation's cos / sin depend on the
+// token and the lane only and are computed once per wave; every head's rows
+// are loaded before any arithmetic.  Lane i holds the rotate-half pair
+// (i, i + 64) of each head (the lane function the decode attention's
+// prologue uses too, so both write the same bits).
+constexpr int kQkHeads = 8;
 struct QkvRopeParams {
   const uint16_t* q;  // [M, Hq*128] (qkv projection output rows)
   const uint16_t* k;  // [M, Hkv*128]
@@ -114,31 +119,57 @@ struct QkvRopeParams {
 __global__ void __launch_bounds__(256) qk_norm_rope_kv_kernel(const QkvRopeParams p) {
   const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int heads = p.Hq + p.Hkv;
-  if (wid >= p.M * heads) return;
-  const int t = wid / heads;
-  const int h = wid - t * heads;
+  const int qg = (p.Hq + kQkHeads - 1) / kQkHeads, kg = (p.Hkv + kQkHeads - 1) / kQkHeads;
+  if (wid >= p.M * (qg + kg)) return;
+  const int t = wid / (qg + kg);
+  const int g = wid - t * (qg + kg);
+  const bool is_q = g < qg;
+  const int h0 = (is_q ? g : g - qg) * kQkHeads;
+  const int nh = min(kQkHeads, (is_q ? p.Hq : p.Hkv) - h0);
   const int offset = p.offset_dev ? *p.offset_dev : p.offset;
-  const float pos = static_cast<float>(offset + t);
-  const bool is_q = h < p.Hq;
-  const int hk = h - p.Hq;
-  const uint16_t* src = is_q ? p.q + (static_cast<int64_t>(t) * p.Hq + h) * 128
-                             : p.k + (static_cast<int64_t>(t) * p.Hkv + hk) * 128;
+  const uint16_t* src = is_q ? p.q + (static_cast<int64_t>(t) * p.Hq + h0) * 128
+                             : p.k + (static_cast<int64_t>(t) * p.Hkv + h0) * 128;
   const uint16_t* nw = is_q ? p.q_norm : p.k_norm;
-  uint16_t o1, o2;
-  qk_norm_rope_lane(bf2f(src[lane]), bf2f(src[lane + 64]), bf2f(nw[lane]), bf2f(nw[lane + 64]), p.tab.inv_freq[lane],
-                    pos, p.eps, o1, o2);
+  uint16_t a[kQkHeads], b[kQkHeads];
+#pragma unroll
+  for (int i = 0; i < kQkHeads; i++) {
+    const int hi = min(i, nh - 1);
+    a[i] = src[hi * 128 + lane];
+    b[i] = src[hi * 128 + lane + 64];
+  }
+  const float wa = bf2f(nw[lane]), wb = bf2f(nw[lane + 64]);
+  float c, s;
+  rope_cs(p.tab.inv_freq[lane], static_cast<float>(offset + t), c, s);
   if (is_q) {
-    uint16_t* dst = p.q_out + (static_cast<int64_t>(h) * p.M + t) * 128;
-    dst[lane] = o1;
-    dst[lane + 64] = o2;
+#pragma unroll
+    for (int i = 0; i < kQkHeads; i++) {
+      if (i >= nh) break;
+      uint16_t o1, o2;
+      qk_norm_rope_lane_cs(bf2f(a[i]), bf2f(b[i]), wa, wb, c, s, p.eps, o1, o2);
+      uint16_t* dst = p.q_out + (static_cast<int64_t>(h0 + i) * p.M + t) * 128;
+      dst[lane] = o1;
+      dst[lane + 64] = o2;
+    }
   } else {
-    const int64_t slot = (static_cast<int64_t>(hk) * p.cap + offset + t) * 128;
-    p.k_cache[slot + lane] = o1;
-    p.k_cache[slot + lane + 64] = o2;
-    const uint16_t* vs = p.v + (static_cast<int64_t>(t) * p.Hkv + hk) * 128;
-    p.v_cache[slot + lane] = vs[lane];
-    p.v_cache[slot + lane + 64] = vs[lane + 64];
+    const uint16_t* vs = p.v + (static_cast<int64_t>(t) * p.Hkv + h0) * 128;
+    uint16_t va[kQkHeads], vb[kQkHeads];
+#pragma unroll
+    for (int i = 0; i < kQkHeads; i++) {
+      const int hi = min(i, nh - 1);
+      va[i] = vs[hi * 128 + lane];
+      vb[i] = vs[hi * 128 + lane + 64];
+    }
+#pragma unroll
+    for (int i = 0; i < kQkHeads; i++) {
+      if (i >= nh) break;
+      uint16_t o1, o2;
+      qk_norm_rope_lane_cs(bf2f(a[i]), bf2f(b[i]), wa, wb, c, s, p.eps, o1, o2);
+      const int64_t slot = (static_cast<int64_t>(h0 + i) * p.cap + offset + t) * 128;
+      p.k_cache[slot + lane] = o1;
+      p.k_cache[slot + lane + 64] = o2;
+      p.v_cache[slot + lane] = va[i];
+      p.v_cache[slot + lane + 64] = vb[i];
+    }
   }
 }
 
@@ -175,7 +206,7 @@ int launch_qk_norm_rope_kv(const uint16_t* q, const uint16_t* k, const uint16_t*
   if (!offset_dev && (offset < 0 || offset + M > cap))
     return set_error(BMX_E_KV_CAPACITY, "KV cache exhausted: requested %d positions, max %d", offset + M, cap);
   QkvRopeParams p{q, k, v, q_norm, k_norm, q_out, k_cache, v_cache, offset_dev, offset, M, Hq, Hkv, cap, eps, tab};
-  const int waves = M * (Hq + Hkv);
+  const int waves = M * ((Hq + kQkHeads - 1) / kQkHeads + (Hkv + kQkHeads - 1) / kQkHeads);
   hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
   return check_launch("qk_norm_rope_kv");
 }

@@ -45,11 +45,13 @@ def test_slice_update(gpu, orc):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("M,offset", [(1, 0), (1, 100), (5, 60), (20, 0), (20, 13)])
-def test_qk_norm_rope_kv(gpu, orc, M, offset):
+# (the kernel takes heads in groups of 8: 12 / 4 and 20 / 10 leave partial groups)
+@pytest.mark.parametrize("M,offset,Hq,Hkv", [(1, 0, 32, 8), (1, 100, 32, 8), (5, 60, 32, 8), (20, 0, 32, 8),
+                                             (20, 13, 32, 8), (20, 13, 12, 4), (3, 5, 20, 10)])
+def test_qk_norm_rope_kv(gpu, orc, M, offset, Hq, Hkv):
     import torch
 
-    Hq, Hkv, cap = 32, 8, 128
+    cap = 128
     q = gpu.fill_normal_bf16(6, (M, Hq * 128), sigma=3.0)
     k = gpu.fill_normal_bf16(7, (M, Hkv * 128), sigma=3.0)
     v = gpu.fill_normal_bf16(8, (M, Hkv * 128))

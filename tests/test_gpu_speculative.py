@@ -119,19 +119,28 @@ def test_speculative_continues_a_filled_cache(gpu, orc):
 
 
 def _agree_with_oracle_greedy(orc, om, tokens, prompt, cap):
-    """The oracle replays `tokens` (teacher forcing): each must be its
-    argmax, except where its top-2 logits are within 2 bf16 ulps (a tie that
-    rounding decides); returns the count of such ties taken differently."""
-    oc = om.new_cache(cap)
+    """The oracle replays `tokens` (teacher forcing), and beside it the oracle
+    with every fp32 reduction in reverse order.  Each token must be the
+    oracle's argmax, except at a rounding tie: the oracle's top-2 logits
+    within 2 bf16 ulps, or within twice what summation order alone moves a
+    logit at that position (the largest |oracle - reversed oracle| over the
+    vocabulary).  Returns the count of ties taken the other way."""
+    oc, rc = om.new_cache(cap), om.new_cache(cap)
     logits = om.forward(oc, prompt)
+    with orc.reversed_accumulation():
+        rlogits = om.forward(rc, prompt)
     ties = 0
     for i, t in enumerate(tokens):
         o = bf16_to_f32(logits).astype(np.float64)
         if int(np.argmax(o)) != int(t):
             top = np.sort(o)[-2:]
-            assert top[1] - top[0] <= 2 * abs(top[1]) * 2.0 ** -7, (i, int(t), int(np.argmax(o)))
+            floor = float(np.max(np.abs(o - bf16_to_f32(rlogits).astype(np.float64))))
+            bar = max(2 * abs(top[1]) * 2.0 ** -7, 2 * floor)
+            assert top[1] - top[0] <= bar, (i, int(t), int(np.argmax(o)), top[1] - top[0], floor)
             ties += 1
         logits = om.forward(oc, [int(t)])
+        with orc.reversed_accumulation():
+            rlogits = om.forward(rc, [int(t)])
     return ties
 
 
