@@ -157,6 +157,8 @@ __device__ __forceinline__ void store_pair(const AttnParams& p, int wid, int lan
 // 0 only) into the caches.  K / V rows of new keys come from LDS instead of
 // the (possibly not yet written) cache rows.
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 constexpr int kDecWaves = 8, kDecWaveKeys = 32, kDecKeys = kDecWaveKeys * kDecWaves;
@@ -466,9 +468,10 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
 //     as its 8-wide k slice in that order;
 //   O += P V with B = V^T from LDS, staged transposed (4 keys x 8 dims per
 //     thread, transposed in registers) so that the same 8 keys are two
-//     8-byte reads.  p stays fp32: it enters the product as three bf16
-//     terms (three MFMAs), and the row sums add it unrounded; O and the
-//     softmax statistics are fp32.  The
+//     8-byte reads.  p enters the product as bf16(p) against V in bf16
+//     plus its residual in fp16 against a fp16 copy of V^T (two MFMAs, p
+//     to ~2^-20), and the row sums add it unrounded; O and the softmax
+//     statistics are fp32.  The
 //     softmax runs in base 2 (v_exp_f32 on scores pre-multiplied by log2 e),
 //     and O is rescaled only in blocks where some row's running max moved.
 // The K and V^T tiles are double-buffered: the loads of key block j+1 are
@@ -485,7 +488,8 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
 constexpr int kFaQ = 64, kFaK = 64;  // queries per 4-wave workgroup, keys per block
 constexpr int kFaKS = kD + 8;        // K tile row stride (elements)
 constexpr int kFaVS = kFaK + 8;      // V^T tile row stride (elements)
-constexpr size_t kFaLds = 2ull * (kFaK * kFaKS + kD * kFaVS) * sizeof(uint16_t);
+// K, V^T (bf16) and V^T (fp16, for the residual term of p), double-buffered
+constexpr size_t kFaLds = 2ull * (kFaK * kFaKS + 2 * kD * kFaVS) * sizeof(uint16_t);
 
 template <int NW, int HG>
 __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams p) {
@@ -494,6 +498,7 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* kt_s = reinterpret_cast<uint16_t*>(smem);  // [2][kFaK][kFaKS]
   uint16_t* vt_s = kt_s + 2 * kFaK * kFaKS;             // [2][kD][kFaVS]
+  uint16_t* vh_s = vt_s + 2 * kD * kFaVS;               // [2][kD][kFaVS] fp16
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // staging thread index: all 256 threads of a 4-wave workgroup stage K and
   // V; with 8 waves, threads 0..255 stage V and 256..511 stage K
@@ -536,15 +541,27 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     return reinterpret_cast<const uint4*>(p.v + hbase + static_cast<int64_t>(min(k0 + 4 * vkq + j, L - 1)) * kD +
                                           vdc * 8);
   };
+  // (with 8 waves a thread stages K or V, never both: its four loads go to
+  // kr0..kr3 either way, so a register set is 16 VGPRs, not 32)
   auto load_block = [&](int k0) {
     Stage r;
-    if (stage_k) {
+    if constexpr (NW == 8) {
+      if (stage_k) {
+        r.kr0 = *kaddr(k0, 0);
+        r.kr1 = *kaddr(k0, 1);
+        r.kr2 = *kaddr(k0, 2);
+        r.kr3 = *kaddr(k0, 3);
+      } else {
+        r.kr0 = *vaddr(k0, 0);
+        r.kr1 = *vaddr(k0, 1);
+        r.kr2 = *vaddr(k0, 2);
+        r.kr3 = *vaddr(k0, 3);
+      }
+    } else {
       r.kr0 = *kaddr(k0, 0);
       r.kr1 = *kaddr(k0, 1);
       r.kr2 = *kaddr(k0, 2);
       r.kr3 = *kaddr(k0, 3);
-    }
-    if (stage_v) {
       r.vr0 = *vaddr(k0, 0);
       r.vr1 = *vaddr(k0, 1);
       r.vr2 = *vaddr(k0, 2);
@@ -565,21 +582,34 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
       kput(3, r.kr3);
     }
     if (!stage_v) return;
+    const uint4 va0 = NW == 8 ? r.kr0 : r.vr0, va1 = NW == 8 ? r.kr1 : r.vr1;
+    const uint4 va2 = NW == 8 ? r.kr2 : r.vr2, va3 = NW == 8 ? r.kr3 : r.vr3;
     // V^T: dim 8 vdc + d gets keys 4 vkq .. + 3 (8 bytes)
     // 4-key chunk vkq of dim row r sits at chunk vkq ^ ((r >> 3) & 7): the
     // 8 rows of one thread share r >> 3 = vdc, so the 16 vdc lanes of a
     // store spread over 8 chunk columns instead of one bank pair
     uint16_t* vb = vt_s + buf * kD * kFaVS + 4 * (vkq ^ (vdc & 7));
+    uint16_t* vh = vh_s + buf * kD * kFaVS + 4 * (vkq ^ (vdc & 7));
+    // fp16 copy: v_cvt_pkrtz is exact for every bf16 value in fp16's normal
+    // range and saturates beyond it (the copy only carries p's residual)
+    auto h2 = [](uint32_t lo16, uint32_t hi16) {
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(lo16 << 16),
+                                                                     __uint_as_float(hi16 << 16)));
+    };
     auto vput = [&](int c, uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
       const uint2 lo = make_uint2((a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16));
       const uint2 hi = make_uint2((a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u));
       *reinterpret_cast<uint2*>(vb + (vdc * 8 + 2 * c) * kFaVS) = lo;
       *reinterpret_cast<uint2*>(vb + (vdc * 8 + 2 * c + 1) * kFaVS) = hi;
+      *reinterpret_cast<uint2*>(vh + (vdc * 8 + 2 * c) * kFaVS) =
+          make_uint2(h2(a0 & 0xffffu, a1 & 0xffffu), h2(a2 & 0xffffu, a3 & 0xffffu));
+      *reinterpret_cast<uint2*>(vh + (vdc * 8 + 2 * c + 1) * kFaVS) =
+          make_uint2(h2(a0 >> 16, a1 >> 16), h2(a2 >> 16, a3 >> 16));
     };
-    vput(0, r.vr0.x, r.vr1.x, r.vr2.x, r.vr3.x);
-    vput(1, r.vr0.y, r.vr1.y, r.vr2.y, r.vr3.y);
-    vput(2, r.vr0.z, r.vr1.z, r.vr2.z, r.vr3.z);
-    vput(3, r.vr0.w, r.vr1.w, r.vr2.w, r.vr3.w);
+    vput(0, va0.x, va1.x, va2.x, va3.x);
+    vput(1, va0.y, va1.y, va2.y, va3.y);
+    vput(2, va0.z, va1.z, va2.z, va3.z);
+    vput(3, va0.w, va1.w, va2.w, va3.w);
   };
 
   f32x4_t o[8];
@@ -604,6 +634,7 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     else sg1 = load_block(min(jb + 2, nkb - 1) * kFaK);
     const uint16_t* kb = kt_s + buf * kFaK * kFaKS;
     const uint16_t* vb = vt_s + buf * kD * kFaVS;
+    const uint16_t* vhb = vh_s + buf * kD * kFaVS;
     // ---- S^T = K Q^T: 4 key tiles of 16 ----
     f32x4_t sc[4];
 #pragma unroll
@@ -634,34 +665,31 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     // row with nothing visible yet keeps m = -inf and is skipped
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    // p in fp32, carried to the matrix cores as three bf16 terms p = hi + mid
-    // + lo (each the bf16 rounding of what the terms before it leave; every
-    // difference is exact in fp32), so P V sees p to ~2^-27 of itself -- as
-    // if p stayed fp32 -- and the row sum adds the unrounded p.  (Two terms
-    // leave ~2^-18 of p, which through softmax cancellation flips ~0.2% of
+    // p in fp32, carried to the matrix cores as two terms: hi = bf16(p)
+    // against V in bf16, and the residual p - hi (exact in fp32, at most
+    // 2^-9 p) rounded to fp16 against V in fp16, so P V sees p to ~2^-20 of
+    // itself; the row sum adds the unrounded p.  (Three bf16 terms reach
+    // 2^-24 for a third more products; two bf16 terms, 2^-16, flip ~0.2% of
     // the bf16 outputs against an fp32 reference.)
     float sum = 0.0f;
-    bf16x8_t pa[3][2];
+    bf16x8_t pa[2];
+    f16x8_t pr[2];
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-      uint32_t pw[3][4];
+      uint32_t ph[4], pl[4];
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int kt = 2 * c + (u >> 1), i0 = 2 * (u & 1);
-        float r0 = __builtin_amdgcn_exp2f(sc[kt][i0] - m_use);
-        float r1 = __builtin_amdgcn_exp2f(sc[kt][i0 + 1] - m_use);
+        const float r0 = __builtin_amdgcn_exp2f(sc[kt][i0] - m_use);
+        const float r1 = __builtin_amdgcn_exp2f(sc[kt][i0 + 1] - m_use);
         sum += r0 + r1;
-#pragma unroll
-        for (int t = 0; t < 3; t++) {
-          const uint16_t b0 = f2bf(r0), b1 = f2bf(r1);
-          pw[t][u] = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
-          r0 -= bf2f(b0);
-          r1 -= bf2f(b1);
-        }
+        const uint16_t b0 = f2bf(r0), b1 = f2bf(r1);
+        ph[u] = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
+        const f16x2_t rr = f16x2_t{static_cast<_Float16>(r0 - bf2f(b0)), static_cast<_Float16>(r1 - bf2f(b1))};
+        pl[u] = __builtin_bit_cast(uint32_t, rr);
       }
-#pragma unroll
-      for (int t = 0; t < 3; t++)
-        pa[t][c] = __builtin_bit_cast(bf16x8_t, make_uint4(pw[t][0], pw[t][1], pw[t][2], pw[t][3]));
+      pa[c] = __builtin_bit_cast(bf16x8_t, make_uint4(ph[0], ph[1], ph[2], ph[3]));
+      pr[c] = __builtin_bit_cast(f16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
     }
     sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
@@ -682,6 +710,9 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     for (int c = 0; c < 2; c++)
 #pragma unroll
       for (int j = 0; j < 8; j++) {
+        // (the scheduler may hoist the V reads of 4 dim rows at most: all
+        // 16 rows' reads up front spilled registers)
+        if (j % 4 == 0) __builtin_amdgcn_sched_barrier(0);
         // dim row j 16 + n, keys 32 c + 4 g.. and 32 c + 16 + 4 g.. (4-key
         // chunks 8 c + g and 8 c + 4 + g, swizzled as stored)
         const int sw = (2 * j + (n >> 3)) & 7;
@@ -689,8 +720,12 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
         const uint2 v0 = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * c + g) ^ sw));
         const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * c + 4 + g) ^ sw));
         const bf16x8_t bv = __builtin_bit_cast(bf16x8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
-#pragma unroll
-        for (int t = 0; t < 3; t++) o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[t][c], bv, o[j], 0, 0, 0);
+        const uint16_t* hrow = vhb + (j * 16 + n) * kFaVS;
+        const uint2 h0 = *reinterpret_cast<const uint2*>(hrow + 4 * ((8 * c + g) ^ sw));
+        const uint2 h1 = *reinterpret_cast<const uint2*>(hrow + 4 * ((8 * c + 4 + g) ^ sw));
+        const f16x8_t bh = __builtin_bit_cast(f16x8_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[c], bv, o[j], 0, 0, 0);
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pr[c], bh, o[j], 0, 0, 0);
       }
     if (more) store_block(P == 0 ? sg1 : sg0, buf ^ 1);
     __syncthreads();
