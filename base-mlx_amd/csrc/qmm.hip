@@ -10,9 +10,10 @@
 // keeps the group decomposition s * sum q x + b * sum x instead.)
 //
 // Workgroup tile: 128 rows of x by 128 rows of W, 4 waves (2 x 2), each
-// 64 x 64 = 4 x 4 tiles of v_mfma_f32_16x16x32_bf16; several workgroups
-// share a CU.  Per K step (one 64-wide group) the workgroup stages x
-// (128 x 64 bf16) and the dequantized W tile (128 x 64 bf16: nibble bytes
+// 64 x 64 = 4 x 4 tiles of v_mfma_f32_16x16x32_bf16, 3 workgroups per CU;
+// on large grids 128 x 256 (waves of 64 x 128, 2 workgroups per CU).  Per K
+// step (one 64-wide group) the workgroup stages x (128 x 64 bf16) and the
+// dequantized W tile (128 or 256 x 64 bf16: nibble bytes
 // through v_cvt_f32_ubyte, one FMA, v_cvt_pk_bf16_f32 per pair) in LDS.  The
 // next group's global loads are issued before this group's products and
 // land in LDS after them.  When the tile grid is small, K is split over
@@ -21,9 +22,9 @@
 //
 // Epilogues (the prefill's MLX op sequence fused, with the same bf16
 // roundings): store; residual, y = res + bf16(x W^T) (qwen3.rs:520-521, 541);
-// SwiGLU of the gate and up weights (kernels.rs:73-74): the 128-row W tile
-// holds 64 gate rows (waves wn = 0) and the same 64 up rows (wn = 1), and
-// the up accumulators cross to the gate waves through LDS.
+// SwiGLU of the gate and up weights (kernels.rs:73-74): each wave's half of
+// the W tile holds gate rows and the up rows of the same output columns, so
+// both products of an output end in one lane.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -48,7 +49,15 @@ constexpr int QBM = 128, QBN = 128, QT = 256;  // tile rows of x, of W; threads
 // bytes) left the operand reads or the W stores 4-8 cycles per instruction
 // in conflicts.
 constexpr int RS = 64;  // LDS row stride (elements)
-constexpr size_t kQmmLds = (1ull * QBM * RS + 1ull * QBN * RS) * 2;
+// LDS of a workgroup with a BN-row W tile: 32 KB (BN 128) or 48 KB (BN 256)
+constexpr size_t qmm_lds(int bn) { return (1ull * QBM * RS + 1ull * bn * RS) * 2; }
+// 256-row W tiles where the grid of them still spans two or more rounds of
+// the 512 resident workgroups they allow (2 per CU): at M = 4096 on
+// 12288 x 4096 / 9728 x 2560 / 19456 x 2560, 10-17% faster than 128-row
+// tiles; on smaller grids tile quantization eats the gain
+bool qmm_wide(int M, int cols_wide_n) {
+  return static_cast<int64_t>((M + QBM - 1) / QBM) * cols_wide_n >= 1024;
+}
 __device__ __forceinline__ int swz(int row, int chunk) { return row * RS + ((chunk ^ (row & 7)) << 3); }
 
 struct QmmParams {
@@ -83,18 +92,23 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
-template <int EPI>
+// BN: W rows per tile, 128 (waves of 64 x 64) or 256 (waves of 64 x 128:
+// the x tile serves twice the W rows, for large grids)
+template <int EPI, int BN>
 __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
+  static_assert(BN == 128 || BN == 256, "W tile rows");
+  constexpr int NJ = BN / 32;   // 16-row W tiles per wave
+  constexpr int WR = BN / 128;  // W rows staged per thread
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [QBM][RS], swizzled
-  uint16_t* ws = xs + QBM * RS;                      // [QBN][RS], swizzled
+  uint16_t* ws = xs + QBM * RS;                      // [BN][RS], swizzled
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;  // wave sub-tile: x rows 64 wm, W rows 64 wn
+  const int wm = wave >> 1, wn = wave & 1;  // wave sub-tile: x rows 64 wm, W rows BN/2 wn
   const int li = lane & 15, q = lane >> 4;
   const int M = p.M, K = p.K, G = K / 64;
   int N = p.N;
-  // output columns per workgroup: 128, or 64 gate / up pairs for SwiGLU
-  constexpr int CN = EPI == QMM_SWIGLU ? QBN / 2 : QBN;
+  // output columns per workgroup: BN, or BN / 2 gate / up pairs for SwiGLU
+  constexpr int CN = EPI == QMM_SWIGLU ? BN / 2 : BN;
   // Tile of this workgroup.  Row-major (column tiles fastest): the ~768
   // resident workgroups cover a few row tiles and every column tile, so
   // each x row tile and W tile is reused from L2 while resident.  With
@@ -145,22 +159,38 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   const uint16_t* xp1 = xrow(tid + QT);
   const uint16_t* xp2 = xrow(tid + 2 * QT);
   const uint16_t* xp3 = xrow(tid + 3 * QT);
-  const int wr = tid >> 1, wh = tid & 1;  // W row of the tile, half of the group
-  const bool up_row = EPI == QMM_SWIGLU && wr >= CN;
-  const int64_t wrow = min(n0 + (EPI == QMM_SWIGLU ? wr % CN : wr), N - 1);
-  const uint32_t* wp = (up_row ? p.w2 : pw) + wrow * (K / 8) + wh * 4;
-  const uint16_t* sp = (up_row ? p.s2 : ps) + wrow * G;
-  const uint16_t* bp = (up_row ? p.b2 : pb) + wrow * G;
-  uint4 xr0, xr1, xr2, xr3, wq;
-  uint16_t sr, br;
+  // W rows wr (and wr + 128 with BN 256) of the tile, half wh of the group
+  const int wr = tid >> 1, wh = tid & 1;
+  // SwiGLU: each wave's BN / 2 W rows are BN / 4 gate rows and the up rows
+  // of the same output columns, so a lane holds both products of its
+  // outputs (gate in tiles j < NJ / 2, up in j + NJ / 2)
+  auto wsrc = [&](int row, const uint32_t*& w_, const uint16_t*& s_, const uint16_t*& b_) {
+    const int r = row % (BN / 2), col = (row / (BN / 2)) * (BN / 4) + r % (BN / 4);
+    const bool up_row = EPI == QMM_SWIGLU && r >= BN / 4;
+    const int64_t wrow = min(n0 + (EPI == QMM_SWIGLU ? col : row), N - 1);
+    w_ = (up_row ? p.w2 : pw) + wrow * (K / 8) + wh * 4;
+    s_ = (up_row ? p.s2 : ps) + wrow * G;
+    b_ = (up_row ? p.b2 : pb) + wrow * G;
+  };
+  const uint32_t *wp0, *wp1 = nullptr;
+  const uint16_t *sp0, *bp0, *sp1 = nullptr, *bp1 = nullptr;
+  wsrc(wr, wp0, sp0, bp0);
+  if constexpr (WR == 2) wsrc(wr + 128, wp1, sp1, bp1);
+  uint4 xr0, xr1, xr2, xr3, wq0, wq1;
+  uint16_t sr0, br0, sr1, br1;
   auto load = [&](int g) {
     xr0 = *reinterpret_cast<const uint4*>(xp0 + g * 64);
     xr1 = *reinterpret_cast<const uint4*>(xp1 + g * 64);
     xr2 = *reinterpret_cast<const uint4*>(xp2 + g * 64);
     xr3 = *reinterpret_cast<const uint4*>(xp3 + g * 64);
-    wq = *reinterpret_cast<const uint4*>(wp + g * 8);
-    sr = sp[g];
-    br = bp[g];
+    wq0 = *reinterpret_cast<const uint4*>(wp0 + g * 8);
+    sr0 = sp0[g];
+    br0 = bp0[g];
+    if constexpr (WR == 2) {
+      wq1 = *reinterpret_cast<const uint4*>(wp1 + g * 8);
+      sr1 = sp1[g];
+      br1 = bp1[g];
+    }
   };
   // ---- registers -> LDS: x as is, W dequantized to bf16 ----
   auto store = [&]() {
@@ -169,6 +199,7 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     put_x(tid + QT, xr1);
     put_x(tid + 2 * QT, xr2);
     put_x(tid + 3 * QT, xr3);
+    auto put_row = [&](int row, const uint4 wq, uint16_t sr, uint16_t br) {
     const float sv = bf2f(sr), bv = bf2f(br);
     auto put_word = [&](int chunk, uint32_t word) {
       // nibble k of the word is value k: even k in the low nibble of byte
@@ -184,19 +215,22 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
       o.z = pk_bf16(fmaf(sv, static_cast<float>((lo >> 16) & 0xffu), bv),
                     fmaf(sv, static_cast<float>((hi >> 16) & 0xffu), bv));
       o.w = pk_bf16(fmaf(sv, static_cast<float>(lo >> 24), bv), fmaf(sv, static_cast<float>(hi >> 24), bv));
-      *reinterpret_cast<uint4*>(ws + swz(wr, chunk)) = o;
+      *reinterpret_cast<uint4*>(ws + swz(row, chunk)) = o;
     };
     put_word(wh * 4, wq.x);
     put_word(wh * 4 + 1, wq.y);
     put_word(wh * 4 + 2, wq.z);
     put_word(wh * 4 + 3, wq.w);
+    };
+    put_row(wr, wq0, sr0, br0);
+    if constexpr (WR == 2) put_row(wr + 128, wq1, sr1, br1);
   };
 
-  f32x4_t acc[4][4];
+  f32x4_t acc[4][NJ];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < NJ; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   load(gb);
   store();
@@ -211,8 +245,8 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
       for (int t = 0; t < 2; t++)
         af[i][t] = *reinterpret_cast<const bf16x8_t*>(xs + swz(wm * 64 + i * 16 + li, t * 4 + q));
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int c = wn * 64 + j * 16 + li;
+    for (int j = 0; j < NJ; j++) {
+      const int c = wn * (BN / 2) + j * 16 + li;
       const bf16x8_t b0 = *reinterpret_cast<const bf16x8_t*>(ws + swz(c, q));
       const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(ws + swz(c, 4 + q));
 #pragma unroll
@@ -229,38 +263,37 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
 
   // ---- epilogue: lane holds W row 16 j + li, x rows 4 q + r of each tile ----
   if constexpr (EPI == QMM_SWIGLU) {
-    // up accumulators (waves wn = 1) to the gate waves of the same rows
-    float* xch = reinterpret_cast<float*>(smem);  // [2 wm][4 i][4 j][4 r][64 lanes]
-    __syncthreads();                              // every read of the last tiles is done
-    if (wn == 1) {
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+      for (int j = 0; j < NJ / 2; j++) {
+        const int n = n0 + wn * (BN / 4) + j * 16 + li;
+        if (n >= N) continue;
 #pragma unroll
-          for (int r = 0; r < 4; r++) xch[(((wm * 4 + i) * 4 + j) * 4 + r) * 64 + lane] = acc[i][j][r];
-    }
-    __syncthreads();
-    if (wn == 1) return;
+        for (int r = 0; r < 4; r++) {
+          const int m = m0 + wm * 64 + i * 16 + 4 * q + r;
+          if (m >= M) continue;
+          // silu(gate) * up, each MLX op rounding to bf16 (kernels.rs:73-74)
+          const float g = round_bf(acc[i][j][r]);
+          const float u = round_bf(acc[i][j + NJ / 2][r]);
+          const float sg = round_bf(1.0f / (1.0f + expf(-g)));
+          py[static_cast<int64_t>(m) * N + n] = f2bf(round_bf(g * sg) * u);
+        }
+      }
+    return;
   }
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int n = n0 + (EPI == QMM_SWIGLU ? 0 : wn * 64) + j * 16 + li;
+    for (int j = 0; j < NJ; j++) {
+      const int n = n0 + wn * (BN / 2) + j * 16 + li;
       if (n >= N) continue;
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + wm * 64 + i * 16 + 4 * q + r;
         if (m >= M) continue;
         const int64_t o = static_cast<int64_t>(m) * N + n;
-        if constexpr (EPI == QMM_SWIGLU) {
-          // silu(gate) * up, each MLX op rounding to bf16 (kernels.rs:73-74)
-          const float g = round_bf(acc[i][j][r]);
-          const float u = round_bf(reinterpret_cast<const float*>(smem)[(((wm * 4 + i) * 4 + j) * 4 + r) * 64 + lane]);
-          const float sg = round_bf(1.0f / (1.0f + expf(-g)));
-          py[o] = f2bf(round_bf(g * sg) * u);
-        } else if (p.part) {
+        if (p.part) {
           p.part[static_cast<int64_t>(blockIdx.z) * M * N + o] = acc[i][j][r];
         } else if constexpr (EPI == QMM_RESIDUAL) {
           py[o] = f2bf(bf2f(p.res[o]) + round_bf(acc[i][j][r]));
@@ -393,9 +426,13 @@ int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const 
     return set_error(BMX_E_ALIGN, "qmm: x and W must be 16-byte aligned");
   if ((M + QBM - 1) / QBM > 65535 || static_cast<int64_t>((M + QBM - 1) / QBM) * ((N + QBN / 2 - 1) / (QBN / 2)) > INT32_MAX)
     return set_error(BMX_E_SHAPE, "qmm: M=%d N=%d too large", M, N);
-  const int cols = epi == QMM_SWIGLU ? QBN / 2 : QBN;  // output columns per workgroup
-  int splits, gps;
-  qmm_split(M, N, K, &splits, &gps, cols);
+  // output columns per workgroup: 128 or 256 (64 or 128 gate / up pairs for
+  // SwiGLU)
+  const int wide_cols = epi == QMM_SWIGLU ? QBN : 2 * QBN;
+  const bool wide = qmm_wide(M, (N + wide_cols - 1) / wide_cols);
+  const int cols = wide ? wide_cols : epi == QMM_SWIGLU ? QBN / 2 : QBN;
+  int splits = 1, gps = K / 64;
+  if (!wide) qmm_split(M, N, K, &splits, &gps, cols);
   // SwiGLU needs both products of an output in one workgroup: no K split
   if (epi == QMM_SWIGLU && splits > 1) return kNoFit;
   const int mtiles = (M + QBM - 1) / QBM, ntiles = (N + cols - 1) / cols;
@@ -407,14 +444,17 @@ int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const 
     if (int rc = split_scratch(static_cast<size_t>(splits) * M * N, ws, ws_floats, stream, &p.part)) return rc;
   }
   const dim3 grid(static_cast<unsigned>(mtiles) * ntiles, 1, splits);
-  auto launch = [&](auto kern) {
-    if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(kern), kQmmLds)) return rc;
-    hipLaunchKernelGGL(kern, grid, dim3(QT), kQmmLds, stream, p);
+  auto launch = [&](auto kern, int bn) {
+    if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(kern), qmm_lds(bn))) return rc;
+    hipLaunchKernelGGL(kern, grid, dim3(QT), qmm_lds(bn), stream, p);
     return check_launch("qmm");
   };
-  const int rc = epi == QMM_SWIGLU    ? launch(qmm_kernel<QMM_SWIGLU>)
-                 : epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL>)
-                                       : launch(qmm_kernel<QMM_STORE>);
+  const int rc = wide ? (epi == QMM_SWIGLU    ? launch(qmm_kernel<QMM_SWIGLU, 256>, 256)
+                         : epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL, 256>, 256)
+                                               : launch(qmm_kernel<QMM_STORE, 256>, 256))
+                      : (epi == QMM_SWIGLU    ? launch(qmm_kernel<QMM_SWIGLU, 128>, 128)
+                         : epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL, 128>, 128)
+                                               : launch(qmm_kernel<QMM_STORE, 128>, 128));
   if (rc) return rc;
   if (splits > 1) {
     const int64_t mn = static_cast<int64_t>(M) * N;
@@ -436,8 +476,16 @@ int launch_qmm_segments(const uint16_t* x, int nseg, const uint32_t* const* w, c
     one = one && n[i] > 0 && n[i] % QBN == 0 && aligned(w[i], 16);
     ntot += n[i];
   }
+  // 256-column tiles when every segment is whole ones and the grid is large
+  bool wide = one && qmm_wide(M, ntot / (2 * QBN));
+  for (int i = 0; i < nseg; i++) wide = wide && n[i] % (2 * QBN) == 0;
   int splits = 2, gps = 0;
-  if (one) qmm_split(M, ntot, K, &splits, &gps, QBN);
+  if (wide) {
+    splits = 1;
+    gps = K / 64;
+  } else if (one) {
+    qmm_split(M, ntot, K, &splits, &gps, QBN);
+  }
   // one launch when every segment is whole tiles and K is not split (the
   // reduction writes one y); else a launch per segment
   if (!one || splits > 1 || (M + QBM - 1) / QBM > 65535) {
@@ -445,7 +493,8 @@ int launch_qmm_segments(const uint16_t* x, int nseg, const uint32_t* const* w, c
       if (int rc = launch_qmm(x, w[i], s[i], b[i], y[i], M, n[i], K, ws, ws_floats, stream)) return rc;
     return BMX_OK;
   }
-  const int mtiles = (M + QBM - 1) / QBM, ntiles = ntot / QBN;
+  const int bn = wide ? 2 * QBN : QBN;
+  const int mtiles = (M + QBM - 1) / QBM, ntiles = ntot / bn;
   QmmParams p{x, w[0], s[0], b[0], nullptr, nullptr, nullptr, nullptr, y[0], nullptr, M, ntot, K, gps, mtiles, 0};
   p.nseg = nseg;
   int c = 0;
@@ -458,9 +507,9 @@ int launch_qmm_segments(const uint16_t* x, int nseg, const uint32_t* const* w, c
     c += n[i];
   }
   for (int i = nseg; i < 4; i++) p.seg_n0[i] = c;
-  if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(qmm_kernel<QMM_STORE>), kQmmLds)) return rc;
-  hipLaunchKernelGGL(qmm_kernel<QMM_STORE>, dim3(static_cast<unsigned>(mtiles) * ntiles, 1, 1), dim3(QT), kQmmLds,
-                     stream, p);
+  auto kern = wide ? qmm_kernel<QMM_STORE, 256> : qmm_kernel<QMM_STORE, 128>;
+  if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(kern), qmm_lds(bn))) return rc;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(mtiles) * ntiles, 1, 1), dim3(QT), qmm_lds(bn), stream, p);
   return check_launch("qmm");
 }
 
