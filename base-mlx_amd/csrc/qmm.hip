@@ -58,6 +58,17 @@ constexpr size_t qmm_lds(int bn) { return (1ull * QBM * RS + 1ull * bn * RS) * 2
 bool qmm_wide(int M, int cols_wide_n) {
   return static_cast<int64_t>((M + QBM - 1) / QBM) * cols_wide_n >= 1024;
 }
+// 160-row W tiles (not SwiGLU) where N is a multiple of 160 and they fill
+// the 512 resident workgroups they allow (2 per CU) better than 128-row
+// tiles fill theirs: N = 2560 at M = 4096 is 640 tiles of 128 (half the
+// CUs run 3) or 512 of 160 (every CU runs 2): 289 -> 271 us at K = 9728.
+// (With one 160-row tile per CU, M = 2048, the K split of 128-row tiles
+// measured faster: 169 against 233 us.)
+bool qmm_tile160(int M, int N) {
+  if (N % 160) return false;
+  const int64_t mt = (M + QBM - 1) / QBM, t128 = mt * ((N + 127) / 128), t160 = mt * (N / 160);
+  return t160 > 384 && t160 <= 512 && (t128 + 255) / 256 * 128 > (t160 + 255) / 256 * 160;
+}
 __device__ __forceinline__ int swz(int row, int chunk) { return row * RS + ((chunk ^ (row & 7)) << 3); }
 
 struct QmmParams {
@@ -96,9 +107,10 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 // the x tile serves twice the W rows, for large grids)
 template <int EPI, int BN>
 __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
-  static_assert(BN == 128 || BN == 256, "W tile rows");
-  constexpr int NJ = BN / 32;   // 16-row W tiles per wave
-  constexpr int WR = BN / 128;  // W rows staged per thread
+  static_assert(BN == 128 || BN == 160 || BN == 256, "W tile rows");
+  static_assert(EPI != QMM_SWIGLU || BN % 64 == 0, "SwiGLU pairs gate and up rows per wave");
+  constexpr int NJ = BN / 32;                // 16-row W tiles per wave
+  constexpr int WR = (BN + 127) / 128;       // W rows staged per thread (the second only below BN)
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [QBM][RS], swizzled
   uint16_t* ws = xs + QBM * RS;                      // [BN][RS], swizzled
@@ -175,7 +187,9 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   const uint32_t *wp0, *wp1 = nullptr;
   const uint16_t *sp0, *bp0, *sp1 = nullptr, *bp1 = nullptr;
   wsrc(wr, wp0, sp0, bp0);
-  if constexpr (WR == 2) wsrc(wr + 128, wp1, sp1, bp1);
+  // (BN 160: the second row exists for wr < 32, i.e. wave 0; uniform per wave)
+  const bool row1 = WR == 2 && wr + 128 < BN;
+  if (row1) wsrc(wr + 128, wp1, sp1, bp1);
   uint4 xr0, xr1, xr2, xr3, wq0, wq1;
   uint16_t sr0, br0, sr1, br1;
   auto load = [&](int g) {
@@ -186,7 +200,7 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     wq0 = *reinterpret_cast<const uint4*>(wp0 + g * 8);
     sr0 = sp0[g];
     br0 = bp0[g];
-    if constexpr (WR == 2) {
+    if (row1) {
       wq1 = *reinterpret_cast<const uint4*>(wp1 + g * 8);
       sr1 = sp1[g];
       br1 = bp1[g];
@@ -223,7 +237,7 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     put_word(wh * 4 + 3, wq.w);
     };
     put_row(wr, wq0, sr0, br0);
-    if constexpr (WR == 2) put_row(wr + 128, wq1, sr1, br1);
+    if (row1) put_row(wr + 128, wq1, sr1, br1);
   };
 
   f32x4_t acc[4][NJ];
@@ -430,9 +444,10 @@ int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const 
   // SwiGLU)
   const int wide_cols = epi == QMM_SWIGLU ? QBN : 2 * QBN;
   const bool wide = qmm_wide(M, (N + wide_cols - 1) / wide_cols);
-  const int cols = wide ? wide_cols : epi == QMM_SWIGLU ? QBN / 2 : QBN;
+  const int bn = wide ? 256 : epi != QMM_SWIGLU && qmm_tile160(M, N) ? 160 : 128;
+  const int cols = epi == QMM_SWIGLU ? bn / 2 : bn;
   int splits = 1, gps = K / 64;
-  if (!wide) qmm_split(M, N, K, &splits, &gps, cols);
+  if (bn == 128) qmm_split(M, N, K, &splits, &gps, cols);
   // SwiGLU needs both products of an output in one workgroup: no K split
   if (epi == QMM_SWIGLU && splits > 1) return kNoFit;
   const int mtiles = (M + QBM - 1) / QBM, ntiles = (N + cols - 1) / cols;
@@ -449,12 +464,14 @@ int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const 
     hipLaunchKernelGGL(kern, grid, dim3(QT), qmm_lds(bn), stream, p);
     return check_launch("qmm");
   };
-  const int rc = wide ? (epi == QMM_SWIGLU    ? launch(qmm_kernel<QMM_SWIGLU, 256>, 256)
-                         : epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL, 256>, 256)
-                                               : launch(qmm_kernel<QMM_STORE, 256>, 256))
-                      : (epi == QMM_SWIGLU    ? launch(qmm_kernel<QMM_SWIGLU, 128>, 128)
-                         : epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL, 128>, 128)
-                                               : launch(qmm_kernel<QMM_STORE, 128>, 128));
+  const int rc = bn == 256   ? (epi == QMM_SWIGLU    ? launch(qmm_kernel<QMM_SWIGLU, 256>, 256)
+                                : epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL, 256>, 256)
+                                                      : launch(qmm_kernel<QMM_STORE, 256>, 256))
+                 : bn == 160 ? (epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL, 160>, 160)
+                                                    : launch(qmm_kernel<QMM_STORE, 160>, 160))
+                             : (epi == QMM_SWIGLU    ? launch(qmm_kernel<QMM_SWIGLU, 128>, 128)
+                                : epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL, 128>, 128)
+                                                      : launch(qmm_kernel<QMM_STORE, 128>, 128));
   if (rc) return rc;
   if (splits > 1) {
     const int64_t mn = static_cast<int64_t>(M) * N;

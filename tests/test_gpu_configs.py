@@ -157,6 +157,36 @@ QMM_SHAPES = [(4096, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (2560, 972
               (4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288), (151936, 4096)]
 
 
+# The GEMM's tile heights: 160-row W tiles (M 4096, N 2560; M 2048, N
+# 5120), 256-row tiles on large grids (M 4096, N 9728), 128 otherwise.
+@pytest.mark.parametrize("M,N,K", [(4096, 2560, 2560), (2048, 5120, 1024), (4096, 9728, 1024), (4096, 2048, 1024)])
+def test_qmm_tile_heights(gpu, orc, M, N, K):
+    """Each tile height against the oracle on 256 sampled output columns
+    (fp64 bar and 2 bf16 ulps of the oracle's dequantizing GEMM), and the
+    exact 2x property over the whole output."""
+    import torch
+
+    rng = np.random.default_rng(N + K)
+    print(f"qmm tiles M={M} N={N} K={K}", flush=True)
+    w, s, b = gpu.init_qlinear(4000 + N, N, K)
+    x = gpu.fill_normal_bf16(4100 + K, (M, K))
+    y = gpu.quantized_matmul(x, w, s, b)
+    cols = np.sort(rng.choice(N, 256, replace=False))
+    cols_t = torch.from_numpy(cols).cuda()
+    rows = np.sort(rng.choice(M, 512, replace=False))
+    rows_t = torch.from_numpy(rows).cuda()
+    xb = torch_bf16_bits(x[rows_t])
+    wq, sb, bb = u32_of(w[cols_t]), torch_bf16_bits(s[cols_t]), torch_bf16_bits(b[cols_t])
+    ys = torch_bf16_bits(y[rows_t][:, cols_t])
+    assert max_rel_err(bf16_to_f32(ys), orc.qmatmul_f64(xb, wq, sb, bb)) < 1e-2
+    ref = orc.qlinear(xb, wq, sb, bb)
+    d = np.abs(_f32(ys) - _f32(ref))
+    assert (d <= np.maximum(2 * np.abs(_f32(ref)) * 2.0 ** -7, 1e-4 * np.max(np.abs(_f32(ref))))).all()
+    y2 = gpu.quantized_matmul(x * 2, w, s, b)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y * 2)
+
+
 @pytest.mark.parametrize("M", [5, 128, 512, 2048])
 def test_config2_qmm_sweep_shapes(gpu, orc, M):
     """Config 2: quantized_matmul at every sweep shape.  Per shape: 256
