@@ -84,9 +84,9 @@ def test_qmatmul_workspace_query_and_no_alloc_variant():
     assert lib.bmx_qmatmul_workspace_bytes(1, 4096, 2560) == 0
     assert lib.bmx_qmatmul_workspace_bytes(0, 4096, 2560) == 0
     assert lib.bmx_qmatmul_workspace_bytes(64, 1024, 100) == 0  # K not a multiple of 64
-    # a small GEMM grid (8 tiles of 128 x 128) splits K = 2560: 3 splits of 16 groups
+    # a small GEMM grid (8 tiles of 128 x 128) splits K = 2560: 5 splits of 8 groups
     need = lib.bmx_qmatmul_workspace_bytes(64, 1024, 2560)
-    assert need == 3 * 64 * 1024 * 4
+    assert need == 5 * 64 * 1024 * 4
     args = (_fake(), _fake(), _fake(), _fake(), _fake(), 64, 1024, 2560, 1, 64, 4)
     assert lib.bmx_qmatmul_affine_ws(*args, _null(), 0, _null()) == bmx.BMX_E_ARG
     assert "workspace" in bmx.last_error()
