@@ -474,6 +474,24 @@ class Qwen3:
              _stream(stream))
         return out[: n.value]
 
+    def decode_greedy(self, cache, token, max_new, eos=(151645, 151643), stream=None):
+        """The greedy decode loop alone (engine.rs:103-115), continuing `cache`
+        from `token`, the token its prefill picked: returns the emitted tokens
+        (token first), at most max_new, stopping before an eos token."""
+        import numpy as np
+
+        e = np.ascontiguousarray(eos, np.uint32)
+        out = np.empty(max_new, np.uint32)
+        n = ctypes.c_int()
+        try:
+            call("bmx_decode_greedy", self.h, cache.h, ctypes.c_uint32(int(token)), max_new,
+                 e.ctypes.data_as(ctypes.c_void_p), e.size, out.ctypes.data_as(ctypes.c_void_p), ctypes.byref(n),
+                 _stream(stream))
+        except BmxError as err:
+            err.tokens = out[: n.value]
+            raise
+        return out[: n.value]
+
 
 def speculative_generate(target, tcache, draft, dcache, prompt, max_new, spec_k=5, eos=(151645, 151643), stream=None):
     import numpy as np

@@ -97,6 +97,7 @@ SIGNATURES = {
     "bmx_qwen3_forward": (c_int, [c_p, c_p, c_p, c_int, c_int, c_p, c_p]),
     "bmx_qwen3_decode_step": (c_int, [c_p, c_p, ctypes.c_uint32, c_p, c_p, c_p]),
     "bmx_generate_greedy": (c_int, [c_p, c_p, c_p, c_int, c_int, c_p, c_int, c_p, c_p, c_p]),
+    "bmx_decode_greedy": (c_int, [c_p, c_p, ctypes.c_uint32, c_int, c_p, c_int, c_p, c_p, c_p]),
     "bmx_speculative_generate": (c_int, [c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_p, c_int, c_p, c_p, c_p,
                                          c_p]),
 }

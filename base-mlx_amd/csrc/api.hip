@@ -67,7 +67,7 @@ using namespace bmx;
 
 extern "C" const char* bmx_last_error(void) { return g_last_error; }
 
-extern "C" int bmx_abi_version(void) { return (2 << 16) | 0; }
+extern "C" int bmx_abi_version(void) { return (2 << 16) | 1; }
 
 namespace {
 

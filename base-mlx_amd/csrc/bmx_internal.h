@@ -166,9 +166,21 @@ int launch_qkv_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v
 int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* ws,
                      size_t ws_floats, int Hq, int Hkv, int M, int D, int cap, int offset, const int* offset_dev,
                      int L_max, float scale, hipStream_t stream);
-int launch_argmax(const uint16_t* x, int64_t rows, int64_t n, uint32_t* out, hipStream_t stream);
+// The hand-off between decode steps queued back to back: io = [token,
+// position, next token, ring count] in device memory, ring = `mask + 1`
+// slots of mapped host memory.  A one-row argmax given a chain writes its
+// token to io[0] (the next step's embedding id), advances io[1] (the next
+// step's position) and stores the token to ring[io[3]++ & mask].
+struct DecodeChain {
+  int* io = nullptr;
+  uint32_t* ring = nullptr;
+  unsigned mask = 0;
+};
+int launch_argmax(const uint16_t* x, int64_t rows, int64_t n, uint32_t* out, hipStream_t stream,
+                  const DecodeChain* chain = nullptr);
 // Reduces `nblk` argmax partials per row (from the qmv epilogue) to out[rows].
-int launch_argmax_partials(const uint2* part, int rows, int nblk, uint32_t* out, hipStream_t stream);
+int launch_argmax_partials(const uint2* part, int rows, int nblk, uint32_t* out, hipStream_t stream,
+                           const DecodeChain* chain = nullptr);
 int launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* y, int64_t n, hipStream_t stream);
 int launch_add(const uint16_t* a, const uint16_t* b, uint16_t* y, int64_t n, hipStream_t stream);
 int launch_tokens_to_ids(const uint32_t* src, int32_t* dst, int n, hipStream_t stream);

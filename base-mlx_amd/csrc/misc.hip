@@ -48,10 +48,23 @@ __device__ __forceinline__ void block_best(float& bv, uint32_t& bi) {
   }
 }
 
+// Row 0's token handed to the next decode step (see DecodeChain): the step's
+// token and position advance in device memory, and the token goes to the
+// next slot of the host ring as one system-scope store (straight to host
+// memory, visible to the polling host without a copy or a stream sync).
+__device__ __forceinline__ void chain_publish(const DecodeChain& ch, uint32_t tok) {
+  int* io = ch.io;
+  io[0] = static_cast<int>(tok);
+  io[1] += 1;
+  const unsigned k = static_cast<unsigned>(io[3]);
+  io[3] = static_cast<int>(k + 1);
+  __hip_atomic_store(ch.ring + (k & ch.mask), tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // one workgroup per row; rows of a multiple of 8 values at 16-byte
 // alignment are read 8 values per load, 8 loads in flight per thread
 __global__ void __launch_bounds__(kArgThreads)
-    argmax_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t* __restrict__ out) {
+    argmax_kernel(const uint16_t* __restrict__ x, int64_t n, uint32_t* __restrict__ out, const DecodeChain ch) {
   const uint16_t* xr = x + static_cast<int64_t>(blockIdx.x) * n;
   float bv = -INFINITY;
   uint32_t bi = 0xffffffffu;
@@ -91,13 +104,18 @@ __global__ void __launch_bounds__(kArgThreads)
   }
   block_best(bv, bi);
   // all -inf / NaN rows: index 0
-  if (threadIdx.x == 0) out[blockIdx.x] = bi == 0xffffffffu ? 0u : bi;
+  if (threadIdx.x == 0) {
+    const uint32_t tok = bi == 0xffffffffu ? 0u : bi;
+    out[blockIdx.x] = tok;
+    if (ch.io != nullptr && blockIdx.x == 0) chain_publish(ch, tok);
+  }
 }
 
 // one workgroup per row over the per-workgroup partials (value bits, index)
 // of the GEMV epilogue
 __global__ void __launch_bounds__(kArgThreads)
-    argmax_partials_kernel(const uint2* __restrict__ part, int nblk, uint32_t* __restrict__ out) {
+    argmax_partials_kernel(const uint2* __restrict__ part, int nblk, uint32_t* __restrict__ out,
+                           const DecodeChain ch) {
   const uint2* pr = part + static_cast<int64_t>(blockIdx.x) * nblk;
   float bv = -INFINITY;
   uint32_t bi = 0xffffffffu;
@@ -119,7 +137,11 @@ __global__ void __launch_bounds__(kArgThreads)
     }
   }
   block_best(bv, bi);
-  if (threadIdx.x == 0) out[blockIdx.x] = bi == 0xffffffffu ? 0u : bi;
+  if (threadIdx.x == 0) {
+    const uint32_t tok = bi == 0xffffffffu ? 0u : bi;
+    out[blockIdx.x] = tok;
+    if (ch.io != nullptr && blockIdx.x == 0) chain_publish(ch, tok);
+  }
 }
 
 __global__ void __launch_bounds__(256)
@@ -147,18 +169,24 @@ __global__ void tokens_to_ids_kernel(const uint32_t* __restrict__ src, int32_t* 
 
 }  // namespace
 
-int launch_argmax(const uint16_t* x, int64_t rows, int64_t n, uint32_t* out, hipStream_t stream) {
+int launch_argmax(const uint16_t* x, int64_t rows, int64_t n, uint32_t* out, hipStream_t stream,
+                  const DecodeChain* chain) {
   if (rows <= 0) return BMX_OK;
   if (n <= 0 || n > UINT32_MAX) return set_error(BMX_E_SHAPE, "argmax: n=%lld", (long long)n);
   if (rows > INT32_MAX) return set_error(BMX_E_SHAPE, "argmax: rows=%lld", (long long)rows);
-  hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(rows)), dim3(kArgThreads), 0, stream, x, n, out);
+  if (chain && (rows != 1 || !chain->io || !chain->ring)) return set_error(BMX_E_ARG, "argmax: chained hand-off of %lld rows", (long long)rows);
+  const DecodeChain ch = chain ? *chain : DecodeChain{};
+  hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(rows)), dim3(kArgThreads), 0, stream, x, n, out, ch);
   return check_launch("argmax");
 }
 
-int launch_argmax_partials(const uint2* part, int rows, int nblk, uint32_t* out, hipStream_t stream) {
+int launch_argmax_partials(const uint2* part, int rows, int nblk, uint32_t* out, hipStream_t stream,
+                           const DecodeChain* chain) {
   if (rows <= 0) return BMX_OK;
   if (nblk <= 0) return set_error(BMX_E_SHAPE, "argmax partials: %d per row", nblk);
-  hipLaunchKernelGGL(argmax_partials_kernel, dim3(rows), dim3(kArgThreads), 0, stream, part, nblk, out);
+  if (chain && (rows != 1 || !chain->io || !chain->ring)) return set_error(BMX_E_ARG, "argmax: chained hand-off of %d rows", rows);
+  const DecodeChain ch = chain ? *chain : DecodeChain{};
+  hipLaunchKernelGGL(argmax_partials_kernel, dim3(rows), dim3(kArgThreads), 0, stream, part, nblk, out, ch);
   return check_launch("argmax_partials");
 }
 

@@ -8,6 +8,8 @@
 //                            (qwen3.rs:109-162)
 //   bmx_generate_greedy  <-> LoadedModel::generate_text with greedy pick_next
 //                            (crates/base-mlx-core/src/engine.rs:100-202)
+//   bmx_decode_greedy    <-> its decode loop alone, after the prefill
+//                            (engine.rs:103-115)
 //   bmx_speculative_generate <-> speculative::generate
 //                            (crates/base-mlx-core/src/speculative.rs:57-286)
 //
@@ -24,7 +26,8 @@
 // fused.  At M > 8 (prefill) the norms, SwiGLU and adds run as their own
 // kernels around the MFMA qmm.  The M = 1 decode step is captured once per
 // cache into a HIP graph that reads the token and position from device
-// memory, so a decode step is one graph launch.
+// memory and leaves the next ones there, so a decode step is one graph
+// launch and the greedy loop queues steps without waiting for each token.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -68,6 +71,13 @@ __global__ void fill_ones_kernel(uint16_t* p, int n) {
 
 using namespace bmx;
 
+// Decode steps in flight: the host ring the decode graph publishes tokens to
+// (a power of two), how many replays the greedy loop queues ahead of the
+// token it is checking, and the value of a slot not yet written.
+constexpr int kRing = 64;
+constexpr int kAhead = 3;
+constexpr uint32_t kRingEmpty = 0xffffffffu;
+
 struct bmx_kv_cache {
   uint64_t id = 0;  // unique per cache: keys the captured decode graph
   int layers = 0, nkv = 0, hd = 0, cap = 0;
@@ -95,7 +105,9 @@ struct bmx_qwen3 {
   int32_t* ids = nullptr;     // [max_tokens] token ids for the embedding gather
   uint32_t* tok_u = nullptr;  // [max(max_tokens, 64)] token staging
   uint32_t* next_tok = nullptr;  // argmax output of the decode step
-  int* step_io = nullptr;        // decode graph: [token, position, next token] (device)
+  int* step_io = nullptr;        // decode graph: [token, position, next token, ring count] (device)
+  uint32_t* ring = nullptr;      // mapped host [kRing]: tokens the decode graph publishes
+  uint32_t* ring_dev = nullptr;  // the same memory, as the device addresses it
   uint2* amax = nullptr;         // lm_head argmax partials of the decode graph
   int amax_cap = 0;
   uint32_t* host_tok = nullptr;    // pinned [64]: token / position / argmax exchange
@@ -301,14 +313,19 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
 // forward, with the lm_head GEMV writing per-workgroup argmax partials, then
 // the reduction of the partials -> step_io[2].  Captured into a graph.  The
 // token is read as the embedding id directly: tokens are below the
-// vocabulary size (checked on the host, or produced by the argmax).
+// vocabulary size (checked on the host, or produced by the argmax).  The
+// argmax also hands the step over to the next one (DecodeChain): the token
+// becomes step_io[0], the position step_io[1] + 1, and the token lands in
+// ring slot step_io[3]++ -- so replays queued back to back decode
+// consecutive tokens without the host in between.
 int decode_step_device(bmx_qwen3* m, bmx_kv_cache* c, hipStream_t st) {
   int nblk = 0;
   if (int rc = forward_device(m, c, 1, 0, m->step_io + 1, false, m->logits1, st, m->step_io, m->amax, &nblk))
     return rc;
   uint32_t* next = reinterpret_cast<uint32_t*>(m->step_io + 2);
-  if (nblk == 0) return launch_argmax(m->logits1, 1, m->cfg.vocab, next, st);
-  return launch_argmax_partials(m->amax, 1, nblk, next, st);
+  const DecodeChain chain{m->step_io, m->ring_dev, kRing - 1};
+  if (nblk == 0) return launch_argmax(m->logits1, 1, m->cfg.vocab, next, st, &chain);
+  return launch_argmax_partials(m->amax, 1, nblk, next, st, &chain);
 }
 
 void drop_graph(bmx_qwen3* m) {
@@ -436,6 +453,13 @@ int qwen3_alloc(const bmx_qwen3_config* cfg, int max_tokens, bmx_qwen3** out) {
   if (!rc) rc = dalloc_t(m, &m->amax, static_cast<size_t>(m->amax_cap));
   if (!rc) rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&m->host_tok), 64 * sizeof(uint32_t), hipHostMallocDefault), "hipHostMalloc");
   if (!rc) rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&m->host_stage), T * sizeof(uint32_t), hipHostMallocDefault), "hipHostMalloc");
+  if (!rc)
+    rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(&m->ring), kRing * sizeof(uint32_t),
+                                 hipHostMallocMapped | hipHostMallocCoherent),
+                   "hipHostMalloc");
+  if (!rc) rc = check_hip(hipHostGetDevicePointer(reinterpret_cast<void**>(&m->ring_dev), m->ring, 0), "ring address");
+  if (!rc)
+    for (int i = 0; i < kRing; i++) m->ring[i] = kRingEmpty;
   if (!rc) rc = check_hip(hipEventCreateWithFlags(&m->stage_done, hipEventDisableTiming), "event create");
   if (!rc) rc = check_hip(hipEventRecord(m->stage_done, st), "event record");
   if (!rc) rc = check_hip(hipStreamCreate(&m->own_stream), "stream create");
@@ -516,6 +540,7 @@ extern "C" void bmx_qwen3_destroy(bmx_qwen3* m) {
   for (void* p : m->allocs) (void)hipFree(p);
   if (m->host_tok) (void)hipHostFree(m->host_tok);
   if (m->host_stage) (void)hipHostFree(m->host_stage);
+  if (m->ring) (void)hipHostFree(m->ring);
   if (m->stage_done) (void)hipEventDestroy(m->stage_done);
   if (m->own_stream) (void)hipStreamDestroy(m->own_stream);
   delete m;
@@ -641,6 +666,102 @@ extern "C" int bmx_qwen3_decode_step(bmx_qwen3* m, bmx_kv_cache* c, uint32_t tok
   return BMX_OK;
 }
 
+// Waits for the decode graph to publish ring slot `slot` (polling the mapped
+// host memory), watching the stream so that a failed or drained stream ends
+// the wait with an error instead of a hang.
+static int ring_wait(bmx_qwen3* m, hipStream_t st, int slot, uint32_t* tok) {
+  volatile uint32_t* r = m->ring + slot;
+  for (unsigned spin = 1;; spin++) {
+    const uint32_t v = *r;
+    if (v != kRingEmpty) {
+      *tok = v;
+      return BMX_OK;
+    }
+    if ((spin & 255) == 0) {
+      const hipError_t e = hipStreamQuery(st);
+      if (e == hipSuccess) {
+        // the stream is idle, so the slot's store has landed if it was made
+        const uint32_t v2 = *r;
+        if (v2 == kRingEmpty)
+          return set_error(static_cast<int>(hipErrorUnknown), "decode: step %d ended without its token", slot);
+        *tok = v2;
+        return BMX_OK;
+      }
+      if (e != hipErrorNotReady) return check_hip(e, "decode wait");
+    }
+    __builtin_ia32_pause();
+  }
+}
+
+// The greedy decode loop of engine.rs:103-115 from the token the prefill
+// picked: emit `first` unless it is an eos token, then decode one token per
+// step from the last one emitted until an eos token (not emitted) or
+// max_new tokens.  The steps are graph replays queued up to kAhead ahead of
+// the token being checked: each replay takes its token and position from
+// the previous one on the device and publishes its token to the host ring,
+// so the GPU runs step after step while the host checks tokens behind it.
+// When an eos token ends the loop, the replays queued past it are drained
+// and the cache is rewound to the steps the loop took (their K/V rows lie at
+// and beyond seq_len, where the next step writes before any step reads).
+// Output, seq_len and errors are those of one synchronous step at a time,
+// including the capacity error at the step that would not fit.
+static int decode_loop(bmx_qwen3* m, bmx_kv_cache* c, hipStream_t st, uint32_t first, int max_new,
+                       const uint32_t* eos, int n_eos, uint32_t* out, int* n_out) {
+  int n = 0;
+  *n_out = 0;
+  if (is_eos(first, eos, n_eos)) return BMX_OK;
+  out[n++] = first;
+  const int steps = max_new - 1;                         // steps the loop takes without an eos
+  const int fit = std::min(steps, c->cap - c->seq_len);  // of which the cache holds
+  const int seq0 = c->seq_len;
+  int rc = BMX_OK, launched = 0, done = 0;
+  if (fit > 0) {
+    rc = ensure_graph(m, c, st);
+    if (!rc) {
+      m->host_tok[0] = first;
+      m->host_tok[1] = static_cast<uint32_t>(seq0);
+      m->host_tok[2] = 0;
+      m->host_tok[3] = 0;  // ring count: step i publishes to slot i
+      rc = check_hip(hipMemcpyAsync(m->step_io, &m->host_tok[0], 16, hipMemcpyHostToDevice, st), "set token");
+    }
+  }
+  while (!rc && done < steps) {
+    while (launched < fit && launched - done < kAhead) {
+      m->ring[launched & (kRing - 1)] = kRingEmpty;
+      rc = check_hip(hipGraphLaunch(m->graph, st), "graph launch");
+      if (rc) break;
+      launched++;
+    }
+    if (rc) break;
+    if (done == fit) {
+      rc = set_error(BMX_E_KV_CAPACITY, "KV cache exhausted: requested %d positions, max %d", seq0 + fit + 1, c->cap);
+      break;
+    }
+    uint32_t t;
+    rc = ring_wait(m, st, done & (kRing - 1), &t);
+    if (rc) break;
+    done++;
+    if (is_eos(t, eos, n_eos)) break;
+    out[n++] = t;
+  }
+  // the replays queued past an eos, and the staging copy, finish here
+  const int rs = check_hip(hipStreamSynchronize(st), "decode sync");
+  c->seq_len = seq0 + done;
+  *n_out = n;
+  return rc ? rc : rs;
+}
+
+extern "C" int bmx_decode_greedy(bmx_qwen3* m, bmx_kv_cache* c, uint32_t token, int max_new, const uint32_t* eos,
+                                 int n_eos, uint32_t* out, int* n_out, void* stream) {
+  if (!m || !c || !out || !n_out || (n_eos > 0 && !eos)) return set_error(BMX_E_ARG, "decode: null pointer");
+  *n_out = 0;
+  if (max_new <= 0) return set_error(BMX_E_ARG, "decode: max_new=%d", max_new);
+  if (token >= static_cast<uint32_t>(m->cfg.vocab)) return set_error(BMX_E_ARG, "decode: token %u", token);
+  if (c->layers != m->cfg.layers || c->nkv != m->cfg.n_kv_heads)  // qwen3.rs:351-358
+    return set_error(BMX_E_SHAPE, "cache layer count %d != model layers %d", c->layers, m->cfg.layers);
+  return decode_loop(m, c, pick_stream(m, stream), token, max_new, eos, n_eos, out, n_out);
+}
+
 extern "C" int bmx_generate_greedy(bmx_qwen3* m, bmx_kv_cache* c, const uint32_t* prompt, int P, int max_new,
                                    const uint32_t* eos, int n_eos, uint32_t* out, int* n_out, void* stream) {
   if (!m || !c || !prompt || !out || !n_out || (n_eos > 0 && !eos)) return set_error(BMX_E_ARG, "generate: null pointer");
@@ -648,7 +769,7 @@ extern "C" int bmx_generate_greedy(bmx_qwen3* m, bmx_kv_cache* c, const uint32_t
   if (P <= 0 || max_new <= 0) return set_error(BMX_E_ARG, "generate: P=%d max_new=%d", P, max_new);
   hipStream_t st = pick_stream(m, stream);
   // prefill in chunks of max_tokens (a single forward in the reference,
-  // engine.rs:107; chunking changes no result: every op is row-wise or
+  // engine.rs:98; chunking changes no result: every op is row-wise or
   // causal over the cache)
   int done = 0;
   while (done < P) {
@@ -667,23 +788,7 @@ extern "C" int bmx_generate_greedy(bmx_qwen3* m, bmx_kv_cache* c, const uint32_t
   if (int rc = check_hip(hipMemcpyAsync(&m->host_tok[2], m->next_tok, 4, hipMemcpyDeviceToHost, st), "read token"))
     return rc;
   if (int rc = check_hip(hipStreamSynchronize(st), "prefill sync")) return rc;
-  uint32_t next = m->host_tok[2];
-  int produced = 0, n = 0;
-  // loop of engine.rs:112-124
-  for (;;) {
-    produced++;
-    if (is_eos(next, eos, n_eos)) break;
-    out[n++] = next;
-    if (produced >= max_new) break;
-    uint32_t nx;
-    if (int rc = graph_step(m, c, st, next, &nx)) {
-      *n_out = n;
-      return rc;
-    }
-    next = nx;
-  }
-  *n_out = n;
-  return BMX_OK;
+  return decode_loop(m, c, st, m->host_tok[2], max_new, eos, n_eos, out, n_out);
 }
 
 // Verify forward for the speculative loop: tokens (host) -> argmax of every

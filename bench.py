@@ -6,8 +6,11 @@ Workload (the headline `value`): a random-init Qwen3-4B-shaped model
 vocab 151936, MLX 4-bit gs64), KV cache [36, 2, 8, 4352, 128] bf16, a
 4096-token seeded random prompt prefilled untimed, then greedy decode.  One
 step = one decode token: a graph launch of the whole forward (36 layers +
-lm_head + argmax) and the 4-byte readback of the token, as the reference's
-generate loop syncs once per token.  `value` = decode tokens / s.
+lm_head + argmax), run by the library's greedy decode loop, which checks each
+token for eos on the host as the reference's generate loop does while the
+next steps are already queued on the GPU.  `value` = decode tokens / s.
+`config.decode_step_sync_tok_s` times the same tokens one synchronous decode
+step at a time (token read back before the next launch).
 
 `roofline`: the qmv GEMV at the gate/up projection shape (9728 x 2560),
 timed with HIP events around a graph of launches on the benchmark stream,
@@ -290,7 +293,7 @@ def speculative_bench(bmx, torch, new_tokens=512, prompt_len=2048, spec_k=5):
 def small_model_bench(bmx, torch, prompt_len=32, new_tokens=64, seed=7, cpu=True):
     """The Qwen3-0.6B-shaped model (28 layers, hidden 1024, tied head): a
     32-token seeded prompt, then 64 greedy decode tokens -- on the GPU
-    (prefill forward, then one graph replay per token) and, as the reference
+    (prefill forward, then the greedy decode loop of graph replays) and, as the reference
     runs this configuration on its CPU path, with the oracle on the host
     cores (prefill forward, then one forward per token).  Also reports how
     many leading greedy tokens the two agree on (random-init logits have
@@ -312,11 +315,8 @@ def small_model_bench(bmx, torch, prompt_len=32, new_tokens=64, seed=7, cpu=True
     tok = int(torch.argmax(logits.float()).item())
     torch.cuda.synchronize()
     gpu_prefill = time.perf_counter() - t0
-    gpu_toks = [tok]
     t0 = time.perf_counter()
-    for _ in range(new_tokens - 1):
-        tok = m.decode_step(c, tok)
-        gpu_toks.append(tok)
+    gpu_toks = [int(v) for v in m.decode_greedy(c, tok, new_tokens, eos=())]
     torch.cuda.synchronize()
     gpu_decode = time.perf_counter() - t0
     m.close()
@@ -484,18 +484,31 @@ def main():
             t = model.decode_step(cache, t)
         cache.truncate(args.prompt)
         torch.cuda.synchronize()
-        # timed region: exactly `steps` decode tokens from position 4096
+        # timed region: exactly `steps` decode tokens from position 4096,
+        # through the greedy decode loop (the prefill's token first, then one
+        # graph replay per token, queued ahead of the token being checked)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        toks = model.decode_greedy(cache, tok, args.steps + 1, eos=())
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        assert len(toks) == args.steps + 1 and cache.seq_len == args.prompt + args.steps
+        # the same steps one synchronous bmx_qwen3_decode_step at a time: the
+        # host reads each token before it launches the next step
+        cache.truncate(args.prompt)
         t = tok
-        toks = []
+        sync_toks = [tok]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
             t = model.decode_step(cache, t)
-            toks.append(t)
+            sync_toks.append(t)
         torch.cuda.synchronize()
-        dt = time.perf_counter() - t0
+        dt_sync = time.perf_counter() - t0
+        assert list(toks) == sync_toks, "queued and synchronous decode steps disagree"
     tok_s = args.steps / dt
-    log(f"decode {args.steps} tokens at ctx {args.prompt}: {dt * 1000 / args.steps:.3f} ms/token, {tok_s:.1f} tok/s")
+    log(f"decode {args.steps} tokens at ctx {args.prompt}: {dt * 1000 / args.steps:.3f} ms/token, {tok_s:.1f} tok/s "
+        f"(one synchronous step at a time: {dt_sync * 1000 / args.steps:.3f} ms/token)")
     model.close()
     del cache
     torch.cuda.empty_cache()
@@ -547,7 +560,8 @@ def main():
         "data": "synthetic: seeded random-init weights N(0,0.02) quantized 4-bit, seeded random token ids",
         "config": {"workload": "Qwen3-4B-shape 4-bit greedy decode, batch 1, after a 4096-token prefill",
                    "prompt_tokens": args.prompt, "kv_cache": [36, 2, 8, max(cap, 4352), 128],
-                   "prefill_ms": round(prefill_s * 1000, 1), "qmv_sweep": sweep, "qmm_sweep": qmm,
+                   "prefill_ms": round(prefill_s * 1000, 1),
+                   "decode_step_sync_tok_s": round(args.steps / dt_sync, 2), "qmv_sweep": sweep, "qmm_sweep": qmm,
                    "speculative": spec, "qwen3_0_6b": small, "gather_qmm": moe},
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -335,6 +335,20 @@ int bmx_qwen3_decode_step(bmx_qwen3 *model, bmx_kv_cache *cache, uint32_t token,
  *   (crates/base-mlx-core/src/engine.rs:100-144, 146-153, 217-223). */
 int bmx_generate_greedy(bmx_qwen3 *model, bmx_kv_cache *cache, const uint32_t *prompt, int P, int max_new,
                         const uint32_t *eos, int n_eos, uint32_t *out, int *n_out, void *stream);
+/* The decode loop of bmx_generate_greedy alone, continuing a cache whose
+ * prefill picked `token` (the first generated token, at position seq_len):
+ * emits `token` unless it is an eos token, then decodes one token per step
+ * from the last one emitted, until an eos token (not emitted) or max_new
+ * tokens in all; out (host, max_new entries) receives them, *n_out their
+ * count, and seq_len advances by the steps taken.  Steps are queued on the
+ * stream ahead of the token being checked; on return the stream is
+ * synchronised and the cache holds exactly the steps the loop took.
+ * BMX_E_KV_CAPACITY (with *n_out tokens written) at the step that would not
+ * fit, as bmx_qwen3_decode_step would return it.
+ * Replaces: the loop of LoadedModel::generate / generate_text with
+ *   temperature 0 (crates/base-mlx-core/src/engine.rs:103-115). */
+int bmx_decode_greedy(bmx_qwen3 *model, bmx_kv_cache *cache, uint32_t token, int max_new, const uint32_t *eos,
+                      int n_eos, uint32_t *out, int *n_out, void *stream);
 /* Greedy speculative decoding with verify width spec_k (leader + spec_k-1
  * drafts; the reference fixes SPEC_K = 4).  out needs max_new entries;
  * stats (optional, 3 entries): iterations, proposed, accepted.

@@ -166,6 +166,56 @@ def test_greedy_stops_at_eos(gpu, orc):
     np.testing.assert_array_equal(g2, g[:first])
 
 
+def test_decode_greedy_queued_steps_equal_single_steps(gpu, orc):
+    """bmx_decode_greedy queues graph replays ahead of the token it checks,
+    each replay taking its token and position from the previous one on the
+    device.  Its tokens, the cache length and the K/V rows it leaves equal
+    those of bmx_qwen3_decode_step one token at a time; an eos token met with
+    replays queued past it rewinds the cache to the steps the loop took, and
+    the next loop overwrites those rows; a cache that fills up mid-loop ends
+    with the capacity error and the tokens decoded before it."""
+    gm, _ = _pair(gpu, orc, seed=8)
+    prompt = orc.fill_tokens(14, 10, SMALL["vocab"])
+    n = 40
+    ref_c = gm.new_cache(64)
+    tok = int(gm.forward(ref_c, prompt).float().argmax())
+    ref = [tok]
+    for _ in range(n - 1):
+        ref.append(gm.decode_step(ref_c, ref[-1]))
+    c = gm.new_cache(64)
+    assert int(gm.forward(c, prompt).float().argmax()) == tok
+    got = gm.decode_greedy(c, tok, n, eos=())
+    np.testing.assert_array_equal(got, ref)
+    assert c.seq_len == ref_c.seq_len == len(prompt) + n - 1
+    for layer in range(SMALL["layers"]):
+        for kv in (0, 1):
+            np.testing.assert_array_equal(c.layer_numpy(layer, kv)[:, : c.seq_len],
+                                          ref_c.layer_numpy(layer, kv)[:, : c.seq_len])
+    # eos at a token's first occurrence, the third token or later where the
+    # greedy sequence has one: `k` emitted and `k` steps kept; replays
+    # queued past the eos wrote rows the rewind drops, and continuing
+    # rewrites them
+    first = [i for i in range(1, n) if ref[i] not in ref[:i]]
+    assert first, ref  # a fixed point from the first token on
+    k = next((i for i in first if i >= 3), first[0])
+    print(f"greedy tokens {ref}; eos at {k}", flush=True)
+    c.truncate(len(prompt))
+    got = gm.decode_greedy(c, tok, n, eos=(ref[k],))
+    np.testing.assert_array_equal(got, ref[:k])
+    assert c.seq_len == len(prompt) + k
+    rest = gm.decode_greedy(c, ref[k], n - k, eos=())
+    np.testing.assert_array_equal(rest, ref[k:])
+    assert c.seq_len == ref_c.seq_len
+    # room for 6 more positions: 7 tokens, then the capacity error
+    small = gm.new_cache(len(prompt) + 6)
+    gm.forward(small, prompt)
+    with pytest.raises(gpu.BmxError) as ei:
+        gm.decode_greedy(small, tok, n, eos=())
+    assert ei.value.code == gpu.BMX_E_KV_CAPACITY
+    np.testing.assert_array_equal(ei.value.tokens, ref[:7])
+    assert small.seq_len == len(prompt) + 6
+
+
 def test_prefill_unsplit_fused_epilogues(gpu, orc):
     """A 2048-token prefill through one Qwen3-4B-shaped layer: at this size
     the o and down GEMMs run unsplit with the residual add in their epilogue
