@@ -270,6 +270,31 @@ def gather_qmm(x, w, scales, biases, rhs_indices, x_bcast=1, out=None, stream=No
     return out
 
 
+def gather_qmm_indexed(x, w, scales, biases, lhs_indices=None, rhs_indices=None, transpose=True, group_size=64,
+                       bits=4, sorted_indices=False, out=None, stream=None):
+    """mlx_ext::gather_qmm with both index arrays (mlx_ext.rs:66-117): x [B, M,
+    K] bf16 (B row blocks), w [E, N, K/8], scales / biases [E, N, K/64];
+    lhs_indices / rhs_indices [R] int32/uint32 on the device or None ->
+    [R, M, N] bf16.  Route r uses x block lhs[r] (None: r // (R // B)) and
+    expert rhs[r] (None: r, with R == E); R is the length of whichever
+    index array is given (both: equal lengths)."""
+    torch = _torch()
+    _require_cuda(x, w, scales, biases, *[t for t in (lhs_indices, rhs_indices) if t is not None])
+    E, N = w.shape[0], w.shape[1]
+    M, K = x.shape[-2], x.shape[-1]
+    B = x.numel() // (M * K)
+    lens = {t.numel() for t in (lhs_indices, rhs_indices) if t is not None}
+    if len(lens) > 1:
+        raise BmxError(BMX_E_SHAPE, f"lhs_indices and rhs_indices differ in length: {sorted(lens)}")
+    R = lens.pop() if lens else E
+    if out is None:
+        out = torch.empty(R, M, N, dtype=torch.bfloat16, device=x.device)
+    call("bmx_gather_qmm_indexed", _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), _ptr(lhs_indices),
+         _ptr(rhs_indices), _ptr(out), R, B, E, M, N, K, int(bool(transpose)), group_size, bits,
+         int(bool(sorted_indices)), _stream(stream))
+    return out
+
+
 def argmax_rows(x, stream=None):
     torch = _torch()
     _require_cuda(x)

@@ -78,6 +78,8 @@ SIGNATURES = {
     "bmx_qwen3_load": (c_int, [ctypes.c_char_p, c_int, c_p]),
     "bmx_gather_qmm": (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                c_int, c_p]),
+    "bmx_gather_qmm_indexed": (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int, c_int, c_int,
+                                       c_int, c_int, c_int, c_int, c_p]),
     "bmx_qk_norm_rope_kv_attention": (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_int, c_int, c_int, c_int,
                                               c_int, c_int, c_f, c_f, c_f, c_p, ctypes.c_size_t, c_p]),
     "bmx_argmax_rows": (c_int, [c_p, c_i64, c_i64, c_p, c_p]),

@@ -1,17 +1,20 @@
 // gather_qmm: routed (MoE expert) 4-bit affine quantized matmul, gfx950.
 //
 // Semantics restated: mlx_ext::gather_qmm(x, w, scales, biases,
-// lhs_indices = None, rhs_indices, transpose = true, 64, 4, sorted = false)
-// (crates/base-mlx-core/src/mlx_ext.rs:66-117) as QSwitchLinear::forward
-// calls it for the experts of SwitchGlu (crates/base-mlx-core/src/model/
-// granite.rs:74-88, 181-201): W, s, b stack E experts ([E, N, K/8] u32,
-// [E, N, K/64] bf16), and route r -- one (token, top-k slot) pair of the
-// index array -- computes
-//   y[r] = x[r / x_bcast] . W[rhs[r]]^T          ([M, K] x [K, N] -> [M, N])
+// lhs_indices, rhs_indices, transpose = true, 64, 4, sorted_indices)
+// (crates/base-mlx-core/src/mlx_ext.rs:66-117), as QSwitchLinear::forward
+// calls it for the experts of SwitchGlu with lhs_indices = None (crates/
+// base-mlx-core/src/model/granite.rs:74-88, 181-201): W, s, b stack E
+// experts ([E, N, K/8] u32, [E, N, K/64] bf16), and route r -- one (token,
+// top-k slot) pair of the index array -- computes
+//   y[r] = x[lhs(r)] . W[rhs(r)]^T               ([M, K] x [K, N] -> [M, N])
 // with quantized_matmul's group decomposition, fp32 accumulation and a bf16
-// result.  x_bcast is MLX's broadcast of x over the top-k axis: top_k for
-// the gate/up projection, whose x [T, 1, 1, K] every slot of a token shares,
-// 1 for the down projection, which has one input row block per route.
+// result.  lhs(r) = lhs_indices[r] when given, else r / x_bcast: MLX's
+// broadcast of x over the top-k axis (top_k for the gate/up projection,
+// whose x [T, 1, 1, K] every slot of a token shares; 1 for the down
+// projection, which has one input row block per route).  rhs(r) =
+// rhs_indices[r] when given, else r.  sorted_indices only tells MLX the
+// routes come grouped by expert; results do not depend on it.
 //
 // Work decomposition: a workgroup of 4 waves owns RB consecutive output
 // rows of one route (grid = row tiles x routes); the expert id is read on
@@ -33,14 +36,15 @@ constexpr int kGMaxNG = 8;    // groups per lane
 constexpr int kGMaxM = 8;     // rows of x per route
 
 struct GatherParams {
-  const uint16_t* x;    // route r: rows [M, K] at x + (r / x_bcast) * x_rstride
+  const uint16_t* x;    // route r: rows [M, K] at x + lhs(r) * x_rstride
   const uint32_t* w;    // [E, N, K/8]
   const uint16_t* s;    // [E, N, K/64]
   const uint16_t* b;    // [E, N, K/64]
-  const uint32_t* rhs;  // [R] expert of each route
+  const uint32_t* lhs;  // [R] x block of each route, or null: r / x_bcast
+  const uint32_t* rhs;  // [R] expert of each route, or null: r
   uint16_t* y;          // route r: rows [M, N] at y + r * y_rstride
   int64_t x_rstride, y_rstride;
-  int x_bcast, E, M, N, K;
+  int x_bcast, nxb, E, M, N, K;  // nxb: x blocks
   int S;                // lanes per output row (power of two, 1..64)
 };
 
@@ -54,9 +58,11 @@ __global__ void __launch_bounds__(kGThreads) gather_qmv_kernel(const GatherParam
   const int slots = 64 >> lshift;
   const int rb = 4 * slots;
   const int route = blockIdx.y;
-  // out-of-range expert ids are clamped (a valid address for every route)
-  const int64_t e = min(p.rhs[route], static_cast<uint32_t>(p.E - 1));
-  const uint16_t* xr = p.x + static_cast<int64_t>(route / p.x_bcast) * p.x_rstride;
+  // out-of-range expert and x block ids are clamped (a valid address for
+  // every route)
+  const int64_t e = min(p.rhs ? p.rhs[route] : static_cast<uint32_t>(route), static_cast<uint32_t>(p.E - 1));
+  const int64_t xb = p.lhs ? min(p.lhs[route], static_cast<uint32_t>(p.nxb - 1)) : route / p.x_bcast;
+  const uint16_t* xr = p.x + xb * p.x_rstride;
   const int row = blockIdx.x * rb + wave * slots + slot;
   const int64_t rr = min(row, p.N - 1);
   const uint32_t* wrow = p.w + (e * p.N + rr) * (K / 8);
@@ -146,11 +152,12 @@ __global__ void __launch_bounds__(kGThreads) gather_qmv_kernel(const GatherParam
 }  // namespace
 
 int launch_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
-                      const uint32_t* rhs, uint16_t* y, int R, int x_bcast, int64_t x_rstride, int64_t y_rstride,
-                      int E, int M, int N, int K, hipStream_t stream) {
+                      const uint32_t* lhs, const uint32_t* rhs, uint16_t* y, int R, int x_bcast, int nxb,
+                      int64_t x_rstride, int64_t y_rstride, int E, int M, int N, int K, hipStream_t stream) {
   if (R == 0) return BMX_OK;
-  if (R < 0 || R > 65535 || E <= 0 || M <= 0 || N <= 0 || K <= 0 || x_bcast <= 0)
-    return set_error(BMX_E_SHAPE, "gather_qmm: bad sizes R=%d E=%d M=%d N=%d K=%d x_bcast=%d", R, E, M, N, K, x_bcast);
+  if (R < 0 || R > 65535 || E <= 0 || M <= 0 || N <= 0 || K <= 0 || x_bcast <= 0 || nxb <= 0)
+    return set_error(BMX_E_SHAPE, "gather_qmm: bad sizes R=%d E=%d M=%d N=%d K=%d x_bcast=%d x blocks=%d", R, E, M,
+                     N, K, x_bcast, nxb);
   if (K % 64) return set_error(BMX_E_SHAPE, "gather_qmm: K=%d not a multiple of the group size 64", K);
   if (M > kGMaxM) return set_error(BMX_E_UNSUPPORTED, "gather_qmm: M=%d rows per route (at most %d)", M, kGMaxM);
   const int G = K / 64;
@@ -167,7 +174,7 @@ int launch_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, c
   const size_t lds = static_cast<size_t>(mt) * (K / 32) * (kGChunk + 4);
   if (lds > 160 * 1024) return set_error(BMX_E_UNSUPPORTED, "gather_qmm: M*K=%d too large", M * K);
   const int rb = 4 * (64 / S);
-  GatherParams p{x, w, s, b, rhs, y, x_rstride, y_rstride, x_bcast, E, M, N, K, S};
+  GatherParams p{x, w, s, b, lhs, rhs, y, x_rstride, y_rstride, x_bcast, nxb, E, M, N, K, S};
   const dim3 grid((N + rb - 1) / rb, R);
   const void* kern = mt == 1   ? reinterpret_cast<const void*>(gather_qmv_kernel<1>)
                      : mt == 2 ? reinterpret_cast<const void*>(gather_qmv_kernel<2>)
@@ -197,7 +204,33 @@ extern "C" int bmx_gather_qmm(const bmx_bf16* x, const uint32_t* w, const bmx_bf
     return set_error(BMX_E_UNSUPPORTED, "gather_qmm: only bits=4, group_size=64 (got %d, %d)", bits, group_size);
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15)
     return set_error(BMX_E_ALIGN, "gather_qmm: x and w must be 16-byte aligned");
-  return launch_gather_qmm(x, w, scales, biases, rhs_indices, out, n_routes, x_bcast,
+  const int nxb = x_bcast > 0 ? (n_routes + x_bcast - 1) / x_bcast : 0;  // x blocks the routes read
+  return launch_gather_qmm(x, w, scales, biases, nullptr, rhs_indices, out, n_routes, x_bcast, nxb,
+                           static_cast<int64_t>(M) * K, static_cast<int64_t>(M) * N, n_experts, M, N, K,
+                           as_stream(stream));
+}
+
+extern "C" int bmx_gather_qmm_indexed(const bmx_bf16* x, const uint32_t* w, const bmx_bf16* scales,
+                                      const bmx_bf16* biases, const uint32_t* lhs_indices,
+                                      const uint32_t* rhs_indices, bmx_bf16* out, int n_routes, int n_x_blocks,
+                                      int n_experts, int M, int N, int K, int transpose, int group_size, int bits,
+                                      int sorted_indices, void* stream) {
+  (void)sorted_indices;  // a grouping hint in MLX; the results do not depend on it
+  if (!x || !w || !scales || !biases || !out) return set_error(BMX_E_ARG, "gather_qmm: null pointer");
+  if (!transpose) return set_error(BMX_E_UNSUPPORTED, "gather_qmm: transpose=false is not supported");
+  if (bits != 4 || group_size != 64)
+    return set_error(BMX_E_UNSUPPORTED, "gather_qmm: only bits=4, group_size=64 (got %d, %d)", bits, group_size);
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15)
+    return set_error(BMX_E_ALIGN, "gather_qmm: x and w must be 16-byte aligned");
+  if (n_x_blocks <= 0 || n_routes < 0) return set_error(BMX_E_SHAPE, "gather_qmm: %d x blocks", n_x_blocks);
+  // without lhs_indices the x blocks broadcast evenly over the routes
+  if (!lhs_indices && n_routes % n_x_blocks)
+    return set_error(BMX_E_SHAPE, "gather_qmm: %d routes over %d x blocks without lhs_indices", n_routes, n_x_blocks);
+  // without rhs_indices route r uses expert r
+  if (!rhs_indices && n_routes != n_experts)
+    return set_error(BMX_E_SHAPE, "gather_qmm: %d routes and %d experts without rhs_indices", n_routes, n_experts);
+  const int x_bcast = lhs_indices || n_routes == 0 ? 1 : n_routes / n_x_blocks;
+  return launch_gather_qmm(x, w, scales, biases, lhs_indices, rhs_indices, out, n_routes, x_bcast, n_x_blocks,
                            static_cast<int64_t>(M) * K, static_cast<int64_t>(M) * N, n_experts, M, N, K,
                            as_stream(stream));
 }

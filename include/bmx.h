@@ -122,6 +122,24 @@ int bmx_qmatmul_affine_noalloc(const bmx_bf16 *x, const uint32_t *w, const bmx_b
 int bmx_gather_qmm(const bmx_bf16 *x, const uint32_t *w, const bmx_bf16 *scales, const bmx_bf16 *biases,
                    const uint32_t *rhs_indices, bmx_bf16 *out, int n_routes, int x_bcast, int n_experts, int M,
                    int N, int K, int group_size, int bits, void *stream);
+/* bmx_gather_qmm with mlx_gather_qmm's whole argument list: for route
+ * r < n_routes,
+ *   out[r] [M, N] = x[lhs(r)] [M, K] . W[rhs(r)]^T
+ * x holds n_x_blocks row blocks of [M, K].  lhs(r) = lhs_indices[r] (device
+ * uint32; ids >= n_x_blocks are clamped to n_x_blocks - 1), or, with
+ * lhs_indices NULL, r / (n_routes / n_x_blocks) (n_x_blocks must divide
+ * n_routes).  rhs(r) = rhs_indices[r] (device uint32; ids >= n_experts are
+ * clamped to n_experts - 1), or, with rhs_indices NULL, r (n_routes must
+ * equal n_experts).  transpose must be 1 (BMX_E_UNSUPPORTED otherwise);
+ * sorted_indices only says the routes come grouped by expert and does not
+ * change the results.  Other limits as bmx_gather_qmm.
+ * Replaces: mlx_ext::gather_qmm(x, w, scales, biases, lhs_indices,
+ *   rhs_indices, transpose, group_size, bits, sorted_indices)
+ *   (crates/base-mlx-core/src/mlx_ext.rs:66-117). */
+int bmx_gather_qmm_indexed(const bmx_bf16 *x, const uint32_t *w, const bmx_bf16 *scales, const bmx_bf16 *biases,
+                           const uint32_t *lhs_indices, const uint32_t *rhs_indices, bmx_bf16 *out, int n_routes,
+                           int n_x_blocks, int n_experts, int M, int N, int K, int transpose, int group_size,
+                           int bits, int sorted_indices, void *stream);
 
 /* out[N,K] = scales * q + biases (fp32, rounded to bf16).
  * Replaces: mlx_rs::ops::dequantize(w, s, b, group_size, bits)

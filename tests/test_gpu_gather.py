@@ -81,3 +81,55 @@ def test_gather_qmm_errors(gpu):
     with pytest.raises(gpu.BmxError) as ei:  # 9 rows of x per route
         gpu.gather_qmm(x, w, s, s, idx)
     assert ei.value.code == gpu.BMX_E_UNSUPPORTED
+
+
+def test_gather_qmm_indexed_lhs_and_rhs(gpu, orc):
+    """mlx_gather_qmm with both index arrays: route r multiplies x block
+    lhs[r] (repeated, permuted and one out-of-range id, clamped to the last
+    block) by expert rhs[r]; checked against the oracle run on the x blocks
+    gathered on the host."""
+    import torch
+
+    E, N, K, M, B, R = 6, 320, 1536, 2, 5, 9
+    print(f"gather_qmm_indexed E={E} N={N} K={K} M={M} x blocks={B} R={R}", flush=True)
+    (w, s, b), (wq, sq, bq) = _experts(gpu, orc, 4000, E, N, K)
+    rng = np.random.default_rng(17)
+    lhs = rng.integers(0, B, R).astype(np.uint32)
+    lhs[2] = B + 3  # clamped to B - 1
+    rhs = rng.integers(0, E, R).astype(np.uint32)
+    x = gpu.fill_normal_bf16(4100, (B, M, K))
+    dev = lambda a: torch.from_numpy(a.view(np.int32)).cuda()  # noqa: E731
+    y = gpu.gather_qmm_indexed(x, w, s, b, dev(lhs), dev(rhs), sorted_indices=True)
+    torch.cuda.synchronize()
+    xg = torch_bf16_bits(x)[np.minimum(lhs, B - 1)]
+    ref = orc.gather_qmm(xg, wq, sq, bq, rhs, 1)
+    assert _close(torch_bf16_bits(y), ref) > 0.999
+    # without lhs_indices the x blocks broadcast over the routes: the same
+    # bits as bmx_gather_qmm with x_bcast = R / B
+    x3 = gpu.fill_normal_bf16(4200, (3, M, K))
+    rhs6 = dev(rng.integers(0, E, 6).astype(np.uint32))
+    a = gpu.gather_qmm_indexed(x3, w, s, b, None, rhs6)
+    c = gpu.gather_qmm(x3, w, s, b, rhs6, x_bcast=2)
+    # without rhs_indices route r uses expert r (R = E)
+    x6 = gpu.fill_normal_bf16(4300, (E, M, K))
+    d = gpu.gather_qmm_indexed(x6, w, s, b, None, None)
+    e = gpu.gather_qmm(x6, w, s, b, dev(np.arange(E, dtype=np.uint32)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(torch_bf16_bits(a), torch_bf16_bits(c))
+    np.testing.assert_array_equal(torch_bf16_bits(d), torch_bf16_bits(e))
+
+
+def test_gather_qmm_indexed_errors(gpu):
+    import torch
+
+    w = torch.zeros(2, 16, 8, dtype=torch.int32, device="cuda")
+    s = torch.zeros(2, 16, 1, dtype=torch.bfloat16, device="cuda")
+    x = torch.zeros(3, 1, 64, dtype=torch.bfloat16, device="cuda")
+    idx = torch.zeros(4, dtype=torch.int32, device="cuda")
+    cases = [(dict(lhs_indices=idx, rhs_indices=idx, transpose=False), gpu.BMX_E_UNSUPPORTED),
+             (dict(lhs_indices=None, rhs_indices=idx), gpu.BMX_E_SHAPE),  # 4 routes over 3 x blocks
+             (dict(lhs_indices=idx, rhs_indices=None), gpu.BMX_E_SHAPE)]  # 4 routes, 2 experts
+    for kw, code in cases:
+        with pytest.raises(gpu.BmxError) as ei:
+            gpu.gather_qmm_indexed(x, w, s, s, **kw)
+        assert ei.value.code == code, kw
