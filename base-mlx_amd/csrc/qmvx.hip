@@ -52,7 +52,7 @@ bool split_shape(int total_tiles, int G, Shape* sh) {
 size_t shape_lds(int mt, int nh, const Shape& sh) {
   const int RW = 16 * sh.TB;
   return static_cast<size_t>(mt) * (sh.KC * 8 + 1) * 16 + static_cast<size_t>(sh.KC) * 16 * 4 +
-         2ull * nh * RW * sb_stride(sh.KC) * 2 + static_cast<size_t>(kWaves) * nh * 4 * 64 * 4 +
+         2ull * nh * RW * sb_stride(sh.KC) * 4 + static_cast<size_t>(kWaves) * nh * 4 * 64 * 4 +
          static_cast<size_t>(kWaves + 1) * mt * 4;
 }
 
@@ -168,7 +168,7 @@ int try_launch_qmvx(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   sh.npc = (KC / 2 + SK - 1) / SK;
   if (sh.npc > np_max) return kNoFit;
   const int RW = 16 * sh.TB;
-  if (nh * 2 * RW * (KC / 8) > kSBU * kThreads) return kNoFit;
+  if (nh * RW * (KC / 8) > kThreads) return kNoFit;  // one s|b unit pair per thread
   // tile-sets; segments start on tile-set boundaries
   if (epi == QMV_SWIGLU) {
     sh.nts = tile_sets(sh.TB);

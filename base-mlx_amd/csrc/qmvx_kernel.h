@@ -13,7 +13,7 @@
 // is multiplied M times.  Here the nibbles are unpacked once and the
 // products run on v_mfma_f32_16x16x32_bf16 -- for every row count, so that
 // one row's arithmetic never depends on how many rows share the launch:
-//   A = x (16 rows, rows >= M are zeros): lane l holds x row l%16 and k
+//   A = x (16 rows; rows >= M are never stored): lane l holds x row l%16 and k
 //       slice l/16 of the 32-wide step, from LDS;
 //   B = W^T: lane l holds W row n = l%16 of a 16-row tile.  W is read 16
 //       bytes per lane, a pair of groups per load: lane quarter q = l/16
@@ -60,7 +60,6 @@ namespace qmvx {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kXU = 12;      // x units (8 values) per thread per chunk: chunk <= 6144 units (96 KB)
-constexpr int kSBU = 2;      // s|b 16-byte units per thread per step (SbRegs v0, v1)
 constexpr int kMaxKC = 128;      // groups in a single chunk
 constexpr int kMaxChunkKC = 64;  // groups per chunk when K needs several
 
@@ -72,11 +71,11 @@ struct Shape {
   int nts;     // tile-sets
 };
 
-// LDS row stride (halfwords) of the s and b tiles of a step, [RW rows][KC
-// groups]: 16-byte aligned rows whose stride in 16-byte units is odd, so
+// LDS row stride (floats) of the s and b - 128 s tiles of a step, [RW rows]
+// [KC groups]: 16-byte aligned rows whose stride in 16-byte units is odd, so
 // that the 16 rows of a tile, read at one group, fall in 16 different banks
 // (KC = 64 unpadded put all of them in one bank)
-__host__ __device__ inline int sb_stride(int KC) { return KC + ((KC / 8) % 2 == 0 ? 8 : 0); }
+__host__ __device__ inline int sb_stride(int KC) { return KC + ((KC / 4) % 2 == 0 ? 4 : 0); }
 
 // Modes: the whole K in one chunk; several chunks walked by each workgroup
 // per tile-set (x restaged per step); K split over workgroups, one chunk
@@ -114,7 +113,8 @@ struct WRegs {
   u32x4 w[NP][NH];
 };
 
-// staging registers of a step: s|b units, x chunk units and norm weight units
+// staging registers of a step: the s and the b unit of one row and 8 groups,
+// x chunk units and norm weight units
 struct SbRegs {
   uint4 v0, v1;
 };
@@ -138,9 +138,9 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
   uint4* xs = reinterpret_cast<uint4*>(smem);                 // [MT][XS]
   float* sxs = reinterpret_cast<float*>(xs + MT * XS);        // [KC][16]
   const int SBS = sb_stride(KC);
-  uint16_t* ss = reinterpret_cast<uint16_t*>(sxs + KC * 16);  // [NH][RW][SBS]
-  uint16_t* bs = ss + NH * RW * SBS;                          // [NH][RW][SBS]
-  float* red = reinterpret_cast<float*>(bs + NH * RW * SBS);  // [kWaves][NH][4][64]
+  float* ss = sxs + KC * 16;                                  // [NH][RW][SBS] s
+  float* bs = ss + NH * RW * SBS;                             // [NH][RW][SBS] b - 128 s
+  float* red = bs + NH * RW * SBS;                            // [kWaves][NH][4][64]
   float* nred = red + kWaves * NH * 4 * 64;                   // [kWaves + 1][MT]: sums of squares, 1 / rms
   const bool has_norm = p.norm_w != nullptr;
   const int grid = static_cast<int>(gridDim.x);
@@ -158,20 +158,19 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
     return sg;
   };
 
-  // ---- s|b of a step: 16-byte units, [NH][s|b][RW rows][KC/8 units] ----
+  // ---- s|b of a step: a thread loads the s and the b unit (8 groups) of
+  // one (matrix, row, unit) of [NH][RW rows][KC/8 units] and stages s and
+  // b - 128 s as fp32, once per row and group instead of once per lane ----
   const int KCU = KC / 8;
-  const int sb_total = NH * 2 * RW * KCU;
-  int sb_u[kSBU], sb_r[kSBU], sb_hs[kSBU];
+  const int sb_total = NH * RW * KCU;  // at most kThreads (checked by the planner)
+  int sb_u, sb_r, sb_h;
   {
     const float rcp_kcu = 1.0f / static_cast<float>(KCU), rcp_rw = 1.0f / static_cast<float>(RW);
-#pragma unroll
-    for (int i = 0; i < kSBU; i++) {
-      const int e = min(i * kThreads + static_cast<int>(threadIdx.x), sb_total - 1);
-      const int ru = udiv_small(e, rcp_kcu);
-      sb_u[i] = e - ru * KCU;
-      sb_hs[i] = udiv_small(ru, rcp_rw);
-      sb_r[i] = ru - sb_hs[i] * RW;
-    }
+    const int e = min(static_cast<int>(threadIdx.x), sb_total - 1);
+    const int ru = udiv_small(e, rcp_kcu);
+    sb_u = e - ru * KCU;
+    sb_h = udiv_small(ru, rcp_rw);
+    sb_r = ru - sb_h * RW;
   }
   auto issue_sb = [&](int ts, int kc, SbRegs& sbr) {
     const int sg = seg_of(ts);
@@ -187,26 +186,34 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
     const uint16_t* s0b = s0.b;
     const uint16_t* s1s = s1.s;
     const uint16_t* s1b = s1.b;
-    auto one = [&](int i) {
-      const int hs = sb_hs[i];
-      const uint16_t* base = (hs & 1) ? s0b : s0s;
-      if constexpr (NH == 2) base = hs >= 2 ? ((hs & 1) ? s1b : s1s) : base;
-      const int64_t row = min(row0 + sb_r[i], rows - 1);
-      return *reinterpret_cast<const uint4*>(base + row * G + g0 + min(sb_u[i], ku - 1) * 8);
-    };
-    sbr.v0 = one(0);
-    sbr.v1 = one(1);
+    const uint16_t* sp = s0s;
+    const uint16_t* bp = s0b;
+    if constexpr (NH == 2) {
+      sp = sb_h ? s1s : s0s;
+      bp = sb_h ? s1b : s0b;
+    }
+    const int64_t off = min(row0 + sb_r, rows - 1) * static_cast<int64_t>(G) + g0 + min(sb_u, ku - 1) * 8;
+    sbr.v0 = *reinterpret_cast<const uint4*>(sp + off);
+    sbr.v1 = *reinterpret_cast<const uint4*>(bp + off);
   };
   auto store_sb = [&](const SbRegs& sbr) {
-    auto one = [&](int i, const uint4& v) {
-      if (i * kThreads + static_cast<int>(threadIdx.x) < sb_total) {
-        const int hs = sb_hs[i];
-        uint16_t* dst = ((hs & 1) ? bs : ss) + ((hs >> 1) * RW + sb_r[i]) * SBS + sb_u[i] * 8;
-        *reinterpret_cast<uint4*>(dst) = v;
+    if (static_cast<int>(threadIdx.x) < sb_total) {
+      const uint32_t sw[4] = {sbr.v0.x, sbr.v0.y, sbr.v0.z, sbr.v0.w};
+      const uint32_t bw[4] = {sbr.v1.x, sbr.v1.y, sbr.v1.z, sbr.v1.w};
+      float sf[8], bf[8];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        sf[2 * k] = bf2f(sw[k] & 0xffffu);
+        sf[2 * k + 1] = bf2f(sw[k] >> 16);
+        bf[2 * k] = __builtin_fmaf(-128.0f, sf[2 * k], bf2f(bw[k] & 0xffffu));
+        bf[2 * k + 1] = __builtin_fmaf(-128.0f, sf[2 * k + 1], bf2f(bw[k] >> 16));
       }
-    };
-    one(0, sbr.v0);
-    one(1, sbr.v1);
+      const int o = (sb_h * RW + sb_r) * SBS + sb_u * 8;
+      *reinterpret_cast<float4*>(ss + o) = make_float4(sf[0], sf[1], sf[2], sf[3]);
+      *reinterpret_cast<float4*>(ss + o + 4) = make_float4(sf[4], sf[5], sf[6], sf[7]);
+      *reinterpret_cast<float4*>(bs + o) = make_float4(bf[0], bf[1], bf[2], bf[3]);
+      *reinterpret_cast<float4*>(bs + o + 4) = make_float4(bf[4], bf[5], bf[6], bf[7]);
+    }
   };
 
   // ---- W of one step: NP group pairs x NH matrices, 16 bytes per lane each ----
@@ -346,10 +353,12 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
   f32x4_t acc[NH];
 #pragma unroll
   for (int h = 0; h < NH; h++) acc[h] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  // A row l%16 is x row l%16 for l%16 < MT; the lanes of rows MT..15 read
+  // row 0 again: each row of the product depends on its own A row only, and
+  // rows >= M are never stored, so they need not be zeros
   const int xm = n_l < MT ? n_l : 0;
   const NibbleK nk = nibble_consts();
   const int pq = ((q & 1) << 1) | (q >> 1);  // this lane's word pair in a group after the swap
-  const uint32_t keep = n_l < MT ? 0xffffffffu : 0u;  // A rows >= MT are zeros
 
   // pf: whether a next step exists (its loads are issued before this step's
   // products); the workgroup's last step issues none
@@ -401,9 +410,7 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
           const int gl = 2 * pl + e;
           const uint4 v0 = xs[xm * XS + gl * 8 + 2 * pq];
           const uint4 v1 = xs[xm * XS + gl * 8 + 2 * pq + 1];
-          const uint4 a0u = make_uint4(v0.x & keep, v0.y & keep, v0.z & keep, v0.w & keep);
-          const uint4 a1u = make_uint4(v1.x & keep, v1.y & keep, v1.z & keep, v1.w & keep);
-          const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, a0u), a1 = __builtin_bit_cast(bf16x8_t, a1u);
+          const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, v0), a1 = __builtin_bit_cast(bf16x8_t, v1);
           const f32x4_t sx = *reinterpret_cast<const f32x4_t*>(sxs + gl * 16 + 4 * q);
 #pragma unroll
           for (int h = 0; h < NH; h++) {
@@ -411,8 +418,8 @@ __global__ void __launch_bounds__(kThreads) qmvx_kernel(const QmvParams p, const
             d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, nibbles_bf16(wv[h][2 * e], nk), d, 0, 0, 0);
             d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, nibbles_bf16(wv[h][2 * e + 1], nk), d, 0, 0, 0);
             const int so = (h * RW + tile * 16 + n_l) * SBS + gl;
-            const float sv = bf2f(ss[so]);
-            const float bb = __builtin_fmaf(-128.0f, sv, bf2f(bs[so]));
+            const float sv = ss[so];
+            const float bb = bs[so];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
               acc[h][r] = __builtin_fmaf(sv, d[r], acc[h][r]);
