@@ -130,7 +130,7 @@ __device__ __forceinline__ void store_pair(const AttnParams& p, int wid, int lan
 
 // Decode / short verify (R = tokens x heads-per-kv-head query rows of one kv
 // head, up to 64).  A workgroup of 8 waves owns one kv head, one tile of
-// RMAX <= 16 of those rows and 256 keys, 32 per wave.  Every K, V and q load
+// RMAX <= 8 of those rows and 256 keys, 32 per wave.  Every K, V and q load
 // of a wave is issued before any arithmetic:
 //   QK on MFMA (v_mfma_f32_16x16x32_bf16): A = the tile's query rows (padded
 //     to 16; lane l holds row l%16, dims 32*ks + 8*(l/16), 4 fragments; the
@@ -769,7 +769,11 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   if (!ws || R > kDecMaxRows || (fuse && M > kFuseMaxM)) return kNoFit;
   if (ws_floats < kCounters) return kNoFit;
   const int max_ns = static_cast<int>((ws_floats - kCounters) / (static_cast<size_t>(Hq) * M * (kD + 2)));
-  const int rmax = R <= 4 ? 4 : R <= 8 ? 8 : 16;
+  // row tiles of 4 (decode: up to 4 q heads per kv head) or 8 rows; a
+  // 16-row tile (half the workgroups for R > 8, each re-reading K and V
+  // fewer times, but twice the PV registers and work per wave) measured
+  // slower: 32B-shape verify step 9.53 against 9.26 ms with 8-row tiles
+  const int rmax = R <= 4 ? 4 : 8;
   const int tiles = (R + rmax - 1) / rmax;
   // 256 keys per split (one per wave of 32 keys).  Smaller splits to spread
   // a 4K context over all 256 CUs measured slower: the K / V stream is
@@ -798,10 +802,8 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   } while (0)
   if (rmax == 4)
     BMX_DECODE_LAUNCH(4);
-  else if (rmax == 8)
-    BMX_DECODE_LAUNCH(8);
   else
-    BMX_DECODE_LAUNCH(16);
+    BMX_DECODE_LAUNCH(8);
 #undef BMX_DECODE_LAUNCH
   return check_launch(fuse ? "attention_decode_fused" : "attention_decode");
 }
