@@ -772,7 +772,8 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   // row tiles of 4 (decode: up to 4 q heads per kv head) or 8 rows; a
   // 16-row tile (half the workgroups for R > 8, each re-reading K and V
   // fewer times, but twice the PV registers and work per wave) measured
-  // slower: 32B-shape verify step 9.53 against 9.26 ms with 8-row tiles
+  // slower: 32B-shape verify step 9.53 against 9.26 ms with 8-row tiles;
+  // 4-row tiles throughout, 9.41 ms
   const int rmax = R <= 4 ? 4 : 8;
   const int tiles = (R + rmax - 1) / rmax;
   // 256 keys per split (one per wave of 32 keys).  Smaller splits to spread
