@@ -77,6 +77,8 @@ using namespace bmx;
 constexpr int kRing = 64;
 constexpr int kAhead = 3;
 constexpr uint32_t kRingEmpty = 0xffffffffu;
+// verify width of speculative decoding (leader + drafts), at most
+constexpr int kMaxSpecK = 8;
 
 struct bmx_kv_cache {
   uint64_t id = 0;  // unique per cache: keys the captured decode graph
@@ -98,6 +100,7 @@ struct bmx_qwen3 {
   // workspace (rows = max_tokens)
   uint16_t *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *att = nullptr,
            *o = nullptr, *g = nullptr, *u = nullptr, *a = nullptr, *logits1 = nullptr;
+  uint16_t* vlogits = nullptr;  // [kMaxSpecK, vocab]: a speculative verify forward's logits
   float* attn_ws = nullptr;
   size_t attn_ws_floats = 0;
   float* qmm_ws = nullptr;  // split-K partials of the prefill GEMMs (per model: models on
@@ -431,6 +434,7 @@ int qwen3_alloc(const bmx_qwen3_config* cfg, int max_tokens, bmx_qwen3** out) {
   if (!rc) rc = dalloc_t(m, &m->u, T * I);
   if (!rc) rc = dalloc_t(m, &m->a, T * I);
   if (!rc) rc = dalloc_t(m, &m->logits1, static_cast<size_t>(cfg->vocab));
+  if (!rc) rc = dalloc_t(m, &m->vlogits, static_cast<size_t>(kMaxSpecK) * cfg->vocab);
   // attention split partials: 256 splits of 256 keys for decode (65536
   // cached positions), 64 for verify forwards of up to 16 tokens
   m->attn_ws_floats = std::max(attention_workspace_floats(cfg->n_heads, 1, 256),
@@ -818,7 +822,8 @@ extern "C" int bmx_speculative_generate(bmx_qwen3* target, bmx_kv_cache* tc, bmx
   if (draft->cfg.vocab != target->cfg.vocab)  // check_compatible, speculative.rs:40-54
     return set_error(BMX_E_ARG, "draft/target vocab mismatch: target=%d draft=%d", target->cfg.vocab, draft->cfg.vocab);
   if (P <= 0 || max_new <= 0) return set_error(BMX_E_ARG, "speculative: P=%d max_new=%d", P, max_new);
-  if (spec_k < 2 || spec_k > 8) return set_error(BMX_E_ARG, "speculative: spec_k=%d outside 2..8", spec_k);
+  if (spec_k < 2 || spec_k > kMaxSpecK)
+    return set_error(BMX_E_ARG, "speculative: spec_k=%d outside 2..%d", spec_k, kMaxSpecK);
   if (spec_k > target->max_tokens) return set_error(BMX_E_SHAPE, "speculative: spec_k > target max_tokens");
   // the caches may already hold context (a continued conversation): every
   // rewind below is relative to where each one starts
@@ -827,11 +832,7 @@ extern "C" int bmx_speculative_generate(bmx_qwen3* target, bmx_kv_cache* tc, bmx
   int64_t iters = 0, proposed = 0, accepted = 0;
   int n = 0, rc = BMX_OK;
   uint32_t leader = 0, dnext = 0;
-  uint16_t* tlog = nullptr;
-  // target verify logits: [spec_k, vocab]
-  if ((rc = check_hip(hipMalloc(reinterpret_cast<void**>(&tlog), static_cast<size_t>(spec_k) * target->cfg.vocab * 2),
-                      "verify logits")))
-    return rc;
+  uint16_t* const tlog = target->vlogits;  // the verify rows' logits: [spec_k, vocab]
   // prefill both (speculative.rs:75-79): only the target's last row is used
   // and the draft's logits are discarded, so only those rows are computed
   {
@@ -901,6 +902,5 @@ done:
     stats[1] = proposed;
     stats[2] = accepted;
   }
-  (void)hipFree(tlog);
   return rc;
 }
