@@ -435,10 +435,12 @@ int qwen3_alloc(const bmx_qwen3_config* cfg, int max_tokens, bmx_qwen3** out) {
   if (!rc) rc = dalloc_t(m, &m->a, T * I);
   if (!rc) rc = dalloc_t(m, &m->logits1, static_cast<size_t>(cfg->vocab));
   if (!rc) rc = dalloc_t(m, &m->vlogits, static_cast<size_t>(kMaxSpecK) * cfg->vocab);
-  // attention split partials: 256 splits of 256 keys for decode (65536
-  // cached positions), 64 for verify forwards of up to 16 tokens
-  m->attn_ws_floats = std::max(attention_workspace_floats(cfg->n_heads, 1, 256),
-                               attention_workspace_floats(cfg->n_heads, 16, 64));
+  // attention split partials: 256 splits of 256 keys (65536 cached
+  // positions) for every forward of up to 16 tokens, so that a verify row
+  // takes the split-key path exactly where a decode step does and the two
+  // stay bit-identical at any context a decode step covers (Hq * 16 * 256
+  // * 130 floats: 68 MB at 32 query heads)
+  m->attn_ws_floats = attention_workspace_floats(cfg->n_heads, 16, 256);
   if (!rc) rc = dalloc_t(m, &m->attn_ws, m->attn_ws_floats);
   // the arrival counters at its head start at zero (and every call leaves them so)
   if (!rc) rc = check_hip(hipMemsetAsync(m->attn_ws, 0, m->attn_ws_floats * sizeof(float), st), "hipMemsetAsync");

@@ -6,7 +6,10 @@ spread fp32 summation order alone causes through the layers: the floor no
 implementation can be held below), plus greedy top-1 agreement.  The bar:
 every position within max(E2E_TOL, FLOOR_FACTOR x the largest floor);
 exact agreement on every position whose oracle top-2 margin is far above
-the measured spread (decided positions, not near-ties); and, over at least
+the measured spread and above the bf16 resolution of the top logit
+(decided positions, not near-ties: two logits a couple of bf16 steps apart
+can round to one value, where the argmax's first-index rule decides); and,
+over at least
 MIN_POSITIONS positions, top-1 agreement of at least min(E2E_TOP1, the
 reordered oracle's own agreement), less two standard deviations of the
 oracle's own flip count (flips are coin tosses at near-ties).  The
@@ -21,6 +24,7 @@ E2E_TOL = 2e-2       # north-star logits bar (L2 relative)
 E2E_TOP1 = 0.99      # north-star greedy top-1 agreement
 FLOOR_FACTOR = 1.5   # GPU spread allowed over the oracle's own reordering spread
 MIN_POSITIONS = 64   # positions for the aggregate top-1 bar
+BF16_STEPS = 4       # a decided position's oracle top-2 gap exceeds this many bf16 steps of its top logit
 
 
 def _f32(bits):
@@ -33,7 +37,7 @@ class Parity:
 
     def __init__(self, name):
         self.name = name
-        self.err, self.floor, self.agree, self.agree_floor, self.margin = [], [], [], [], []
+        self.err, self.floor, self.agree, self.agree_floor, self.margin, self.resolved = [], [], [], [], [], []
 
     def add(self, g_bits, o_bits, r_bits):
         g = _f32(g_bits).reshape(-1, o_bits.shape[-1])
@@ -46,6 +50,9 @@ class Parity:
             self.agree_floor.append(int(np.argmax(ri) == np.argmax(oi)))
             top2 = np.partition(oi, -2)[-2:]
             self.margin.append(float((top2[1] - top2[0]) / (np.linalg.norm(oi) / np.sqrt(oi.size))))
+            # bf16 spacing at the top logit: 2^(exponent - 7)
+            ulp = 2.0 ** (np.floor(np.log2(max(abs(top2[1]), 1e-30))) - 7)
+            self.resolved.append(bool(top2[1] - top2[0] > BF16_STEPS * ulp))
 
     def check(self):
         err, floor = np.array(self.err), np.array(self.floor)
@@ -53,7 +60,7 @@ class Parity:
         margin = np.array(self.margin)
         # positions whose top-2 margin (in units of the logits' rms) is well
         # above the spread the reordering causes are decided, not near-ties
-        decided = margin > 4.0 * max(float(np.max(floor)), float(np.max(err)))
+        decided = (margin > 4.0 * max(float(np.max(floor)), float(np.max(err)))) & np.array(self.resolved, bool)
         bar = max(E2E_TOL, FLOOR_FACTOR * float(np.max(floor)))
         print(f"[{self.name}] {len(err)} positions: GPU-vs-oracle L2 max {err.max():.3e} mean {err.mean():.3e}; "
               f"reordered-oracle floor max {floor.max():.3e} mean {floor.mean():.3e}; bar {bar:.3e}; "

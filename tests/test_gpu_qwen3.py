@@ -216,6 +216,39 @@ def test_decode_greedy_queued_steps_equal_single_steps(gpu, orc):
     assert small.seq_len == len(prompt) + 6
 
 
+def test_long_context_decode_and_verify(gpu, orc):
+    """Long contexts after identical synthetic KV fills of GPU and oracle
+    caches: a graph decode step at position 65535, the last one the 256 key
+    splits of 256 of the model's attention workspace cover; and at context
+    20000 a 5-token and a 16-token verify (fused split-key attention over 79
+    splits) and a 24-token forward (96 query rows per kv head, past the
+    split-key path's 64, so flash attention at that offset).  Logits against
+    the oracle and its reordered floor."""
+    gm, om = _pair(gpu, orc, seed=12, max_tokens=24)
+    for ctx, cap, widths in [(65535, 65536, [1]), (20000, 20480, [5, 16, 24])]:
+        print(f"context {ctx}: synthetic KV fills", flush=True)
+        gc, oc, rc = gm.new_cache(cap), om.new_cache(cap), om.new_cache(cap)
+        for c in (gc, oc, rc):
+            c.fill_synthetic(77, ctx)
+        np.testing.assert_array_equal(gc.layer_numpy(2, 1)[:, :ctx], oc.data()[2, 1][:, :ctx])
+        par = Parity(f"SMALL at context {ctx}")
+        for i, M in enumerate(widths):
+            toks = orc.fill_tokens(300 + i, M, SMALL["vocab"])
+            if M == 1:
+                g = gm.decode_step(gc, int(toks[0]), want_logits=True)[1][None]
+            else:
+                g = gm.forward(gc, toks, all_logits=True)
+            o = om.forward(oc, toks, all_logits=True)
+            with orc.reversed_accumulation():
+                r = om.forward(rc, toks, all_logits=True)
+            par.add(torch_bf16_bits(g), o, r)
+            assert gc.seq_len == oc.seq_len == ctx + M
+            for c in (gc, oc, rc):
+                c.truncate(ctx)
+        par.check()
+        del gc, oc, rc
+
+
 def test_prefill_unsplit_fused_epilogues(gpu, orc):
     """A 2048-token prefill through one Qwen3-4B-shaped layer: at this size
     the o and down GEMMs run unsplit with the residual add in their epilogue

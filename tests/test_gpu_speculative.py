@@ -72,6 +72,15 @@ def test_32b_shape_verify_rows_equal_decode_steps(gpu, orc):
     _verify_rows_equal_decode_steps(gpu, m, None, orc.fill_tokens(41, 5, QWEN3_32B["vocab"]), 2304, fill=2048)
 
 
+def test_small_verify_rows_equal_decode_steps_at_long_context(gpu, orc):
+    """An 8-token verify at context 40000 (157 key splits of 256) equals
+    eight decode steps: the model's attention workspace holds 256 splits for
+    every fused width, so verify rows take the split-key path wherever a
+    decode step does."""
+    m = _gpu(gpu, SMALL, 23, max_tokens=16)
+    _verify_rows_equal_decode_steps(gpu, m, None, orc.fill_tokens(43, 8, SMALL["vocab"]), 40960, fill=40000)
+
+
 def _spec_equals_greedy(gpu, target, draft, prompt, n, spec_k=5):
     greedy = target.generate_greedy(target.new_cache(len(prompt) + n + 16), prompt, n, eos=())
     spec, stats = gpu.speculative_generate(target, target.new_cache(len(prompt) + n + 16), draft,
