@@ -437,15 +437,19 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
   __syncthreads();
   if (threadIdx.x == 0) {
-    // Arrival: an agent-scope release increment that wraps to 0 on the
-    // ns-th arrival (ready for the next call); the release publishes this
-    // workgroup's partials (stored by all its threads before the barrier).
-    // Only the last arrival acquires -- an agent-scope acquire fence after
-    // reading the final count synchronizes with every release before it --
-    // so only that workgroup pays the cache invalidation; its threads read
-    // the partials after the next barrier.
+    // Arrival: an agent-scope increment that wraps to 0 on the ns-th
+    // arrival (ready for the next call).  It is relaxed: every partial of
+    // this workgroup is an agent-scope atomic store (sc1, written through
+    // its XCD's L2) that its thread has waited to complete before the
+    // barrier above, so the partials are coherent across the XCDs before
+    // the increment issues -- the step of an agent-scope release that
+    // applies to them; the release's other step, an L2 writeback (for
+    // stores cached in L2, which the partials are not), is left out.
+    // Only the last arrival acquires (an agent-scope acquire fence after
+    // reading the final count), so only that workgroup pays the cache
+    // invalidation; its threads read the partials after the next barrier.
     last = __builtin_amdgcn_atomic_inc32(p.cnt + kvh * gridDim.z + blockIdx.z, static_cast<unsigned>(p.ns - 1),
-                                         __ATOMIC_RELEASE, "agent") == static_cast<unsigned>(p.ns - 1);
+                                         __ATOMIC_RELAXED, "agent") == static_cast<unsigned>(p.ns - 1);
     if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
