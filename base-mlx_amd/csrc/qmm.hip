@@ -296,6 +296,40 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
       }
     return;
   }
+  if constexpr (EPI == QMM_RESIDUAL) {
+    if (!p.part) {
+      // y may be res itself (the in-place residual add), so the compiler
+      // keeps each residual load behind the previous output store and the
+      // epilogue would wait out one memory round trip per output; each
+      // thread reads and writes only its own outputs, so the residuals of
+      // a 16-row slice are loaded first, then its outputs stored
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        uint16_t rv[NJ][4];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+          const int n = n0 + wn * (BN / 2) + j * 16 + li;
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int m = m0 + wm * 64 + i * 16 + 4 * q + r;
+            rv[j][r] = (n < N && m < M) ? p.res[static_cast<int64_t>(m) * N + n] : 0;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+          const int n = n0 + wn * (BN / 2) + j * 16 + li;
+          if (n >= N) continue;
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int m = m0 + wm * 64 + i * 16 + 4 * q + r;
+            if (m >= M) continue;
+            py[static_cast<int64_t>(m) * N + n] = f2bf(bf2f(rv[j][r]) + round_bf(acc[i][j][r]));
+          }
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -309,8 +343,6 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
         const int64_t o = static_cast<int64_t>(m) * N + n;
         if (p.part) {
           p.part[static_cast<int64_t>(blockIdx.z) * M * N + o] = acc[i][j][r];
-        } else if constexpr (EPI == QMM_RESIDUAL) {
-          py[o] = f2bf(bf2f(p.res[o]) + round_bf(acc[i][j][r]));
         } else {
           py[o] = f2bf(acc[i][j][r]);
         }
