@@ -352,10 +352,38 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
 
 // y = bf16(sum over splits of the fp32 partials) (or res + that, rounded
 // as the residual epilogue), 4 outputs per thread
+// vec (mn % 4 == 0, part 16-byte and y / res 8-byte aligned): each split's
+// four partials in one 16-byte load and the four residuals in one 8-byte
+// load ahead of the one 8-byte store (y may be res), summed in the same
+// order as the element loop.
 __global__ void __launch_bounds__(256) qmm_reduce_kernel(const float* part, const uint16_t* res, uint16_t* y,
-                                                         int64_t mn, int splits) {
+                                                         int64_t mn, int splits, int vec) {
   const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (i0 >= mn) return;
+  if (vec) {
+    float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < splits; s++) {
+      const float4 v = *reinterpret_cast<const float4*>(part + s * mn + i0);
+      t[0] += v.x;
+      t[1] += v.y;
+      t[2] += v.z;
+      t[3] += v.w;
+    }
+    uint16_t o[4];
+    if (res) {
+      const uint2 r2 = *reinterpret_cast<const uint2*>(res + i0);
+      const uint16_t r[4] = {static_cast<uint16_t>(r2.x & 0xffffu), static_cast<uint16_t>(r2.x >> 16),
+                             static_cast<uint16_t>(r2.y & 0xffffu), static_cast<uint16_t>(r2.y >> 16)};
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = f2bf(bf2f(r[e]) + round_bf(t[e]));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = f2bf(t[e]);
+    }
+    *reinterpret_cast<uint2*>(y + i0) = make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16),
+                                                   o[2] | (static_cast<uint32_t>(o[3]) << 16));
+    return;
+  }
   for (int64_t i = i0; i < min(i0 + 4, mn); i++) {
     float t = 0.0f;
     for (int s = 0; s < splits; s++) t += part[s * mn + i];
@@ -507,8 +535,10 @@ int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const 
   if (rc) return rc;
   if (splits > 1) {
     const int64_t mn = static_cast<int64_t>(M) * N;
+    const uint16_t* r = epi == QMM_RESIDUAL ? res : nullptr;
+    const int vec = mn % 4 == 0 && aligned(p.part, 16) && aligned(y, 8) && (r == nullptr || aligned(r, 8));
     hipLaunchKernelGGL(qmm_reduce_kernel, dim3(static_cast<unsigned>((mn + 1023) / 1024)), dim3(256), 0, stream,
-                       p.part, epi == QMM_RESIDUAL ? res : nullptr, y, mn, splits);
+                       p.part, r, y, mn, splits, vec);
     return check_launch("qmm_reduce");
   }
   return BMX_OK;
