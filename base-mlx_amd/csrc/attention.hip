@@ -61,8 +61,9 @@ struct FuseParams {
 // The split partials travel between workgroups on different XCDs (each with
 // its own L2) through agent-scope atomic loads and stores (relaxed, issued
 // with sc1: coherent across the XCDs); the arrival counter's agent-scope
-// release increment and the last arrival's acquire fence order them (one
-// per workgroup, not per wave).
+// release increment and the last arrival's agent-scope acquire fence order
+// them (one of each per workgroup, not per wave), so the handoff rests on
+// the memory model alone, whatever else the workgroup stores.
 // Pairs of floats move as one 8-byte access (8-byte aligned addresses).
 __device__ __forceinline__ void store_agent2(float* a, float x, float y) {
   const uint64_t v = static_cast<uint64_t>(__float_as_uint(x)) | (static_cast<uint64_t>(__float_as_uint(y)) << 32);
@@ -187,6 +188,15 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
   const int RT = min(RMAX, R - r0);   // rows in the tile
   const int offset = p.offset_dev ? *p.offset_dev : p.offset;
   const int L = offset + p.M;
+  // The grid holds a split per kps keys of the largest context the launch
+  // may see (a captured decode step: the cache capacity); only the first
+  // ns_live hold keys of this call's context.  The others leave before any
+  // load, and the arrival counter and the merge count only the live ones,
+  // so the cost follows the context, not the capacity.  (A split without
+  // visible keys contributes nothing to the merge either way: results are
+  // the same bits as with every split taking part.)
+  const int ns_live = min(p.ns, (L + p.kps - 1) / p.kps);
+  if (split >= ns_live) return;
   // this workgroup's keys: [kbase, kbase + kps), of which those < kend exist
   const int kbase = split * p.kps;
   const int kend = min(L, kbase + p.kps);
@@ -433,23 +443,20 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
       if (d4 == 0) store_agent2(p.part_ml + base * 2, m, l);
     }
   }
-  // ---- the last of the ns workgroups of this (kv head, row tile) merges ----
+  // ---- the last of the ns_live workgroups of this (kv head, row tile) merges ----
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
   __syncthreads();
   if (threadIdx.x == 0) {
-    // Arrival: an agent-scope increment that wraps to 0 on the ns-th
-    // arrival (ready for the next call).  It is relaxed: every partial of
-    // this workgroup is an agent-scope atomic store (sc1, written through
-    // its XCD's L2) that its thread has waited to complete before the
-    // barrier above, so the partials are coherent across the XCDs before
-    // the increment issues -- the step of an agent-scope release that
-    // applies to them; the release's other step, an L2 writeback (for
-    // stores cached in L2, which the partials are not), is left out.
-    // Only the last arrival acquires (an agent-scope acquire fence after
-    // reading the final count), so only that workgroup pays the cache
-    // invalidation; its threads read the partials after the next barrier.
-    last = __builtin_amdgcn_atomic_inc32(p.cnt + kvh * gridDim.z + blockIdx.z, static_cast<unsigned>(p.ns - 1),
-                                         __ATOMIC_RELAXED, "agent") == static_cast<unsigned>(p.ns - 1);
+    // Arrival: an agent-scope release increment that wraps to 0 on the
+    // ns_live-th arrival (ready for the next call).  Every thread's partial
+    // stores completed before the barrier above, and the release orders
+    // them (and every other store of this workgroup) before the increment
+    // for any workgroup that acquires the count.  Only the last arrival
+    // acquires (an agent-scope acquire fence after reading the final
+    // count), so only that workgroup pays the cache invalidation; its
+    // threads read the partials after the next barrier.
+    last = __builtin_amdgcn_atomic_inc32(p.cnt + kvh * gridDim.z + blockIdx.z, static_cast<unsigned>(ns_live - 1),
+                                         __ATOMIC_RELEASE, "agent") == static_cast<unsigned>(ns_live - 1);
     if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
@@ -457,7 +464,7 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
   // (Two waves per row, each folding half of the splits and merged through
   // LDS, measured 2% slower end to end.)
   for (int r = wave; r < RT; r += NW)
-    store_pair(p, kvh * R + r0 + r, lane, combine_range(p, kvh * R + r0 + r, lane, 0, p.ns));
+    store_pair(p, kvh * R + r0 + r, lane, combine_range(p, kvh * R + r0 + r, lane, 0, ns_live));
 }
 
 // Prefill / long verify: flash attention on MFMA.  A workgroup of 4 waves

@@ -649,7 +649,9 @@ static int graph_step(bmx_qwen3* m, bmx_kv_cache* c, hipStream_t st, uint32_t to
   if (int rc = ensure_graph(m, c, st)) return rc;
   m->host_tok[0] = tok;
   m->host_tok[1] = static_cast<uint32_t>(c->seq_len);
-  if (int rc = check_hip(hipMemcpyAsync(m->step_io, &m->host_tok[0], 8, hipMemcpyHostToDevice, st), "set token"))
+  m->host_tok[2] = 0;
+  m->host_tok[3] = 0;  // ring count: this replay publishes to slot 0, whatever ran before
+  if (int rc = check_hip(hipMemcpyAsync(m->step_io, &m->host_tok[0], 16, hipMemcpyHostToDevice, st), "set token"))
     return rc;
   if (int rc = check_hip(hipGraphLaunch(m->graph, st), "graph launch")) return rc;
   if (int rc = check_hip(hipMemcpyAsync(&m->host_tok[2], m->step_io + 2, 4, hipMemcpyDeviceToHost, st), "read token"))

@@ -12,10 +12,18 @@ next steps are already queued on the GPU.  `value` = decode tokens / s.
 `config.decode_step_sync_tok_s` times the same tokens one synchronous decode
 step at a time (token read back before the next launch).
 
-`roofline`: the qmv GEMV at the gate/up projection shape (9728 x 2560),
-timed with HIP events around a graph of launches on the benchmark stream,
-rotating over >= 1 GiB of distinct weights so no launch reads from the
-256 MB Infinity Cache; algorithmic bytes per launch = 0.5625 N K + 2 K + 2 N.
+`roofline`: the decode step's dominant kernel -- the fused decode attention
+(QK-norm, RoPE, KV-row write, split-key GQA attention and merge; one launch
+per layer, the largest share of a decode token) -- for one new token at
+position 4096, launched through its C-ABI entry point (the kernel the decode
+graph launches) in a graph over 36 distinct layer caches (604 MB of K/V:
+more than the 256 MB Infinity Cache), timed with HIP events on the capturing
+stream; algorithmic bytes per launch = K and V rows of the 4096 cached
+positions plus the new token's rows, the q row, the norm weights and the
+output.  `step_roofline`: the whole decode step, bytes every token must read
+(weights + the K/V of the context) over the measured time per token.
+`config.qmv_sweep`: the M = 1 GEMV per Qwen3-4B projection shape, 1000
+launches per shape in a graph rotating over >= 1 GiB of distinct weights.
 
 `cpu_baseline`: the C restatement of the same decode step (oracle/, OpenMP)
 on this host's cores, timed over a bounded sample of decode tokens at context
@@ -46,6 +54,7 @@ ROOF_SHAPE = (9728, 2560)
 QMM_SHAPES = QMV_SHAPES + [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288), (151936, 4096)]
 QMM_M = [5, 128, 512, 2048]
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+PREFILLS = 5  # warm prefills timed for the median
 
 
 def _profile_value(name, key):
@@ -59,20 +68,24 @@ def _profile_value(name, key):
     return None
 
 
+TRAFFIC_PROFILE = "decode_attention_ctx4096_pmc.md"
+TRACE_PROFILE = "bench_default_qwen3_4b_decode.md"
+
+
 def measured_traffic():
-    """HBM bytes per launch of the roofline GEMV, from the committed
+    """HBM bytes per launch of the roofline kernel, read from the committed
     rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE scaled by a copy of
-    known size); None when that summary is absent."""
-    v = _profile_value("qmv_9728x2560_pmc.md", "traffic_bytes_per_launch")
+    known size; not measured in this run); None when it is absent."""
+    v = _profile_value(TRAFFIC_PROFILE, "traffic_bytes_per_launch")
     return None if v is None else int(v)
 
 
 def traced_duration_us():
-    """Average duration of the roofline GEMV in the committed rocprofv3
+    """Average duration of the roofline kernel in the committed rocprofv3
     kernel trace of the default bench command (the tracer's per-dispatch
-    timestamps; the line's `achieved` uses HIP events around graph replays
-    instead); None when that summary is absent."""
-    return _profile_value("bench_default_qwen3_4b_decode.md", "roofline_kernel_trace_avg_us")
+    timestamps; not measured in this run, whose `achieved` uses HIP events
+    around graph replays); None when that summary is absent."""
+    return _profile_value(TRACE_PROFILE, "roofline_kernel_trace_avg_us")
 
 
 def host_info():
@@ -100,9 +113,10 @@ def qmv_bytes(N, K, M=1):
     return int(0.5625 * N * K + 2 * M * K + 2 * M * N)
 
 
-def time_qmv(bmx, torch, N, K, reps=200, M=1):
-    """Average duration (us) of one qmv launch, graph-captured, rotating over
-    >= 1 GiB of distinct weights; HIP events on the capturing stream."""
+def time_qmv(bmx, torch, N, K, reps=1000, M=1):
+    """Average duration (us) of one qmv launch over `reps` timed launches
+    (one graph replay, after an untimed one), rotating over >= 1 GiB of
+    distinct weights; HIP events on the capturing stream."""
     nbytes = qmv_bytes(N, K, M)
     copies = max(2, -(-(1 << 30) // nbytes))
     ws = [bmx.init_qlinear(5000 + i, N, K) for i in range(copies)]
@@ -124,13 +138,80 @@ def time_qmv(bmx, torch, N, K, reps=200, M=1):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(st)
         g.replay()
-        g.replay()
         e1.record(st)
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / (2 * reps)
+    us = e0.elapsed_time(e1) * 1000.0 / reps
     del g, ws
     torch.cuda.empty_cache()
     return us, nbytes
+
+
+ATT_CTX = 4096  # cached positions before the first timed decode token
+ATT_LAYERS = 36
+
+
+def attention_bytes(ctx, Hq=32, Hkv=8, D=128):
+    """Algorithmic bytes of one decode-attention launch for the token at
+    position ctx: K and V rows of the ctx cached positions, the q, k and v
+    rows of the new token, its K / V rows written to the cache, the two norm
+    weights and the output row (bf16)."""
+    return 2 * 2 * ctx * Hkv * D + 2 * Hq * D + 2 * 2 * Hkv * D + 2 * 2 * Hkv * D + 2 * 2 * D + 2 * Hq * D
+
+
+def _attention_inputs(bmx, torch, ctx, layers, cap=4352, Hq=32, Hkv=8):
+    kcs = [bmx.fill_normal_bf16(100 + i, (Hkv, cap, 128)) for i in range(layers)]
+    vcs = [bmx.fill_normal_bf16(200 + i, (Hkv, cap, 128)) for i in range(layers)]
+    q = bmx.fill_normal_bf16(1, (1, Hq * 128))
+    k = bmx.fill_normal_bf16(2, (1, Hkv * 128))
+    v = bmx.fill_normal_bf16(3, (1, Hkv * 128))
+    qn = bmx.fill_normal_bf16(4, (128,))
+    kn = bmx.fill_normal_bf16(5, (128,))
+    return kcs, vcs, q, k, v, qn, kn
+
+
+def time_decode_attention(bmx, torch, ctx=ATT_CTX, layers=ATT_LAYERS, per_layer=28):
+    """Average duration (us) of the decode step's attention launch
+    (bmx_qk_norm_rope_kv_attention: the kernel the decode graph launches per
+    layer) for one token at position ctx, Qwen3-4B head layout: a graph of
+    layers x per_layer launches cycling over `layers` distinct layer caches
+    (each launch reads K / V no other launch near it read), HIP events on
+    the capturing stream around one replay after an untimed one."""
+    kcs, vcs, q, k, v, qn, kn = _attention_inputs(bmx, torch, ctx, layers)
+    ws = bmx.attention_workspace(32, 1)
+    reps = layers * per_layer
+    st = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        for i in range(layers):
+            bmx.qk_norm_rope_kv_attention(q, k, v, qn, kn, kcs[i], vcs[i], ctx, workspace=ws, stream=st)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=st):
+            for i in range(reps):
+                bmx.qk_norm_rope_kv_attention(q, k, v, qn, kn, kcs[i % layers], vcs[i % layers], ctx, workspace=ws,
+                                              stream=st)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        g.replay()
+        e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / reps
+    del g, kcs, vcs
+    torch.cuda.empty_cache()
+    return us, attention_bytes(ctx)
+
+
+def decode_weight_bytes(shape):
+    """Packed weight bytes one decode token reads: every projection of every
+    layer and the (tied) vocabulary head, 0.5625 B per weight, plus the norm
+    weights."""
+    H, I, L = shape["hidden"], shape["inter"], shape["layers"]
+    qd, kvd = shape["n_heads"] * shape["head_dim"], shape["n_kv_heads"] * shape["head_dim"]
+    per_layer = qd * H + 2 * kvd * H + H * qd + 2 * I * H + H * I
+    norms = L * (2 * H + 2 * shape["head_dim"]) * 2 + 2 * H
+    return int(0.5625 * (L * per_layer + shape["vocab"] * H)) + norms
 
 
 def time_qmm(bmx, torch, M, N, K):
@@ -353,9 +434,18 @@ def small_model_bench(bmx, torch, prompt_len=32, new_tokens=64, seed=7, cpu=True
 
 
 def profile_roofline(bmx, torch, launches=200):
-    """Counter-collection workload: the roofline GEMV shape launched eagerly
-    (rotating over >= 1 GiB of weights), then a plain 256 MiB device copy as
-    the calibration kernel whose FETCH_SIZE / WRITE_SIZE must read 256 MiB."""
+    """Counter-collection workload: the roofline kernel (the decode step's
+    attention launch at position 4096) launched eagerly over 36 layer
+    caches, the gate/up-shape GEMV (rotating over >= 1 GiB of weights), then
+    a plain 256 MiB device copy as the calibration kernel whose FETCH_SIZE /
+    WRITE_SIZE must read 256 MiB."""
+    kcs, vcs, q, k, v, qn, kn = _attention_inputs(bmx, torch, ATT_CTX, ATT_LAYERS)
+    aws = bmx.attention_workspace(32, 1)
+    for i in range(launches):
+        bmx.qk_norm_rope_kv_attention(q, k, v, qn, kn, kcs[i % ATT_LAYERS], vcs[i % ATT_LAYERS], ATT_CTX,
+                                      workspace=aws)
+    torch.cuda.synchronize()
+    del kcs, vcs
     N, K = ROOF_SHAPE
     nbytes = qmv_bytes(N, K)
     copies = max(2, -(-(1 << 30) // nbytes))
@@ -371,8 +461,9 @@ def profile_roofline(bmx, torch, launches=200):
     for _ in range(10):
         dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"profile-roofline: {launches} qmv launches N={N} K={K} ({nbytes} algorithmic bytes each), "
-        f"10 copies of {256 << 20} bytes")
+    log(f"profile-roofline: {launches} decode attention launches at position {ATT_CTX} "
+        f"({attention_bytes(ATT_CTX)} algorithmic bytes each), {launches} qmv launches N={N} K={K} "
+        f"({nbytes} algorithmic bytes each), 10 copies of {256 << 20} bytes")
 
 
 def profile_mfma(bmx, torch, launches=20):
@@ -467,17 +558,25 @@ def main():
         model = bmx.Qwen3(bmx.qwen3_config(**SHAPE_4B), 42, 0.02, max_tokens=min(args.prompt, 4096))
         cache = model.new_cache(max(cap, 4352))
         prompt = np.array([int(v) for v in np.random.default_rng(11).integers(0, 151936, args.prompt)], np.uint32)
-        # prefill twice: the first forward of the process also pays one-time
-        # setup (LDS limits, the split-K buffer); the second is timed
-        model.forward(cache, prompt)
-        cache.reset()
-        torch.cuda.synchronize()
-        t0 = time.time()
+        # prefill: the first forward of the process also pays one-time setup
+        # (LDS limits, the split-K buffer); then PREFILLS warm ones, each
+        # timed with HIP events on the stream (tokens upload to logits)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * (PREFILLS + 1))]
+        ev[0].record(stream)
         logits = model.forward(cache, prompt)
+        ev[1].record(stream)
+        for i in range(PREFILLS):
+            cache.reset()
+            ev[2 + 2 * i].record(stream)
+            logits = model.forward(cache, prompt)
+            ev[3 + 2 * i].record(stream)
         tok = int(torch.argmax(logits.float()).item())
         torch.cuda.synchronize()
-        prefill_s = time.time() - t0
-        log(f"prefill {args.prompt} tokens: {prefill_s * 1000:.1f} ms")
+        prefill_first_ms = ev[0].elapsed_time(ev[1])
+        prefill_runs = sorted(ev[2 + 2 * i].elapsed_time(ev[3 + 2 * i]) for i in range(PREFILLS))
+        prefill_ms = float(np.median(prefill_runs))
+        log(f"prefill {args.prompt} tokens: first {prefill_first_ms:.1f} ms, warm median of {PREFILLS} "
+            f"{prefill_ms:.2f} ms (runs {', '.join(f'{x:.2f}' for x in prefill_runs)})")
         # warmup (captures the decode graph), then rewind to the prompt
         t = tok
         for _ in range(args.warmup):
@@ -513,22 +612,41 @@ def main():
     del cache
     torch.cuda.empty_cache()
 
+    # whole-step roofline: bytes each timed token reads (weights, and the
+    # K / V of its context: token i of the timed region sits at position
+    # prompt + i) over the measured time per token
+    kv_per_pos = 2 * 2 * SHAPE_4B["layers"] * SHAPE_4B["n_kv_heads"] * SHAPE_4B["head_dim"]
+    step_bytes = decode_weight_bytes(SHAPE_4B) + kv_per_pos * (args.prompt + (args.steps - 1) / 2.0)
+    step_gbs = step_bytes * tok_s / 1e9
+    step_roof = {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                 "frac": round(step_gbs / HBM_PEAK_GBS, 4), "bytes_per_token": int(step_bytes),
+                 "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1)}
+    log(f"decode step: {step_bytes / 1e9:.3f} GB per token -> {step_gbs:.0f} GB/s "
+        f"({100 * step_gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s; roofline {step_roof['roofline_tok_s']} tok/s)")
+
+    att_us, att_bytes = time_decode_attention(bmx, torch)
+    att_gbs = att_bytes / att_us / 1e3
+    tr = traced_duration_us()
+    roof = {"bound": "hbm", "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+            "kernel": f"decode attention (attn_decode_kernel: QK-norm, RoPE, KV write, split-key GQA, merge), "
+                      f"Qwen3-4B heads, token at position {ATT_CTX}",
+            "avg_launch_us": round(att_us, 3), "bytes_per_launch": att_bytes,
+            "traffic_from": f"profiles/{TRAFFIC_PROFILE} (rocprofv3 --pmc; not measured in this run)",
+            "trace_avg_us": tr, "trace_avg_us_from": f"profiles/{TRACE_PROFILE} (rocprofv3 kernel trace of the "
+                                                      f"default bench command; not measured in this run)",
+            "frac_trace": None if tr is None else round(att_bytes / tr / 1e3 / HBM_PEAK_GBS, 4)}
+    log(f"decode attention at position {ATT_CTX}: {att_us:.2f} us per launch, {att_gbs:.0f} GB/s "
+        f"({100 * att_gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
+
     sweep = []
-    roof = None
     if not args.no_sweep:
         for (N, K) in QMV_SHAPES:
             us, nb = time_qmv(bmx, torch, N, K)
             gbs = nb / us / 1e3
             sweep.append({"N": N, "K": K, "us": round(us, 3), "GB/s": round(gbs, 1),
-                          "frac": round(gbs / HBM_PEAK_GBS, 4)})
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": 1000})
             log(f"qmv N={N} K={K}: {us:.2f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
-            if (N, K) == ROOF_SHAPE:
-                tr = traced_duration_us()
-                roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                        "kernel": f"qmv M=1 N={N} K={K}", "avg_launch_us": round(us, 3), "bytes_per_launch": nb,
-                        "trace_avg_us": tr,
-                        "frac_trace": None if tr is None else round(nb / tr / 1e3 / HBM_PEAK_GBS, 4)}
 
     qmm = [] if args.no_qmm_sweep else qmm_sweep(bmx, torch)
     spec = None if args.no_speculative else speculative_bench(bmx, torch)
@@ -560,10 +678,12 @@ def main():
         "data": "synthetic: seeded random-init weights N(0,0.02) quantized 4-bit, seeded random token ids",
         "config": {"workload": "Qwen3-4B-shape 4-bit greedy decode, batch 1, after a 4096-token prefill",
                    "prompt_tokens": args.prompt, "kv_cache": [36, 2, 8, max(cap, 4352), 128],
-                   "prefill_ms": round(prefill_s * 1000, 1),
+                   "prefill_ms": round(prefill_ms, 2), "prefill_first_call_ms": round(prefill_first_ms, 2),
+                   "prefill_runs_ms": [round(x, 2) for x in prefill_runs],
                    "decode_step_sync_tok_s": round(args.steps / dt_sync, 2), "qmv_sweep": sweep, "qmm_sweep": qmm,
                    "speculative": spec, "qwen3_0_6b": small, "gather_qmm": moe},
         "roofline": roof,
+        "step_roofline": step_roof,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

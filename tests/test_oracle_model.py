@@ -61,7 +61,25 @@ def test_kv_capacity_error_leaves_cache(orc):
     np.testing.assert_array_equal(c.data(), snap)
 
 
-def _hf_model(orc, m, cfg):
+NORM_NAMES = ["input_layernorm", "post_attention_layernorm", "self_attn.q_norm", "self_attn.k_norm"]
+
+
+def _random_norms(orc, m, cfg, seed):
+    """Fills every norm of the oracle model with its own random weights in
+    [0.25, 2] (bf16), so that two norms swapped, or a norm left at 1, change
+    the logits."""
+    rng = np.random.default_rng(seed)
+    for l in list(range(cfg.layers)) + [-1]:
+        for which in (range(4) if l >= 0 else (0,)):
+            v = m.norm(l, which)
+            v[:] = orc.f32_to_bf16(rng.uniform(0.25, 2.0, v.size).astype(np.float32))
+
+
+def _hf_model(orc, m, cfg, norm_map=None):
+    """HF Qwen3ForCausalLM in float32 on the oracle's dequantized weights and
+    norm weights.  norm_map(l, which) -> (l', which') wires HF's norm
+    (l, which) to the oracle's (l', which') instead (layer -1: final norm),
+    for the negative controls."""
     from transformers import Qwen3Config, Qwen3ForCausalLM
 
     hc = Qwen3Config(vocab_size=cfg.vocab, hidden_size=cfg.hidden, intermediate_size=cfg.inter,
@@ -75,37 +93,68 @@ def _hf_model(orc, m, cfg):
         w, s, b = m.qlinear(layer, slot)
         return torch.from_numpy(bf16_to_f32(orc.dequantize(w, s, b)))
 
-    sd = {"model.embed_tokens.weight": deq(-1, 0)}
+    def norm(layer, which):
+        src = norm_map(layer, which) if norm_map else (layer, which)
+        return torch.from_numpy(bf16_to_f32(m.norm(*src)).copy())
+
+    sd = {"model.embed_tokens.weight": deq(-1, 0), "model.norm.weight": norm(-1, 0)}
     names = ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
              "mlp.up_proj", "mlp.down_proj"]
     for l in range(cfg.layers):
         for sl, n in enumerate(names):
             sd[f"model.layers.{l}.{n}.weight"] = deq(l, sl)
+        for which, n in enumerate(NORM_NAMES):
+            sd[f"model.layers.{l}.{n}.weight"] = norm(l, which)
     with torch.no_grad():
         for k, p in hf.named_parameters():
             if k in sd:
                 p.copy_(sd[k])
-            elif k.endswith("norm.weight"):
-                p.fill_(1.0)
             elif k != "lm_head.weight":
                 raise AssertionError(f"unmapped parameter {k}")
         hf.tie_weights()
     return hf
 
 
-def test_forward_matches_transformers_qwen3(orc):
-    m = tiny(orc, seed=3)
-    cfg = m.cfg
-    hf = _hf_model(orc, m, cfg)
-    toks = orc.fill_tokens(11, 16, cfg.vocab)
+def _hf_errors(orc, m, cfg, toks, norm_map=None):
+    hf = _hf_model(orc, m, cfg, norm_map)
     with torch.no_grad():
         ref = hf(torch.from_numpy(toks.astype(np.int64))[None]).logits[0].double().numpy()
-    c = m.new_cache(32)
-    got = bf16_to_f32(m.forward(c, toks, all_logits=True)).astype(np.float64)
-    for t in range(16):
-        assert max_rel_err(got[t], ref[t]) < 3e-2, t
-    agree = np.mean(np.argmax(got, 1) == np.argmax(ref, 1))
+    got = bf16_to_f32(m.forward(m.new_cache(32), toks, all_logits=True)).astype(np.float64)
+    errs = np.array([max_rel_err(got[t], ref[t]) for t in range(len(toks))])
+    return errs, float(np.mean(np.argmax(got, 1) == np.argmax(ref, 1)))
+
+
+def test_forward_matches_transformers_qwen3(orc):
+    """The oracle's forward against HF's, every norm weight random and
+    distinct: each position within 3e-2 and >= 80% top-1 agreement."""
+    m = tiny(orc, seed=3)
+    cfg = m.cfg
+    _random_norms(orc, m, cfg, 17)
+    toks = orc.fill_tokens(11, 16, cfg.vocab)
+    errs, agree = _hf_errors(orc, m, cfg, toks)
+    print(f"oracle vs HF Qwen3 (random norms): max rel err {errs.max():.2e}, top-1 {agree:.3f}")
+    assert (errs < 3e-2).all(), errs
     assert agree >= 0.8
+
+
+@pytest.mark.parametrize("swap", ["q_k", "input_post", "final_input0", "layers"])
+def test_transformers_pin_detects_swapped_norms(orc, swap):
+    """Negative controls of the pin above: the same comparison with two of
+    HF's norm weights wired the other way round fails its bar, so a swap in
+    the oracle's norm wiring could not pass it either."""
+    m = tiny(orc, seed=3)
+    cfg = m.cfg
+    _random_norms(orc, m, cfg, 17)
+    toks = orc.fill_tokens(11, 16, cfg.vocab)
+    maps = {
+        "q_k": lambda l, w: (l, {2: 3, 3: 2}.get(w, w)) if l >= 0 else (l, w),
+        "input_post": lambda l, w: (l, {0: 1, 1: 0}.get(w, w)) if l >= 0 else (l, w),
+        "final_input0": lambda l, w: (0, 0) if l < 0 else ((-1, 0) if (l, w) == (0, 0) else (l, w)),
+        "layers": lambda l, w: ((1 - l), w) if l >= 0 else (l, w),
+    }
+    errs, _ = _hf_errors(orc, m, cfg, toks, maps[swap])
+    print(f"swapped norms ({swap}): max rel err {errs.max():.2e}")
+    assert errs.max() > 3e-2, errs
 
 
 def test_greedy_generate_follows_forward(orc):
