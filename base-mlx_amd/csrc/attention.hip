@@ -59,80 +59,119 @@ struct FuseParams {
 };
 
 // The split partials travel between workgroups on different XCDs (each with
-// its own L2) through agent-scope atomic loads and stores (relaxed, issued
-// with sc1: coherent across the XCDs); the arrival counter's agent-scope
-// release increment and the last arrival's agent-scope acquire fence order
-// them (one of each per workgroup, not per wave), so the handoff rests on
-// the memory model alone, whatever else the workgroup stores.
-// Pairs of floats move as one 8-byte access (8-byte aligned addresses).
+// its own L2).  The writers store them with agent-scope atomic stores
+// (relaxed, issued with sc1: written through to memory), every thread waits
+// for its stores, the workgroup meets at a barrier, and one thread bumps the
+// arrival counter with an agent-scope release; the last arrival takes an
+// agent-scope acquire fence, and after the next barrier its threads read the
+// partials with ordinary loads.  Release, acquire and the two workgroup
+// barriers order the stores before the loads (message passing in the
+// memory model), whatever else either workgroup stores.
+// Pairs of floats are stored as one 8-byte access (8-byte aligned addresses).
 __device__ __forceinline__ void store_agent2(float* a, float x, float y) {
   const uint64_t v = static_cast<uint64_t>(__float_as_uint(x)) | (static_cast<uint64_t>(__float_as_uint(y)) << 32);
   __hip_atomic_store(reinterpret_cast<uint64_t*>(a), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float2 load_agent2(const float* a) {
-  const uint64_t v =
-      __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(a)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_float2(__uint_as_float(static_cast<uint32_t>(v)), __uint_as_float(static_cast<uint32_t>(v >> 32)));
-}
 
-// A running (max, sum, o) of softmax partials: lane = 2 dims.
-struct Part {
-  float mx, l, o0, o1;
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+
+// A running (max, sum, o) of softmax partials while merging splits: lane l
+// holds dims 4 (l % 32) .. + 3 of the splits of parity l / 32.
+struct Fold {
+  float mx, l;
+  float o[4];
 };
 
-// Folds the partials of splits [s_begin, s_end) of one (head, token) pair
-// `wid`; one wave, lane = 2 dims.  Up to 24 splits are read per batch (48
-// loads, all in flight within the 63 outstanding loads a wave can count),
-// batches folded with an online rescale.
-__device__ __forceinline__ Part combine_range(const AttnParams& p, int wid, int lane, int s_begin, int s_end) {
-  const int64_t base = static_cast<int64_t>(wid) * p.ns;
-  constexpr int B = 24;
-  Part r{-INFINITY, 0.0f, 0.0f, 0.0f};
-  for (int s0 = s_begin; s0 < s_end; s0 += B) {
-    float2 ml[B], ov[B];
+// Folds the partials of splits [0, ns) of NR (head, token) rows wids[i]
+// into r[i]; one wave.  Splits come in batches of 48 at fixed boundaries:
+// lane s loads the (max, sum) pair of split s0 + s (one load per row), and
+// each 16-byte load of o partials brings split s0 + 2u to lanes 0-31 and
+// split s0 + 2u + 1 to lanes 32-63 (24 loads per row and batch, every load
+// of the batch issued before the first is used, from clamped addresses so
+// that the count in flight is fixed).  The weights exp(m_s - max) come from
+// the lane that holds m_s; a split without visible keys (m = -inf) is left
+// out -- how many such trailing splits a launch has depends on its
+// context, not on the row, so they leave a row's bits unchanged.  Each half
+// of the wave folds its splits in increasing order; the halves are added at
+// the end (merge_halves).
+template <int NR>
+__device__ __forceinline__ void combine_splits(const AttnParams& p, const int (&wids)[NR], int lane, int ns,
+                                               Fold (&r)[NR]) {
+  constexpr int B = 24;  // 16-byte o loads per row and batch: 48 splits
+  const int half = lane >> 5, dl = 4 * (lane & 31);
 #pragma unroll
-    for (int u = 0; u < B; u++) {
-      if (s0 + u < s_end) {
-        ml[u] = load_agent2(p.part_ml + (base + s0 + u) * 2);
-        ov[u] = load_agent2(p.part_o + (base + s0 + u) * kD + 2 * lane);
+  for (int i = 0; i < NR; i++) r[i] = Fold{-INFINITY, 0.0f, {0.0f, 0.0f, 0.0f, 0.0f}};
+  for (int s0 = 0; s0 < ns; s0 += 2 * B) {
+    const int nb = min(2 * B, ns - s0);
+    f32x2_t ml[NR];
+    f32x4_t ov[NR][B];
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+      const int64_t base = static_cast<int64_t>(wids[i]) * p.ns + s0;
+      ml[i] = *reinterpret_cast<const f32x2_t*>(p.part_ml + (base + min(lane, nb - 1)) * 2);
+#pragma unroll
+      for (int u = 0; u < B; u++)
+        ov[i][u] = *reinterpret_cast<const f32x4_t*>(p.part_o + (base + min(2 * u + half, nb - 1)) * kD + dl);
+    }
+    // every load of the batch goes out before any use of the first
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+      const float m = lane < nb ? ml[i].x : -INFINITY;
+      const float bm = max_xor32(max_xor16(row16_max(m)));
+      const float nm = fmaxf(r[i].mx, bm);
+      if (nm == -INFINITY) continue;  // uniform: nothing visible so far
+      const float a = (r[i].mx == -INFINITY) ? 0.0f : expf(r[i].mx - nm);
+      const float w = (m == -INFINITY) ? 0.0f : expf(m - nm);
+      // batch sum of w_s l_s: lane s holds split s; fixed butterfly order
+      float wl = w * (lane < nb ? ml[i].y : 0.0f);
+      wl = add_xor32(add_xor16(row16_sum(wl)));
+      r[i].l = __builtin_fmaf(r[i].l, a, wl);
+      r[i].mx = nm;
+#pragma unroll
+      for (int d = 0; d < 4; d++) r[i].o[d] *= a;
+#pragma unroll
+      for (int u = 0; u < B; u++) {
+        if (2 * u >= nb) break;  // uniform
+        const float m_lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 2 * u));
+        const float m_hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), min(2 * u + 1, 63)));
+        const float w_lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 2 * u));
+        const float w_hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), min(2 * u + 1, 63)));
+        const float ms = half ? m_hi : m_lo, ws = half ? w_hi : w_lo;
+        if (ms != -INFINITY) {
+#pragma unroll
+          for (int d = 0; d < 4; d++) r[i].o[d] = __builtin_fmaf(ws, ov[i][u][d], r[i].o[d]);
+        }
       }
     }
-    float bm = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < B; u++)
-      if (s0 + u < s_end) bm = fmaxf(bm, ml[u].x);
-    const float nm = fmaxf(r.mx, bm);
-    if (nm == -INFINITY) continue;
-    const float a = (r.mx == -INFINITY) ? 0.0f : expf(r.mx - nm);
-    r.l *= a;
-    r.o0 *= a;
-    r.o1 *= a;
-#pragma unroll
-    for (int u = 0; u < B; u++) {
-      if (s0 + u >= s_end || ml[u].x == -INFINITY) continue;
-      const float w = expf(ml[u].x - nm);
-      r.l += w * ml[u].y;
-      r.o0 += w * ov[u].x;
-      r.o1 += w * ov[u].y;
-    }
-    r.mx = nm;
   }
-  return r;
 }
 
-// Normalises a merged partial and writes the pair `wid` (head h, token t).
-__device__ __forceinline__ void store_pair(const AttnParams& p, int wid, int lane, Part r) {
+// Normalises a merged row (the two halves of the wave added) and writes it:
+// row `wid` = (head h, token t); lanes 0-31 store 4 dims each.
+__device__ __forceinline__ void store_fold(const AttnParams& p, int wid, int lane, const Fold& r) {
+  float o[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) o[d] = add_xor32(r.o[d]);
+  if (lane >= 32) return;
   const int h = wid / p.M, t = wid - h * p.M;
   const float inv = r.l > 0.0f ? 1.0f / r.l : 0.0f;
-  uint16_t* o = p.out + static_cast<int64_t>(t) * p.Hq * kD + h * kD + 2 * lane;
-  o[0] = f2bf(r.o0 * inv);
-  o[1] = f2bf(r.o1 * inv);
+  uint16_t* dst = p.out + static_cast<int64_t>(t) * p.Hq * kD + h * kD + 4 * lane;
+  const uint32_t w0 = static_cast<uint32_t>(f2bf(o[0] * inv)) | (static_cast<uint32_t>(f2bf(o[1] * inv)) << 16);
+  const uint32_t w1 = static_cast<uint32_t>(f2bf(o[2] * inv)) | (static_cast<uint32_t>(f2bf(o[3] * inv)) << 16);
+  *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
 }
 
+
 // Decode / short verify (R = tokens x heads-per-kv-head query rows of one kv
-// head, up to 64).  A workgroup of 8 waves owns one kv head, one tile of
-// RMAX <= 8 of those rows and 256 keys, 32 per wave.  Every K, V and q load
-// of a wave is issued before any arithmetic:
+// head, up to 64).  A workgroup of NW waves owns one kv head, one tile of
+// RMAX <= 8 of those rows and 32 NW keys, 32 per wave.  Every K, V and q
+// load of a wave is issued before any arithmetic:
 //   QK on MFMA (v_mfma_f32_16x16x32_bf16): A = the tile's query rows (padded
 //     to 16; lane l holds row l%16, dims 32*ks + 8*(l/16), 4 fragments; the
 //     R rows of one kv head are contiguous in [Hq, M, 128]), B = K^T (lane l
@@ -144,9 +183,9 @@ __device__ __forceinline__ void store_pair(const AttnParams& p, int wid, int lan
 //   PV on VALU in fp32: V in 16-byte loads, lane = 8 dims x 8 keys, the
 //     four key quarters added by permlane swap butterflies (the same
 //     operations for every row, whatever RMAX).
-// The 8 waves' (o, m, l) are merged in LDS, 8 rows at a time, and one
+// The NW waves' (o, m, l) are merged in LDS, 8 rows at a time, and one
 // unnormalised partial per row and workgroup goes to the split workspace
-// (NS = ceil(L / 256)).  The last workgroup of a (kv head, row tile) to
+// (NS = ceil(L / 32 NW)).  The last workgroup of a (kv head, row tile) to
 // finish -- an arrival counter per pair, bumped once the workgroup's partial
 // stores have completed, wrapping back to zero on the last arrival -- merges
 // the NS partials of its rows into out; no workgroup waits for another.
@@ -154,20 +193,19 @@ __device__ __forceinline__ void store_pair(const AttnParams& p, int wid, int lan
 // FUSED: q holds the raw q projection rows, and the prologue does the work
 // of qk_norm_rope_kv_kernel first: each wave norms and rotates whole head
 // rows (qk_norm_rope_lane) -- the tile's q rows into LDS, and the new keys
-// offset + t that fall in this workgroup's 256 keys into LDS and (row tile
+// offset + t that fall in this workgroup's keys into LDS and (row tile
 // 0 only) into the caches.  K / V rows of new keys come from LDS instead of
 // the (possibly not yet written) cache rows.
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
-typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
-typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
-typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
-constexpr int kDecWaves = 8, kDecWaveKeys = 32, kDecKeys = kDecWaveKeys * kDecWaves;
+constexpr int kDecWaveKeys = 32;  // keys per wave
 constexpr int kDecMaxRows = 64;  // query rows per kv head on this path
 constexpr int kMergeRows = 8;    // rows merged per LDS pass
 constexpr int kFuseMaxM = 16;    // new tokens of the fused prologue
 constexpr int kQS = kD + 8;      // LDS row stride of the prologue's q / k rows
 constexpr int kCounters = 1024;  // arrival counters at the head of the workspace
+// Third word of a raw gfx9 buffer resource (no format conversion, range
+// checked against num_records in bytes)
+constexpr int kBufferConfig = 0x00020000;
 
 template <int RMAX, bool FUSED, int NW>
 __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p, const FuseParams f) {
@@ -183,34 +221,21 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
   const int tn = p.M;
   const int rep = p.Hq / p.Hkv;
   const int R = tn * rep;  // row r = j * tn + i: head kvh*rep + j, token i
-  const int kvh = blockIdx.x, split = blockIdx.y;
+  // splits in reverse launch order: the last, partly filled split goes out
+  // first, so that where a CU holds two workgroups the second is a full one
+  // and the short one does not queue its loads behind a full one's
+  const int kvh = blockIdx.x, split = gridDim.y - 1 - blockIdx.y;
   const int r0 = blockIdx.z * RMAX;   // first row of this workgroup's tile
   const int RT = min(RMAX, R - r0);   // rows in the tile
-  const int offset = p.offset_dev ? *p.offset_dev : p.offset;
-  const int L = offset + p.M;
-  // The grid holds a split per kps keys of the largest context the launch
-  // may see (a captured decode step: the cache capacity); only the first
-  // ns_live hold keys of this call's context.  The others leave before any
-  // load, and the arrival counter and the merge count only the live ones,
-  // so the cost follows the context, not the capacity.  (A split without
-  // visible keys contributes nothing to the merge either way: results are
-  // the same bits as with every split taking part.)
-  const int ns_live = min(p.ns, (L + p.kps - 1) / p.kps);
-  if (split >= ns_live) return;
-  // this workgroup's keys: [kbase, kbase + kps), of which those < kend exist
-  const int kbase = split * p.kps;
-  const int kend = min(L, kbase + p.kps);
-  const int c0 = kbase + wave * kDecWaveKeys;
-  const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
-  // ---- fused prologue, part 1: raw rows of this wave's items (issued first,
-  // so that waiting for them does not wait for the K / V loads) ----
-  // items: it < RT: q row r0 + it; else new token t_lo + it - RT
+  constexpr int KPS = kDecWaveKeys * NW;  // keys per split
+  // ---- fused prologue, part 1: the raw rows of this wave's items -- the
+  // tile's q rows, then the k / v rows of the M new tokens -- and the norm
+  // weights.  None depends on the cache position, so these loads go out
+  // together with the load of the position (one memory round trip for
+  // both); every load is unconditional, from a valid row, so that the waits
+  // for them come after the K / V stream is issued and count only these ----
+  // items: it < RT: q row r0 + it; else new token it - RT
   constexpr int kItems = FUSED ? (RMAX + kFuseMaxM + NW - 1) / NW : 0;
-  const int t_lo = max(0, kbase - offset);
-  const int t_hi = min(p.M, kbase + p.kps - offset);
-  const int n_items = RT + max(0, t_hi - t_lo);
-  // (every load unconditional, from a valid row, so that the waits for
-  // them come after the K / V stream is issued and count only these)
   constexpr int kI = kItems > 0 ? kItems : 1;
   uint16_t ra[kI], rb[kI], rv0[kI], rv1[kI], wa[kI], wb[kI];
   float freq = 0.0f;
@@ -221,7 +246,7 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
       const int it = wave + u * NW;
       const bool is_q = it < RT;
       const int rg = r0 + min(it, RT - 1), j = rg / tn, i = rg - j * tn;
-      const int64_t krow = static_cast<int64_t>(min(max(t_lo + it - RT, 0), p.M - 1)) * p.Hkv + kvh;
+      const int64_t krow = static_cast<int64_t>(min(max(it - RT, 0), p.M - 1)) * p.Hkv + kvh;
       const uint16_t* src = is_q ? p.q + (static_cast<int64_t>(i) * p.Hq + kvh * rep + j) * kD : f.k_new + krow * kD;
       const uint16_t* nw = is_q ? f.q_norm : f.k_norm;
       ra[u] = src[lane];
@@ -231,8 +256,27 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
       wa[u] = nw[lane];
       wb[u] = nw[lane + 64];
     }
-    __builtin_amdgcn_sched_barrier(0);
   }
+  const int offset = p.offset_dev ? *p.offset_dev : p.offset;
+  if constexpr (FUSED) __builtin_amdgcn_sched_barrier(0);
+  const int L = offset + p.M;
+  // The grid holds a split per KPS keys of the largest context the launch
+  // may see (a captured decode step: the cache capacity); only the first
+  // ns_live hold keys of this call's context.  The others leave before the
+  // K / V loads, and the arrival counter and the merge count only the live
+  // ones, so the cost follows the context, not the capacity.  (A split
+  // without visible keys contributes nothing to the merge either way:
+  // results are the same bits as with every split taking part.)
+  const int ns_live = min(p.ns, (L + KPS - 1) / KPS);
+  if (split >= ns_live) return;
+  // this workgroup's keys: [kbase, kbase + KPS), of which those < kend exist
+  const int kbase = split * KPS;
+  const int kend = min(L, kbase + KPS);
+  const int c0 = kbase + wave * kDecWaveKeys;
+  const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
+  // new tokens whose keys fall in this workgroup's range
+  const int t_lo = max(0, kbase - offset);
+  const int t_hi = min(p.M, kbase + KPS - offset);
   // ---- issue loads: q fragments, K fragments, V rows ----
   uint4 qa[4];
   if constexpr (!FUSED) {
@@ -240,34 +284,48 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) qa[ks] = *reinterpret_cast<const uint4*>(qrow + ks * 32);
   }
+  // K and V rows of this kv head through buffer resources that end at the
+  // L visible positions: a lane whose key lies beyond them gets zeros
+  // without a memory access (a raw buffer load past num_records), so a
+  // partly filled split moves only its keys' bytes
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.k) + hbase, static_cast<short>(0), L * kD * 2, kBufferConfig);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.v) + hbase, static_cast<short>(0), L * kD * 2, kBufferConfig);
   uint4 kb[2][4];
 #pragma unroll
   for (int t = 0; t < 2; t++) {
-    const int key = max(min(c0 + t * 16 + li, L - 1), 0);
-    const uint16_t* krow = p.k + hbase + static_cast<int64_t>(key) * kD + g * 8;
+    const int kofs = (c0 + t * 16 + li) * (kD * 2) + g * 16;
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++) kb[t][ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
+    for (int ks = 0; ks < 4; ks++)
+      kb[t][ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, kofs + ks * 64, 0, 0));
   }
   // V: lane holds dims 8 vc .. 8 vc + 7 of keys vq + 4 j, j < 8 (one 16-byte
   // load per key; an instruction reads 4 whole key rows)
   const int vc = lane & 15, vq = lane >> 4;
   uint4 vw[8];
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const int key = max(min(c0 + vq + 4 * j, L - 1), 0);
-    vw[j] = *reinterpret_cast<const uint4*>(p.v + hbase + static_cast<int64_t>(key) * kD + 8 * vc);
-  }
+  for (int j = 0; j < 8; j++)
+    vw[j] = __builtin_bit_cast(
+        uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, (c0 + vq + 4 * j) * (kD * 2) + 16 * vc, 0, 0));
   if constexpr (FUSED) {
-    // ---- fused prologue, part 2: norm + rope into LDS (and the caches) ----
+    // ---- fused prologue, part 2: norm + rope into LDS (and the caches).
+    // The rotation's cos / sin depend on the token only: a wave evaluates
+    // them once per token it meets (once in all for a decode step) ----
+    int ct = -1;
+    float rc = 1.0f, rs = 0.0f;
 #pragma unroll
     for (int u = 0; u < kItems; u++) {
       const int it = wave + u * NW;
-      if (it < n_items) {
-        const bool is_q = it < RT;
-        const int t = is_q ? (r0 + it) % tn : t_lo + it - RT;
+      const bool is_q = it < RT;
+      const int t = is_q ? (r0 + it) % tn : it - RT;
+      if (is_q || (t >= t_lo && t < t_hi)) {
+        if (t != ct) {
+          rope_cs(freq, static_cast<float>(offset + t), rc, rs);
+          ct = t;
+        }
         uint16_t o1, o2;
-        qk_norm_rope_lane(bf2f(ra[u]), bf2f(rb[u]), bf2f(wa[u]), bf2f(wb[u]), freq, static_cast<float>(offset + t),
-                          f.eps, o1, o2);
+        qk_norm_rope_lane_cs(bf2f(ra[u]), bf2f(rb[u]), bf2f(wa[u]), bf2f(wb[u]), rc, rs, f.eps, o1, o2);
         if (is_q) {
           qs[it][lane] = o1;
           qs[it][lane + 64] = o2;
@@ -364,9 +422,8 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
     for (int d = 0; d < 8; d++) acc[r][d] = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
-    // rows past this split's keys (clamped or another split's) are never
-    // weighted, and are zeroed so that stale contents cannot be NaN
-    const uint4 vj = (c0 + vq + 4 * j < kend) ? vw[j] : make_uint4(0, 0, 0, 0);
+    // rows past the visible keys came back as zeros (never weighted either)
+    const uint4 vj = vw[j];
     const uint32_t w4[4] = {vj.x, vj.y, vj.z, vj.w};
     float v[8];
 #pragma unroll
@@ -461,10 +518,23 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
   }
   __syncthreads();
   if (!last) return;
-  // (Two waves per row, each folding half of the splits and merged through
-  // LDS, measured 2% slower end to end.)
-  for (int r = wave; r < RT; r += NW)
-    store_pair(p, kvh * R + r0 + r, lane, combine_range(p, kvh * R + r0 + r, lane, 0, ns_live));
+  // one row per wave; with more rows than waves, a wave folds two rows with
+  // the loads of both in flight together
+  if (RT <= NW) {
+    if (wave < RT) {
+      const int wid[1] = {kvh * R + r0 + wave};
+      Fold r[1];
+      combine_splits<1>(p, wid, lane, ns_live, r);
+      store_fold(p, wid[0], lane, r[0]);
+    }
+  } else {
+    const int rb = min(wave + NW, RT - 1);
+    const int wid[2] = {kvh * R + r0 + wave, kvh * R + r0 + rb};
+    Fold r[2];
+    combine_splits<2>(p, wid, lane, ns_live, r);
+    store_fold(p, wid[0], lane, r[0]);
+    if (wave + NW < RT) store_fold(p, wid[1], lane, r[1]);
+  }
 }
 
 // Prefill / long verify: flash attention on MFMA.  A workgroup of 4 waves
@@ -669,8 +739,7 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
         sc[kt][i] = key < lim ? sc[kt][i] * scale2 : -INFINITY;
         mx = fmaxf(mx, sc[kt][i]);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = max_xor32(max_xor16(mx));
     const float m_new = fmaxf(m_run, mx);
     // 2^(-inf) = 0 covers the first block (m_run = -inf) and masked keys; a
     // row with nothing visible yet keeps m = -inf and is skipped
@@ -702,8 +771,7 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
       pa[c] = __builtin_bit_cast(bf16x8_t, make_uint4(ph[0], ph[1], ph[2], ph[3]));
       pr[c] = __builtin_bit_cast(f16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
     }
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
+    sum = add_xor32(add_xor16(sum));
     l_run = l_run * alpha + sum;
     m_run = m_new;
     // ---- rescale O (rows = queries 4 g + i) when a running max moved, then
@@ -778,6 +846,7 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   const int Hq = base.Hq, Hkv = base.Hkv, M = base.M;
   const int rep = Hq / Hkv, R = M * rep;
   if (!ws || R > kDecMaxRows || (fuse && M > kFuseMaxM)) return kNoFit;
+  if (!aligned(ws, 16)) return set_error(BMX_E_ALIGN, "attention: workspace must be 16-byte aligned");
   if (ws_floats < kCounters) return kNoFit;
   const int max_ns = static_cast<int>((ws_floats - kCounters) / (static_cast<size_t>(Hq) * M * (kD + 2)));
   // row tiles of 4 (decode: up to 4 q heads per kv head) or 8 rows; a
@@ -787,11 +856,16 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   // 4-row tiles throughout, 9.41 ms
   const int rmax = R <= 4 ? 4 : 8;
   const int tiles = (R + rmax - 1) / rmax;
-  // 256 keys per split (one per wave of 32 keys).  Smaller splits to spread
-  // a 4K context over all 256 CUs measured slower: the K / V stream is
-  // latency-bound (its first loads take ~3.5 us to return either way) and
-  // more splits lengthen the merge.
-  const int kps = kDecKeys;
+  // Keys per split: 32 per wave, 4 waves (128 keys) for caches of up to
+  // 8192 positions, else 8 waves (256 keys).  Each CU streams K / V at a
+  // bounded rate (~20 GB/s with this access pattern: the loads it can keep
+  // in flight over the memory latency), so a context has to spread over all
+  // CUs -- at 4096 positions, 8 kv heads x 33 splits of 128 keys against 8 x
+  // 17 of 256 -- while the splits stay few enough for one merge batch.  The
+  // split size is a function of the capacity only, so that every row of a
+  // cache (decode or verify) is partitioned alike.
+  const int nw = base.cap <= 8192 ? 4 : 8;
+  const int kps = kDecWaveKeys * nw;
   const int chunks = (L_max + kps - 1) / kps;
   if (chunks > max_ns) return kNoFit;
   if (Hkv * tiles > kCounters) return kNoFit;
@@ -804,18 +878,22 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   p.kps = kps;
   p.causal = M > 1 ? 1 : 0;
   const FuseParams f = fuse ? *fuse : FuseParams{};
-  const dim3 grid(Hkv, chunks, tiles), block(64 * kDecWaves);
-#define BMX_DECODE_LAUNCH(RM)                                                                   \
-  do {                                                                                          \
-    if (fuse)                                                                                   \
-      hipLaunchKernelGGL((attn_decode_kernel<RM, true, kDecWaves>), grid, block, 0, stream, p, f);  \
-    else                                                                                        \
-      hipLaunchKernelGGL((attn_decode_kernel<RM, false, kDecWaves>), grid, block, 0, stream, p, f); \
+  const dim3 grid(Hkv, chunks, tiles), block(64 * nw);
+#define BMX_DECODE_LAUNCH(RM, NW)                                                        \
+  do {                                                                                   \
+    if (fuse)                                                                            \
+      hipLaunchKernelGGL((attn_decode_kernel<RM, true, NW>), grid, block, 0, stream, p, f);  \
+    else                                                                                 \
+      hipLaunchKernelGGL((attn_decode_kernel<RM, false, NW>), grid, block, 0, stream, p, f); \
   } while (0)
-  if (rmax == 4)
-    BMX_DECODE_LAUNCH(4);
+  if (rmax == 4 && nw == 4)
+    BMX_DECODE_LAUNCH(4, 4);
+  else if (rmax == 4)
+    BMX_DECODE_LAUNCH(4, 8);
+  else if (nw == 4)
+    BMX_DECODE_LAUNCH(8, 4);
   else
-    BMX_DECODE_LAUNCH(8);
+    BMX_DECODE_LAUNCH(8, 8);
 #undef BMX_DECODE_LAUNCH
   return check_launch(fuse ? "attention_decode_fused" : "attention_decode");
 }

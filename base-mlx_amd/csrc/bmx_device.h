@@ -134,38 +134,6 @@ __device__ __forceinline__ float gemv_chunk(uint4 w, uint4 x0, uint4 x1, uint4 x
   return __builtin_fmaf(bb, sx, acc);
 }
 
-// Per-head RMSNorm (fp32 inside, bf16 result) followed by rotate-half RoPE
-// at angle pos * freq, for one head row of 128 held by a whole wave: lane
-// holds dims lane and lane + 64 (values a, b and norm weights wa, wb on
-// entry; the rotated bf16 pair on return).  QK-norm and rope of
-// Qwen3::forward_internal (crates/base-mlx-core/src/model/qwen3.rs:392-413).
-// Every kernel that norms and rotates q or k calls this, so they agree bit
-// for bit.
-// the same with the rotation's cos / sin given (they depend on the position
-// and lane only, so a wave over several heads of one token computes them once)
-__device__ __forceinline__ void qk_norm_rope_lane_cs(float a, float b, float wa, float wb, float c, float s,
-                                                     float eps, uint16_t& o1, uint16_t& o2) {
-  // the fused multiply-adds are written out, so every place this function
-  // is inlined rounds the same way
-  const float ss = wave_sum_xor(__builtin_fmaf(a, a, __fmul_rn(b, b)), 64);
-  const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
-  const float na = bf2f(f2bf(wa * round_bf(a * inv)));
-  const float nb = bf2f(f2bf(wb * round_bf(b * inv)));
-  o1 = f2bf(__builtin_fmaf(na, c, -__fmul_rn(nb, s)));
-  o2 = f2bf(__builtin_fmaf(nb, c, __fmul_rn(na, s)));
-}
-__device__ __forceinline__ void rope_cs(float freq, float pos, float& c, float& s) {
-  const float ang = pos * freq;
-  c = cosf(ang);
-  s = sinf(ang);
-}
-__device__ __forceinline__ void qk_norm_rope_lane(float a, float b, float wa, float wb, float freq, float pos,
-                                                  float eps, uint16_t& o1, uint16_t& o2) {
-  float c, s;
-  rope_cs(freq, pos, c, s);
-  qk_norm_rope_lane_cs(a, b, wa, wb, c, s, eps, o1, o2);
-}
-
 // DPP lane moves within 16-lane rows (gfx9 dpp_ctrl encodings):
 // quad_perm [1,0,3,2] = 0xB1 (lane ^ 1), quad_perm [2,3,0,1] = 0x4E
 // (lane ^ 2), row_ror:4 = 0x124 and row_ror:8 = 0x128 (rotations by 4 and 8
@@ -194,14 +162,70 @@ __device__ __forceinline__ float row16_sum(float v) {
 // of a group gets the group's sum.  Inside 16-lane rows with DPP: quad_perm
 // [1,0,3,2] (0xB1), quad_perm [2,3,0,1] (0x4E), row_half_mirror (0x141:
 // lane i <-> 7 - i within 8), row_mirror (0x140: lane i <-> 15 - i).
+// v + (v of lane ^ 16) and v + (v of lane ^ 32) through the gfx950 lane
+// swaps (v_permlane16_swap: odd 16-lane rows of one operand against even
+// rows of the other; v_permlane32_swap: the two 32-lane halves), one VALU
+// step each instead of a round trip through the LDS crossbar.  With both
+// operands v, the two results hold the pair's values in a fixed order, and
+// since a + b == b + a exactly, every lane gets the bits of the shuffle form.
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
 __device__ __forceinline__ float lanes_sum(float v, int S) {
   v += dpp_f32<0xB1>(v);
   v += dpp_f32<0x4E>(v);
   v += dpp_f32<0x141>(v);
   if (S >= 16) v += dpp_f32<0x140>(v);
-  if (S >= 32) v += __shfl_xor(v, 16, 64);
-  if (S >= 64) v += __shfl_xor(v, 32, 64);
+  if (S >= 32) v = add_xor16(v);
+  if (S >= 64) v = add_xor32(v);
   return v;
+}
+
+// Per-head RMSNorm (fp32 inside, bf16 result) followed by rotate-half RoPE
+// at angle pos * freq, for one head row of 128 held by a whole wave: lane
+// holds dims lane and lane + 64 (values a, b and norm weights wa, wb on
+// entry; the rotated bf16 pair on return).  QK-norm and rope of
+// Qwen3::forward_internal (crates/base-mlx-core/src/model/qwen3.rs:392-413).
+// Every kernel that norms and rotates q or k calls this, so they agree bit
+// for bit.
+// the same with the rotation's cos / sin given (they depend on the position
+// and lane only, so a wave over several heads of one token computes them once)
+__device__ __forceinline__ void qk_norm_rope_lane_cs(float a, float b, float wa, float wb, float c, float s,
+                                                     float eps, uint16_t& o1, uint16_t& o2) {
+  // the fused multiply-adds are written out, so every place this function
+  // is inlined rounds the same way
+  // the row's sum of squares: a symmetric butterfly (DPP inside 16-lane
+  // rows, lane swaps across them), every lane the same bits
+  const float ss = lanes_sum(__builtin_fmaf(a, a, __fmul_rn(b, b)), 64);
+  const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
+  const float na = bf2f(f2bf(wa * round_bf(a * inv)));
+  const float nb = bf2f(f2bf(wb * round_bf(b * inv)));
+  o1 = f2bf(__builtin_fmaf(na, c, -__fmul_rn(nb, s)));
+  o2 = f2bf(__builtin_fmaf(nb, c, __fmul_rn(na, s)));
+}
+__device__ __forceinline__ void rope_cs(float freq, float pos, float& c, float& s) {
+  const float ang = pos * freq;
+  c = cosf(ang);
+  s = sinf(ang);
+}
+__device__ __forceinline__ void qk_norm_rope_lane(float a, float b, float wa, float wb, float freq, float pos,
+                                                  float eps, uint16_t& o1, uint16_t& o2) {
+  float c, s;
+  rope_cs(freq, pos, c, s);
+  qk_norm_rope_lane_cs(a, b, wa, wb, c, s, eps, o1, o2);
 }
 
 // floor(a / b) for 0 <= a < 2^20 and b >= 1, from rcp_b = 1.0f / b (correctly

@@ -219,7 +219,7 @@ int bmx_qk_norm_rope_kv(const bmx_bf16 *q, const bmx_bf16 *k, const bmx_bf16 *v,
  * kv head h / (n_heads / n_kv_heads); for M > 1 query t sees keys
  * j <= offset + t.  `workspace` (may be NULL: no key split) holds arrival
  * counters and split partials; bmx_attention_workspace_bytes(n_heads, M) is
- * enough.  It must be zero-filled before its first use; every call leaves
+ * enough, 16-byte aligned.  It must be zero-filled before its first use; every call leaves
  * the counters zero again, so it is reused as is.  Calls that share one
  * workspace must not run concurrently.
  * Replaces: mlx_rs::fast::scaled_dot_product_attention with the
