@@ -856,15 +856,14 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   // 4-row tiles throughout, 9.41 ms
   const int rmax = R <= 4 ? 4 : 8;
   const int tiles = (R + rmax - 1) / rmax;
-  // Keys per split: 32 per wave, 4 waves (128 keys) for caches of up to
-  // 8192 positions, else 8 waves (256 keys).  Each CU streams K / V at a
-  // bounded rate (~20 GB/s with this access pattern: the loads it can keep
-  // in flight over the memory latency), so a context has to spread over all
-  // CUs -- at 4096 positions, 8 kv heads x 33 splits of 128 keys against 8 x
-  // 17 of 256 -- while the splits stay few enough for one merge batch.  The
-  // split size is a function of the capacity only, so that every row of a
-  // cache (decode or verify) is partitioned alike.
-  const int nw = base.cap <= 8192 ? 4 : 8;
+  // Keys per split: 32 per wave, 8 waves (256 keys).  Splits of 128 keys
+  // (4 waves: a 4K context over all CUs, 33 splits per kv head against 17)
+  // measured slower in the decode step at context 4096: 12.93 against 12.15
+  // us per layer -- the data phase shortens by ~1 us, but twice as many
+  // arrivals serialize on each kv head's counter (~0.1 us apiece).  The
+  // split size is fixed, so every row of a cache (decode or verify) is
+  // partitioned alike.
+  const int nw = 8;
   const int kps = kDecWaveKeys * nw;
   const int chunks = (L_max + kps - 1) / kps;
   if (chunks > max_ns) return kNoFit;

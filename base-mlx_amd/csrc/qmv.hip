@@ -627,6 +627,258 @@ int try_launch_qmv1(QmvEpilogue epi, int mt, int S, const QmvParams& p, int bloc
   }
 }
 
+// One-workgroup-per-CU GEMV for one row of x (the decode step's q|k|v, o,
+// gate|up and down projections).  A launch of one workgroup per CU (up to
+// 16 waves, a block of consecutive weight rows each) removes the load
+// ordering that holds the single-workgroup kernels back: every wave first
+// issues its staging loads (x, the norm weight, its rows' s|b), the
+// workgroup meets at a barrier -- so on each CU all of them are queued ahead
+// of any W load -- and then every lane issues its whole W stream at once;
+// the RMSNorm and the LDS staging run while W is on its way.  Each row is
+// computed with the operations of qmv1_kernel in the same order (the same S
+// lanes per row and chunk -> lane assignment, the norm's sums of squares
+// from the first 256 threads as qmv1 assigns them, the same chunk sums and
+// reductions), so its bits equal qmv1's for the same row.  Rows of a
+// workgroup may span q|k|v segments: a lane's segment follows its row.
+constexpr int kQmvcMaxThreads = 1024;
+constexpr int kQmvcMinLanes = 16;  // lanes per row from which it is used
+constexpr int kQmvcPreLoads = 64;  // W loads per CU issued ahead of the staging
+
+__device__ __forceinline__ int qmvc_seg_of(const QmvParams& p, int r) {
+  return (p.nseg > 2 && r >= p.seg[2].row0) ? 2 : (p.nseg > 1 && r >= p.seg[1].row0) ? 1 : 0;
+}
+// a field of segment sg (0..2) by selects, so that a per-lane segment does
+// not index the kernel-argument struct
+#define BMX_SEG_FIELD(p, sg, f) ((sg) == 0 ? (p).seg[0].f : (sg) == 1 ? (p).seg[1].f : (p).seg[2].f)
+
+template <int NI, int EPI, int XU, bool NORM, int NPRE>
+__global__ void __launch_bounds__(kQmvcMaxThreads) qmvc_kernel(const QmvParams p, const int S, const int rows_wg) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NH = (EPI == QMV_SWIGLU) ? 2 : 1;
+  const int lshift = __builtin_ctz(S);
+  const int SLOTS = 64 >> lshift;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int t256 = tid & (kThreads - 1);  // staging thread as qmv1 numbers it
+  const int slot = lane >> lshift;
+  const int sl = lane & (S - 1);
+  const int K = p.K;
+  const int G = K / 64, C = K / 32, W8 = K / 8, GU = G / 8;
+  // output rows: all segments in one numbering (SWIGLU: rows of one matrix)
+  const int n_rows = (EPI == QMV_SWIGLU) ? p.N : p.seg[p.nseg - 1].row0 + p.seg[p.nseg - 1].rows;
+  unsigned char* xs = smem;                                            // [C] x 80 B
+  float* sxs = reinterpret_cast<float*>(smem + C * kChunkBytes);       // [C]
+  uint32_t* sbs = reinterpret_cast<uint32_t*>(sxs + C);                // [NH][rows_wg][G]
+  float* red = reinterpret_cast<float*>(sbs + NH * rows_wg * G);       // [4]
+  const int wg_row0 = blockIdx.x * rows_wg;
+
+  // ---- 1. staging loads: x and the norm weight (units as qmv1's 256
+  // threads take them; waves past the fourth load copies they do not use),
+  // the workgroup's s|b units ----
+  uint4 xr[XU], nr[XU];
+#pragma unroll
+  for (int i = 0; i < XU; i++) {
+    const int idx = min(i * kThreads + t256, W8 - 1);
+    xr[i] = *reinterpret_cast<const uint4*>(p.x + idx * 8);
+    if constexpr (NORM) nr[i] = *reinterpret_cast<const uint4*>(p.norm_w + idx * 8);
+  }
+  const int sb_units = rows_wg * GU;
+  const float rcp_gu = 1.0f / static_cast<float>(GU);
+  const int e_sb = min(tid, sb_units - 1);
+  const int r_sb = udiv_small(e_sb, rcp_gu);  // row within the workgroup
+  const int gr_sb = min(wg_row0 + r_sb, n_rows - 1);
+  const int sg_sb = qmvc_seg_of(p, gr_sb);
+  uint4 sr[NH], br[NH];
+#pragma unroll
+  for (int h = 0; h < NH; h++) {
+    const int sg = EPI == QMV_SWIGLU ? h : sg_sb;
+    const int lr = EPI == QMV_SWIGLU ? gr_sb : gr_sb - BMX_SEG_FIELD(p, sg, row0);
+    const int64_t off = static_cast<int64_t>(lr) * G + (e_sb - r_sb * GU) * 8;
+    sr[h] = *reinterpret_cast<const uint4*>(BMX_SEG_FIELD(p, sg, s) + off);
+    br[h] = *reinterpret_cast<const uint4*>(BMX_SEG_FIELD(p, sg, b) + off);
+  }
+  // every staging load of the CU is issued before any W load
+  __syncthreads();
+
+  // ---- 2. the whole W stream of the lane, chunk by chunk ----
+  const int rl = wave * SLOTS + slot;  // row within the workgroup
+  const int grow = wg_row0 + rl;
+  const bool valid = grow < n_rows;
+  const int gr = min(grow, n_rows - 1);
+  const int sg_w = EPI == QMV_SWIGLU ? 0 : qmvc_seg_of(p, gr);
+  const int lrow = EPI == QMV_SWIGLU ? gr : gr - BMX_SEG_FIELD(p, sg_w, row0);
+  const uint32_t* wrow[NH];
+#pragma unroll
+  for (int h = 0; h < NH; h++) {
+    const int sg = EPI == QMV_SWIGLU ? h : sg_w;
+    wrow[h] = BMX_SEG_FIELD(p, sg, w) + static_cast<int64_t>(lrow) * (K / 8);
+  }
+  uint4 wv[NI][NH];
+  auto issue_w = [&](int u) {
+    const int c = min(sl + (u << lshift), C - 1);
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[h] + c * 4));
+      wv[u][h] = make_uint4(t.x, t.y, t.z, t.w);
+    }
+  };
+  // the first NPRE chunks now, the rest once x and s|b are staged: a wave
+  // with more loads than the CU's load queue takes stalls at issue, and the
+  // first four waves still have the staging to do
+#pragma unroll
+  for (int u = 0; u < NPRE; u++) issue_w(u);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 3. fused RMSNorm (fast::rms_norm, qwen3.rs:50-55): the sums of
+  // squares of the first four waves, as in qmv1 ----
+  float inv = 1.0f;
+  if constexpr (NORM) {
+    if (wave < 4) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < XU; i++) {
+        if (i * kThreads >= W8) break;
+        if (i * kThreads + t256 < W8) ss = gemv_ss_unit(xr[i], ss);
+      }
+      ss = lanes_sum(ss, 64);
+      if (lane == 0) red[wave] = ss;
+    }
+    __syncthreads();
+    inv = gemv_norm_inv(red[0], red[1], red[2], red[3], K, p.eps);
+  }
+  // ---- 4. x (pair-permuted, chunk sums) and s|b into LDS ----
+  if (wave < 4) {
+#pragma unroll
+    for (int i = 0; i < XU; i++) {
+      if (i * kThreads >= W8) break;
+      const int idx = i * kThreads + t256;
+      const bool act = idx < W8;
+      uint4 d = xr[i];
+      float part = 0.0f;
+      if (act) {
+        if constexpr (NORM) d = gemv_norm_unit(d, nr[i], inv);
+        part = gemv_unit_sum(d);
+      }
+      part += dpp_f32<0xB1>(part);
+      part += dpp_f32<0x4E>(part);
+      if (act) {
+        *reinterpret_cast<uint4*>(xs + (idx >> 2) * kChunkBytes + (idx & 3) * 16) = permute_pairs(d);
+        if ((idx & 3) == 0) sxs[idx >> 2] = part;
+      }
+    }
+  }
+  if (tid < sb_units && wg_row0 + r_sb < n_rows) {
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      const uint32_t s4[4] = {sr[h].x, sr[h].y, sr[h].z, sr[h].w};
+      const uint32_t b4[4] = {br[h].x, br[h].y, br[h].z, br[h].w};
+      uint32_t* dst = sbs + (h * rows_wg + r_sb) * G + (e_sb - r_sb * GU) * 8;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        dst[2 * q] = (s4[q] & 0xffffu) | (b4[q] << 16);
+        dst[2 * q + 1] = (s4[q] >> 16) | (b4[q] & 0xffff0000u);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = NPRE; u < NI; u++) issue_w(u);
+  __syncthreads();
+  // ---- 5. dot products, chunk by chunk as the W stream arrives ----
+  const NibbleK nk = nibble_consts();
+  float acc[NH];
+#pragma unroll
+  for (int h = 0; h < NH; h++) acc[h] = 0.0f;
+#pragma unroll
+  for (int u = 0; u < NI; u++) {
+    const int c = sl + (u << lshift);
+    if (c < C) {
+      float sv[NH], bb[NH];
+#pragma unroll
+      for (int h = 0; h < NH; h++) gemv_sb(sbs[(h * rows_wg + rl) * G + (c >> 1)], sv[h], bb[h]);
+      const uint4* xp = reinterpret_cast<const uint4*>(xs + c * kChunkBytes);
+      const uint4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+      const float sx = sxs[c];
+#pragma unroll
+      for (int h = 0; h < NH; h++) acc[h] = gemv_chunk(wv[u][h], x0, x1, x2, x3, sv[h], bb[h], sx, acc[h], nk);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // ---- 6. reduce the S lanes of each row, epilogue ----
+#pragma unroll
+  for (int h = 0; h < NH; h++) acc[h] = lanes_sum(acc[h], S);
+  if (sl == 0 && valid) {
+    if constexpr (EPI == QMV_STORE)
+      BMX_SEG_FIELD(p, sg_w, y)[lrow] = f2bf(acc[0]);  // a lane's segment, by selects
+    else
+      gemv_store<EPI>(p, 0, 0, p.N, lrow, acc[0], acc[NH - 1]);
+  }
+}
+#undef BMX_SEG_FIELD
+
+template <int NI, int XU, int NPRE>
+int launch_qmvc_xu(QmvEpilogue epi, int S, const QmvParams& p, int blocks, int threads, int rows_wg, size_t lds,
+                   hipStream_t st) {
+  const bool norm = p.norm_w != nullptr;
+  auto go = [&](auto kern) {
+    if (int rc = allow_lds(kern, lds)) return rc;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(threads), lds, st, p, S, rows_wg);
+    return check_launch("qmvc");
+  };
+  switch (epi) {
+    case QMV_STORE:
+      return norm ? go(qmvc_kernel<NI, QMV_STORE, XU, true, NPRE>) : go(qmvc_kernel<NI, QMV_STORE, XU, false, NPRE>);
+    case QMV_RESIDUAL:
+      return norm ? kNoFit : go(qmvc_kernel<NI, QMV_RESIDUAL, XU, false, NPRE>);
+    default:
+      return norm ? go(qmvc_kernel<NI, QMV_SWIGLU, XU, true, NPRE>) : kNoFit;
+  }
+}
+
+// Launches the one-workgroup-per-CU GEMV when it applies: one row of x, no
+// argmax partials, K within the single-phase limits, a workgroup of at most
+// 16 waves whose s|b units fit one per thread.  kNoFit otherwise.
+int try_launch_qmvc(QmvEpilogue epi, int S, const QmvParams& p, hipStream_t st) {
+  if (p.m != 1 || p.amax || !p.sb_vec || p.K / 8 > kThreads * kXU1) return kNoFit;
+  if (S < kQmvcMinLanes) return kNoFit;
+  const int C = p.K / 32, G = p.K / 64;
+  const int slots = 64 / S;
+  const int n_rows = epi == QMV_SWIGLU ? p.N : p.seg[p.nseg - 1].row0 + p.seg[p.nseg - 1].rows;
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  const int per_cu = (n_rows + cus - 1) / cus;
+  const int waves = (per_cu + slots - 1) / slots;
+  if (waves < 4 || waves > kQmvcMaxThreads / 64) return kNoFit;
+  const int rows_wg = waves * slots;
+  if (rows_wg * (G / 8) > waves * 64) return kNoFit;
+  const int blocks = (n_rows + rows_wg - 1) / rows_wg;
+  const int nh = epi == QMV_SWIGLU ? 2 : 1;
+  const size_t lds = static_cast<size_t>(C) * (kChunkBytes + 4) + static_cast<size_t>(nh) * rows_wg * G * 4 + 16;
+  if (lds > 64 * 1024) return kNoFit;
+  const int ni = (C + S - 1) / S;
+  const int xu = qmv1_xu(p.K);
+  // W loads issued ahead of the staging: all of them while the CU's waves
+  // have at most kQmvcPreLoads in all, else two chunks per lane
+  const bool all_pre = waves * nh * ni <= kQmvcPreLoads;
+  auto by_ni = [&](auto xu_c) {
+    constexpr int XU = decltype(xu_c)::value;
+    if (ni <= 2) return launch_qmvc_xu<2, XU, 2>(epi, S, p, blocks, waves * 64, rows_wg, lds, st);
+    if (ni <= 3)
+      return all_pre ? launch_qmvc_xu<3, XU, 3>(epi, S, p, blocks, waves * 64, rows_wg, lds, st)
+                     : launch_qmvc_xu<3, XU, 2>(epi, S, p, blocks, waves * 64, rows_wg, lds, st);
+    if (ni <= 5)
+      return all_pre ? launch_qmvc_xu<5, XU, 5>(epi, S, p, blocks, waves * 64, rows_wg, lds, st)
+                     : launch_qmvc_xu<5, XU, 2>(epi, S, p, blocks, waves * 64, rows_wg, lds, st);
+    return kNoFit;
+  };
+  return xu == 2 ? by_ni(std::integral_constant<int, 2>{}) : by_ni(std::integral_constant<int, kXU1>{});
+}
+
 // Persistent GEMV for M <= 8 rows of x with the whole K in LDS.  About two
 // workgroups per CU stage x once (with the fused RMSNorm for M = 1) and then
 // stream their share of row tiles (RB rows each; a tile is what one
@@ -1067,6 +1319,10 @@ int launch_qmv(QmvParams p, QmvEpilogue epi, hipStream_t stream) {
   const bool amax_multi = p.amax != nullptr && mt > 1;
   if (rows_total >= kPersistentRows && !amax_multi) {
     const int rc = try_launch_qmvp(epi, mt, S, p, blocks, stream);
+    if (rc != kNoFit) return rc;
+  }
+  if (mt == 1) {
+    const int rc = try_launch_qmvc(epi, S, p, stream);
     if (rc != kNoFit) return rc;
   }
   if (!amax_multi) {
