@@ -723,9 +723,9 @@ __global__ void __launch_bounds__(kQmvcMaxThreads) qmvc_kernel(const QmvParams p
       wv[u][h] = make_uint4(t.x, t.y, t.z, t.w);
     }
   };
-  // the first NPRE chunks now, the rest once x and s|b are staged: a wave
-  // with more loads than the CU's load queue takes stalls at issue, and the
-  // first four waves still have the staging to do
+  // the first NPRE chunks now, the rest behind the dot products: a wave with
+  // more loads than the CU's load queue takes stalls at issue, which would
+  // hold the staging barrier below
 #pragma unroll
   for (int u = 0; u < NPRE; u++) issue_w(u);
   __builtin_amdgcn_sched_barrier(0);
@@ -781,10 +781,11 @@ __global__ void __launch_bounds__(kQmvcMaxThreads) qmvc_kernel(const QmvParams p
       }
     }
   }
-#pragma unroll
-  for (int u = NPRE; u < NI; u++) issue_w(u);
   __syncthreads();
-  // ---- 5. dot products, chunk by chunk as the W stream arrives ----
+  // ---- 5. dot products, chunk by chunk as the W stream arrives; the
+  // chunks not yet issued go out one by one behind the products (after
+  // chunk u, chunk u + NPRE), so no wave waits at a barrier while its loads
+  // queue ----
   const NibbleK nk = nibble_consts();
   float acc[NH];
 #pragma unroll
@@ -802,6 +803,7 @@ __global__ void __launch_bounds__(kQmvcMaxThreads) qmvc_kernel(const QmvParams p
 #pragma unroll
       for (int h = 0; h < NH; h++) acc[h] = gemv_chunk(wv[u][h], x0, x1, x2, x3, sv[h], bb[h], sx, acc[h], nk);
     }
+    if (u + NPRE < NI) issue_w(u + NPRE);
     __builtin_amdgcn_sched_barrier(0);
   }
   // ---- 6. reduce the S lanes of each row, epilogue ----
