@@ -301,13 +301,19 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
       kb[t][ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, kofs + ks * 64, 0, 0));
   }
   // V: lane holds dims 8 vc .. 8 vc + 7 of keys vq + 4 j, j < 8 (one 16-byte
-  // load per key; an instruction reads 4 whole key rows)
+  // load per key; an instruction reads 4 whole key rows).  With the fused
+  // prologue the V loads go out after its barrier: a wave whose loads
+  // outrun the CU's load queue stalls at issue, and with K and V both ahead
+  // of the barrier every wave's prologue waited for the slowest issuer
   const int vc = lane & 15, vq = lane >> 4;
   uint4 vw[8];
+  auto issue_v = [&]() {
 #pragma unroll
-  for (int j = 0; j < 8; j++)
-    vw[j] = __builtin_bit_cast(
-        uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, (c0 + vq + 4 * j) * (kD * 2) + 16 * vc, 0, 0));
+    for (int j = 0; j < 8; j++)
+      vw[j] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, (c0 + vq + 4 * j) * (kD * 2) + 16 * vc, 0, 0));
+  };
+  if constexpr (!FUSED) issue_v();
   if constexpr (FUSED) {
     // ---- fused prologue, part 2: norm + rope into LDS (and the caches).
     // The rotation's cos / sin depend on the token only: a wave evaluates
@@ -361,13 +367,7 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
         for (int ks = 0; ks < 4; ks++) kb[t][ks] = *reinterpret_cast<const uint4*>(&kn[tt][ks * 32 + g * 8]);
       }
     }
-    if (t_hi > t_lo) {
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const int tt = c0 + vq + 4 * j - offset;
-        if (tt >= t_lo && tt < t_hi) vw[j] = *reinterpret_cast<const uint4*>(&vn[tt][8 * vc]);
-      }
-    }
+    issue_v();
   }
   if (li >= RT) qa[0] = qa[1] = qa[2] = qa[3] = make_uint4(0, 0, 0, 0);
   // ---- S = q K^T on MFMA ----
@@ -422,8 +422,14 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
     for (int d = 0; d < 8; d++) acc[r][d] = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
-    // rows past the visible keys came back as zeros (never weighted either)
-    const uint4 vj = vw[j];
+    // rows past the visible keys came back as zeros (never weighted either);
+    // the rows of this call's new tokens come from LDS (the cache rows may
+    // not be written yet)
+    uint4 vj = vw[j];
+    if constexpr (FUSED) {
+      const int tt = c0 + vq + 4 * j - offset;
+      if (tt >= t_lo && tt < t_hi) vj = *reinterpret_cast<const uint4*>(&vn[tt][8 * vc]);
+    }
     const uint32_t w4[4] = {vj.x, vj.y, vj.z, vj.w};
     float v[8];
 #pragma unroll
