@@ -642,7 +642,8 @@ int try_launch_qmv1(QmvEpilogue epi, int mt, int S, const QmvParams& p, int bloc
 // workgroup may span q|k|v segments: a lane's segment follows its row.
 constexpr int kQmvcMaxThreads = 1024;
 constexpr int kQmvcMinLanes = 16;  // lanes per row from which it is used
-constexpr int kQmvcPreLoads = 64;  // W loads per CU issued ahead of the staging
+constexpr int kQmvcPreLoads = 40;   // W loads per CU all issued ahead of the staging
+constexpr int kQmvcPipeLoads = 32;  // else about this many, the rest pipelined
 
 __device__ __forceinline__ int qmvc_seg_of(const QmvParams& p, int r) {
   return (p.nseg > 2 && r >= p.seg[2].row0) ? 2 : (p.nseg > 1 && r >= p.seg[1].row0) ? 1 : 0;
@@ -864,18 +865,25 @@ int try_launch_qmvc(QmvEpilogue epi, int S, const QmvParams& p, hipStream_t st) 
   if (lds > 64 * 1024) return kNoFit;
   const int ni = (C + S - 1) / S;
   const int xu = qmv1_xu(p.K);
-  // W loads issued ahead of the staging: all of them while the CU's waves
-  // have at most kQmvcPreLoads in all, else two chunks per lane
-  const bool all_pre = waves * nh * ni <= kQmvcPreLoads;
+  // W chunks issued ahead of the staging (the rest go out behind the
+  // products): all of them while the CU's waves have at most kQmvcPreLoads
+  // loads in all, else about kQmvcPipeLoads, at least two chunks per lane.
+  // Probe timings per launch (eager, weights rotated over 1 GiB), chunks
+  // ahead 1 / 2 / 3 / all: gate|up SwiGLU 9728 x 2560 8.63 / 7.79 / 8.64 /
+  // 9.71 us; 9728 x 2560 store 6.44 / 5.51 / 5.46 / 5.61; down 2560 x 9728
+  // - / 6.34 / 6.07 / 6.11; q|k|v 5.84 / 5.26 / 5.10 (all).
+  const int per_lane = waves * nh;
+  const int npre = per_lane * ni <= kQmvcPreLoads ? ni : std::min(ni, std::max(2, kQmvcPipeLoads / per_lane));
   auto by_ni = [&](auto xu_c) {
     constexpr int XU = decltype(xu_c)::value;
     if (ni <= 2) return launch_qmvc_xu<2, XU, 2>(epi, S, p, blocks, waves * 64, rows_wg, lds, st);
     if (ni <= 3)
-      return all_pre ? launch_qmvc_xu<3, XU, 3>(epi, S, p, blocks, waves * 64, rows_wg, lds, st)
-                     : launch_qmvc_xu<3, XU, 2>(epi, S, p, blocks, waves * 64, rows_wg, lds, st);
+      return npre == 3 ? launch_qmvc_xu<3, XU, 3>(epi, S, p, blocks, waves * 64, rows_wg, lds, st)
+                       : launch_qmvc_xu<3, XU, 2>(epi, S, p, blocks, waves * 64, rows_wg, lds, st);
     if (ni <= 5)
-      return all_pre ? launch_qmvc_xu<5, XU, 5>(epi, S, p, blocks, waves * 64, rows_wg, lds, st)
-                     : launch_qmvc_xu<5, XU, 2>(epi, S, p, blocks, waves * 64, rows_wg, lds, st);
+      return npre == 5   ? launch_qmvc_xu<5, XU, 5>(epi, S, p, blocks, waves * 64, rows_wg, lds, st)
+             : npre >= 3 ? launch_qmvc_xu<5, XU, 3>(epi, S, p, blocks, waves * 64, rows_wg, lds, st)
+                         : launch_qmvc_xu<5, XU, 2>(epi, S, p, blocks, waves * 64, rows_wg, lds, st);
     return kNoFit;
   };
   return xu == 2 ? by_ni(std::integral_constant<int, 2>{}) : by_ni(std::integral_constant<int, kXU1>{});
