@@ -202,7 +202,13 @@ constexpr int kDecMaxRows = 64;  // query rows per kv head on this path
 constexpr int kMergeRows = 8;    // rows merged per LDS pass
 constexpr int kFuseMaxM = 16;    // new tokens of the fused prologue
 constexpr int kQS = kD + 8;      // LDS row stride of the prologue's q / k rows
-constexpr int kCounters = 1024;  // arrival counters at the head of the workspace
+// Arrival counters at the head of the workspace, one per (kv head, row
+// tile), each in its own 256-byte block: agent-scope atomics on one memory
+// line complete one after another, so counters packed into one line made
+// the arrivals of every kv head queue on each other
+constexpr int kCounterStride = 64;                        // uints
+constexpr int kMaxCounters = 64;                          // kv heads x row tiles
+constexpr int kCounters = kMaxCounters * kCounterStride;  // floats
 // Third word of a raw gfx9 buffer resource (no format conversion, range
 // checked against num_records in bytes)
 constexpr int kBufferConfig = 0x00020000;
@@ -518,8 +524,9 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
     // acquires (an agent-scope acquire fence after reading the final
     // count), so only that workgroup pays the cache invalidation; its
     // threads read the partials after the next barrier.
-    last = __builtin_amdgcn_atomic_inc32(p.cnt + kvh * gridDim.z + blockIdx.z, static_cast<unsigned>(ns_live - 1),
-                                         __ATOMIC_RELEASE, "agent") == static_cast<unsigned>(ns_live - 1);
+    last = __builtin_amdgcn_atomic_inc32(p.cnt + (kvh * gridDim.z + blockIdx.z) * kCounterStride,
+                                         static_cast<unsigned>(ns_live - 1), __ATOMIC_RELEASE,
+                                         "agent") == static_cast<unsigned>(ns_live - 1);
     if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
@@ -873,7 +880,7 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   const int kps = kDecWaveKeys * nw;
   const int chunks = (L_max + kps - 1) / kps;
   if (chunks > max_ns) return kNoFit;
-  if (Hkv * tiles > kCounters) return kNoFit;
+  if (Hkv * tiles > kMaxCounters) return kNoFit;
   AttnParams p = base;
   p.cnt = reinterpret_cast<unsigned*>(ws);
   p.part_o = ws + kCounters;
