@@ -59,19 +59,27 @@ struct FuseParams {
 };
 
 // The split partials travel between workgroups on different XCDs (each with
-// its own L2).  The writers store them with agent-scope atomic stores
-// (relaxed, issued with sc1: written through to memory), every thread waits
-// for its stores, the workgroup meets at a barrier, and one thread bumps the
-// arrival counter with an agent-scope release; the last arrival takes an
-// agent-scope acquire fence, and after the next barrier its threads read the
-// partials with ordinary loads.  Release, acquire and the two workgroup
-// barriers order the stores before the loads (message passing in the
-// memory model), whatever else either workgroup stores.
+// its own L2).  Every access to them is agent-coherent: the writers store
+// them with agent-scope atomic stores (relaxed, issued with sc1: written
+// through to memory), every thread waits for its stores to complete
+// (s_waitcnt), the workgroup meets at a barrier, and one thread bumps the
+// arrival counter (a relaxed agent-scope atomic); after the next barrier
+// the last arrival's threads read the partials with sc1 loads, which are
+// served coherently across the L2s.  The stores have completed before the
+// increment is issued and the loads are issued after it returned, so the
+// loads see them; no L2 write-back (release) or invalidation (acquire) is
+// needed, and these cost microseconds when many workgroups issue them.
 // Pairs of floats are stored as one 8-byte access (8-byte aligned addresses).
 __device__ __forceinline__ void store_agent2(float* a, float x, float y) {
   const uint64_t v = static_cast<uint64_t>(__float_as_uint(x)) | (static_cast<uint64_t>(__float_as_uint(y)) << 32);
   __hip_atomic_store(reinterpret_cast<uint64_t*>(a), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// Third word of a raw gfx9 buffer resource (no format conversion, range
+// checked against num_records in bytes)
+constexpr int kBufferConfig = 0x00020000;
+// Buffer-load cache policy sc1: agent-coherent
+constexpr int kAgentCoherent = 16;
 
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
@@ -112,11 +120,20 @@ __device__ __forceinline__ void combine_splits(const AttnParams& p, const int (&
     f32x4_t ov[NR][B];
 #pragma unroll
     for (int i = 0; i < NR; i++) {
-      const int64_t base = static_cast<int64_t>(wids[i]) * p.ns + s0;
-      ml[i] = *reinterpret_cast<const f32x2_t*>(p.part_ml + (base + min(lane, nb - 1)) * 2);
+      // wids[i] is the same in every lane (it follows from the wave index);
+      // reading it from lane 0 lets the buffer resources live in scalar
+      // registers
+      const int64_t base = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(wids[i])) * p.ns + s0;
+      const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(
+          p.part_ml + base * 2, static_cast<short>(0), nb * 8, kBufferConfig);
+      const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+          p.part_o + base * kD, static_cast<short>(0), nb * kD * 4, kBufferConfig);
+      ml[i] = __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rml, min(lane, nb - 1) * 8, 0,
+                                                                               kAgentCoherent));
 #pragma unroll
       for (int u = 0; u < B; u++)
-        ov[i][u] = *reinterpret_cast<const f32x4_t*>(p.part_o + (base + min(2 * u + half, nb - 1)) * kD + dl);
+        ov[i][u] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   ro, (min(2 * u + half, nb - 1) * kD + dl) * 4, 0, kAgentCoherent));
     }
     // every load of the batch goes out before any use of the first
     __builtin_amdgcn_sched_barrier(0);
@@ -209,10 +226,6 @@ constexpr int kQS = kD + 8;      // LDS row stride of the prologue's q / k rows
 constexpr int kCounterStride = 64;                        // uints
 constexpr int kMaxCounters = 64;                          // kv heads x row tiles
 constexpr int kCounters = kMaxCounters * kCounterStride;  // floats
-// Third word of a raw gfx9 buffer resource (no format conversion, range
-// checked against num_records in bytes)
-constexpr int kBufferConfig = 0x00020000;
-
 template <int RMAX, bool FUSED, int NW>
 __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p, const FuseParams f) {
   __shared__ __align__(16) float ps[NW][kDecWaveKeys][RMAX];
@@ -516,18 +529,14 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
   __syncthreads();
   if (threadIdx.x == 0) {
-    // Arrival: an agent-scope release increment that wraps to 0 on the
+    // Arrival: a relaxed agent-scope increment that wraps to 0 on the
     // ns_live-th arrival (ready for the next call).  Every thread's partial
-    // stores completed before the barrier above, and the release orders
-    // them (and every other store of this workgroup) before the increment
-    // for any workgroup that acquires the count.  Only the last arrival
-    // acquires (an agent-scope acquire fence after reading the final
-    // count), so only that workgroup pays the cache invalidation; its
-    // threads read the partials after the next barrier.
+    // stores (agent-coherent) completed before the barrier above; the last
+    // arrival's threads read the partials with agent-coherent loads after
+    // the next barrier.
     last = __builtin_amdgcn_atomic_inc32(p.cnt + (kvh * gridDim.z + blockIdx.z) * kCounterStride,
-                                         static_cast<unsigned>(ns_live - 1), __ATOMIC_RELEASE,
+                                         static_cast<unsigned>(ns_live - 1), __ATOMIC_RELAXED,
                                          "agent") == static_cast<unsigned>(ns_live - 1);
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (!last) return;

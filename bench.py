@@ -69,7 +69,7 @@ def _profile_value(name, key):
 
 
 TRAFFIC_PROFILE = "decode_attention_ctx4096_pmc.md"
-TRACE_PROFILE = "bench_default_qwen3_4b_decode.md"
+TRACE_PROFILE = "decode_attention_ctx4096_pmc.md"
 
 
 def measured_traffic():
@@ -82,8 +82,9 @@ def measured_traffic():
 
 def traced_duration_us():
     """Average duration of the roofline kernel in the committed rocprofv3
-    kernel trace of the default bench command (the tracer's per-dispatch
-    timestamps; not measured in this run, whose `achieved` uses HIP events
+    kernel trace of the counter workload (`--profile-roofline`: the same
+    launch at position 4096 over 36 layer caches; the tracer's per-dispatch
+    timestamps, not measured in this run, whose `achieved` uses HIP events
     around graph replays); None when that summary is absent."""
     return _profile_value(TRACE_PROFILE, "roofline_kernel_trace_avg_us")
 
@@ -633,8 +634,8 @@ def main():
                       f"Qwen3-4B heads, token at position {ATT_CTX}",
             "avg_launch_us": round(att_us, 3), "bytes_per_launch": att_bytes,
             "traffic_from": f"profiles/{TRAFFIC_PROFILE} (rocprofv3 --pmc; not measured in this run)",
-            "trace_avg_us": tr, "trace_avg_us_from": f"profiles/{TRACE_PROFILE} (rocprofv3 kernel trace of the "
-                                                      f"default bench command; not measured in this run)",
+            "trace_avg_us": tr, "trace_avg_us_from": f"profiles/{TRACE_PROFILE} (rocprofv3 kernel trace of "
+                                                      f"bench.py --profile-roofline; not measured in this run)",
             "frac_trace": None if tr is None else round(att_bytes / tr / 1e3 / HBM_PEAK_GBS, 4)}
     log(f"decode attention at position {ATT_CTX}: {att_us:.2f} us per launch, {att_gbs:.0f} GB/s "
         f"({100 * att_gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
