@@ -69,6 +69,10 @@ struct FuseParams {
 // increment is issued and the loads are issued after it returned, so the
 // loads see them; no L2 write-back (release) or invalidation (acquire) is
 // needed, and these cost microseconds when many workgroups issue them.
+// This holds only while store_agent2 (and the s_waitcnt before the arrival)
+// stays the only way the partials are written: a plain store into the
+// split workspace could sit in one XCD's L2, and would need the release
+// increment and the acquire fence back.
 // Pairs of floats are stored as one 8-byte access (8-byte aligned addresses).
 __device__ __forceinline__ void store_agent2(float* a, float x, float y) {
   const uint64_t v = static_cast<uint64_t>(__float_as_uint(x)) | (static_cast<uint64_t>(__float_as_uint(y)) << 32);
