@@ -575,10 +575,13 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
 //     as its 8-wide k slice in that order;
 //   O += P V with B = V^T from LDS, staged transposed (4 keys x 8 dims per
 //     thread, transposed in registers) so that the same 8 keys are two
-//     8-byte reads.  p enters the product as bf16(p) against V in bf16
-//     plus its residual in fp16 against a fp16 copy of V^T (two MFMAs, p
-//     to ~2^-20), and the row sums add it unrounded; O and the softmax
-//     statistics are fp32.  The
+//     8-byte reads.  p enters the product in fp16 against a fp16 copy of
+//     V^T (one MFMA, p to 2^-11: the end-to-end logits sit at the
+//     summation-order floor of the fp32 oracle with it, as with two
+//     terms); a key block holding a V value beyond fp16's range (seen
+//     while staging it) takes two terms instead -- bf16(p) against V in
+//     bf16 plus the residual p - bf16(p) in fp16 -- and the row sums add p
+//     unrounded; O and the softmax statistics are fp32.  The
 //     softmax runs in base 2 (v_exp_f32 on scores pre-multiplied by log2 e),
 //     and O is rescaled only in blocks where some row's running max moved.
 // The K and V^T tiles are double-buffered: the loads of key block j+1 are
@@ -595,14 +598,18 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
 constexpr int kFaQ = 64, kFaK = 64;  // queries per 4-wave workgroup, keys per block
 constexpr int kFaKS = kD + 8;        // K tile row stride (elements)
 constexpr int kFaVS = kFaK + 8;      // V^T tile row stride (elements)
-// K, V^T (bf16) and V^T (fp16, for the residual term of p), double-buffered
+// K, V^T (bf16) and V^T (fp16), double-buffered
 constexpr size_t kFaLds = 2ull * (kFaK * kFaKS + 2 * kD * kFaVS) * sizeof(uint16_t);
+// one bit per key block: a V value of the block lies beyond fp16's range;
+// blocks past the bits (beyond 262144 keys) always take the two terms
+constexpr int kFaSatWords = 128;
 
 template <int NW, int HG>
 __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams p) {
   static_assert((NW == 4 && HG == 1) || (NW == 8 && 8 % HG == 0), "workgroup shape");
   constexpr int TQ = 16 * NW / HG;  // tokens per workgroup
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ unsigned vsat[kFaSatWords];
   uint16_t* kt_s = reinterpret_cast<uint16_t*>(smem);  // [2][kFaK][kFaKS]
   uint16_t* vt_s = kt_s + 2 * kFaK * kFaKS;             // [2][kD][kFaVS]
   uint16_t* vh_s = vt_s + 2 * kD * kFaVS;               // [2][kD][kFaVS] fp16
@@ -676,7 +683,7 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     }
     return r;
   };
-  auto store_block = [&](const Stage r, int buf) {
+  auto store_block = [&](const Stage r, int buf, int blk) {
     uint16_t* kb = kt_s + buf * kFaK * kFaKS;
     auto kput = [&](int i, const uint4& v) {
       const int e = tid + 256 * i, key = e >> 4, ch = e & 15;
@@ -698,7 +705,14 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     uint16_t* vb = vt_s + buf * kD * kFaVS + 4 * (vkq ^ (vdc & 7));
     uint16_t* vh = vh_s + buf * kD * kFaVS + 4 * (vkq ^ (vdc & 7));
     // fp16 copy: v_cvt_pkrtz is exact for every bf16 value in fp16's normal
-    // range and saturates beyond it (the copy only carries p's residual)
+    // range and saturates beyond it; a bf16 magnitude of 0x4780 (2^16) or
+    // more -- past fp16's largest, 65504, or inf / NaN -- marks the block for
+    // the two-term product (|v| + 0x3880 carries into bit 15 of its half)
+    uint32_t sat = 0;
+    auto chk = [&](uint32_t w) { sat |= ((w & 0x7fff7fffu) + 0x38803880u) & 0x80008000u; };
+    chk(va0.x), chk(va0.y), chk(va0.z), chk(va0.w), chk(va1.x), chk(va1.y), chk(va1.z), chk(va1.w);
+    chk(va2.x), chk(va2.y), chk(va2.z), chk(va2.w), chk(va3.x), chk(va3.y), chk(va3.z), chk(va3.w);
+    if (sat != 0 && blk < 32 * kFaSatWords) atomicOr(&vsat[blk >> 5], 1u << (blk & 31));
     auto h2 = [](uint32_t lo16, uint32_t hi16) {
       return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(lo16 << 16),
                                                                      __uint_as_float(hi16 << 16)));
@@ -728,7 +742,9 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
 
   Stage sg0 = load_block(0);
   Stage sg1 = load_block(min(1, nkb - 1) * kFaK);
-  store_block(sg0, 0);
+  for (int i = threadIdx.x; i < kFaSatWords; i += 64 * NW) vsat[i] = 0u;
+  __syncthreads();
+  store_block(sg0, 0, 0);
   __syncthreads();
   // block jb: products from LDS buffer jb & 1; register set jb & 1 receives
   // block jb + 2 (at the end, the last block again: every iteration issues
@@ -771,31 +787,58 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
     // row with nothing visible yet keeps m = -inf and is skipped
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    // p in fp32, carried to the matrix cores as two terms: hi = bf16(p)
-    // against V in bf16, and the residual p - hi (exact in fp32, at most
-    // 2^-9 p) rounded to fp16 against V in fp16, so P V sees p to ~2^-20 of
-    // itself; the row sum adds the unrounded p.  (Three bf16 terms reach
-    // 2^-24 for a third more products; two bf16 terms, 2^-16, flip ~0.2% of
-    // the bf16 outputs against an fp32 reference.)
+    // p in fp32, carried to the matrix cores in fp16 against V in fp16
+    // (p to 2^-11 of itself).  A block with a V value beyond fp16's range
+    // takes two terms: hi = bf16(p) against V in bf16, and the residual
+    // p - hi (exact in fp32, at most 2^-9 p) rounded to fp16 against V in
+    // fp16 (p to ~2^-20; a V element beyond fp16's range enters the
+    // residual saturated at 65504, so its products keep hi's 2^-9).  The
+    // row sum adds the unrounded p.  (One bf16
+    // term, 2^-8, left the 4096-token one-layer prefill 10x further from the
+    // oracle than its summation-order floor; fp16 and the two terms sit at
+    // it.)
+    const bool two = jb >= 32 * kFaSatWords || ((vsat[jb >> 5] >> (jb & 31)) & 1u) != 0u;
     float sum = 0.0f;
-    bf16x8_t pa[2];
-    f16x8_t pr[2];
+    float pv_[16];  // p of the lane's 16 keys: c, u, pair element
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-      uint32_t ph[4], pl[4];
+    for (int c = 0; c < 2; c++)
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int kt = 2 * c + (u >> 1), i0 = 2 * (u & 1);
         const float r0 = __builtin_amdgcn_exp2f(sc[kt][i0] - m_use);
         const float r1 = __builtin_amdgcn_exp2f(sc[kt][i0 + 1] - m_use);
         sum += r0 + r1;
-        const uint16_t b0 = f2bf(r0), b1 = f2bf(r1);
-        ph[u] = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
-        const f16x2_t rr = f16x2_t{static_cast<_Float16>(r0 - bf2f(b0)), static_cast<_Float16>(r1 - bf2f(b1))};
-        pl[u] = __builtin_bit_cast(uint32_t, rr);
+        pv_[8 * c + 2 * u] = r0;
+        pv_[8 * c + 2 * u + 1] = r1;
       }
-      pa[c] = __builtin_bit_cast(bf16x8_t, make_uint4(ph[0], ph[1], ph[2], ph[3]));
-      pr[c] = __builtin_bit_cast(f16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
+    bf16x8_t pa[2];
+    f16x8_t pr[2];
+    if (two) {  // uniform; bf16(p) and the fp16 residual only where needed
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        uint32_t ph[4], pl[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const float r0 = pv_[8 * c + 2 * u], r1 = pv_[8 * c + 2 * u + 1];
+          const uint16_t b0 = f2bf(r0), b1 = f2bf(r1);
+          ph[u] = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
+          pl[u] = __builtin_bit_cast(
+              uint32_t, f16x2_t{static_cast<_Float16>(r0 - bf2f(b0)), static_cast<_Float16>(r1 - bf2f(b1))});
+        }
+        pa[c] = __builtin_bit_cast(bf16x8_t, make_uint4(ph[0], ph[1], ph[2], ph[3]));
+        pr[c] = __builtin_bit_cast(f16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        uint32_t pl[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+          pl[u] = __builtin_bit_cast(uint32_t, f16x2_t{static_cast<_Float16>(pv_[8 * c + 2 * u]),
+                                                       static_cast<_Float16>(pv_[8 * c + 2 * u + 1])});
+        pa[c] = bf16x8_t{};
+        pr[c] = __builtin_bit_cast(f16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
+      }
     }
     sum = add_xor32(add_xor16(sum));
     l_run = l_run * alpha + sum;
@@ -811,6 +854,9 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
 #pragma unroll
         for (int i = 0; i < 4; i++) o[j][i] *= ar[i];
     }
+    // the fp16 product always; a block with V beyond fp16's range adds its
+    // bf16 term in a second pass (one branch per block: a branch per MFMA
+    // cost what the single product saves)
 #pragma unroll
     for (int c = 0; c < 2; c++)
 #pragma unroll
@@ -821,18 +867,27 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
         // dim row j 16 + n, keys 32 c + 4 g.. and 32 c + 16 + 4 g.. (4-key
         // chunks 8 c + g and 8 c + 4 + g, swizzled as stored)
         const int sw = (2 * j + (n >> 3)) & 7;
-        const uint16_t* vrow = vb + (j * 16 + n) * kFaVS;
-        const uint2 v0 = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * c + g) ^ sw));
-        const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * c + 4 + g) ^ sw));
-        const bf16x8_t bv = __builtin_bit_cast(bf16x8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
         const uint16_t* hrow = vhb + (j * 16 + n) * kFaVS;
         const uint2 h0 = *reinterpret_cast<const uint2*>(hrow + 4 * ((8 * c + g) ^ sw));
         const uint2 h1 = *reinterpret_cast<const uint2*>(hrow + 4 * ((8 * c + 4 + g) ^ sw));
         const f16x8_t bh = __builtin_bit_cast(f16x8_t, make_uint4(h0.x, h0.y, h1.x, h1.y));
-        o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[c], bv, o[j], 0, 0, 0);
         o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pr[c], bh, o[j], 0, 0, 0);
       }
-    if (more) store_block(P == 0 ? sg1 : sg0, buf ^ 1);
+    if (two) {
+#pragma unroll
+      for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          if (j % 4 == 0) __builtin_amdgcn_sched_barrier(0);
+          const int sw = (2 * j + (n >> 3)) & 7;
+          const uint16_t* vrow = vb + (j * 16 + n) * kFaVS;
+          const uint2 v0 = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * c + g) ^ sw));
+          const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 4 * ((8 * c + 4 + g) ^ sw));
+          const bf16x8_t bv = __builtin_bit_cast(bf16x8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
+          o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[c], bv, o[j], 0, 0, 0);
+        }
+    }
+    if (more) store_block(P == 0 ? sg1 : sg0, buf ^ 1, jb + 1);
     __syncthreads();
   };
   for (int jb = 0; jb < nkb; jb += 2) {

@@ -96,6 +96,27 @@ def test_attention(gpu, orc, Hq, Hkv, M, offset):
         assert _close(yb, ref, ulps=2, floor=2e-3) > 0.999
 
 
+@pytest.mark.parametrize("M,offset", [(130, 70), (300, 0)])
+def test_attention_prefill_v_beyond_fp16_range(gpu, orc, M, offset):
+    """The prefill kernel multiplies p by an fp16 copy of V; a key block with
+    a V value beyond fp16's range (here keys 64..127 scaled by 2^17, about
+    1.3e5) must take the two-term bf16 product instead, or those keys'
+    contributions would saturate at 65504."""
+    Hq, Hkv = 32, 8
+    cap = offset + M + 5
+    q = gpu.fill_normal_bf16(21, (Hq, M, 128))
+    kc = gpu.fill_normal_bf16(22, (Hkv, cap, 128))
+    vc = gpu.fill_normal_bf16(23, (Hkv, cap, 128))
+    vc[:, 64:128] *= 2.0 ** 17  # exact in bf16
+    assert float(vc.float().abs().max()) > 65504.0
+    scale = 1 / np.sqrt(128)
+    ref = orc.sdpa(torch_bf16_bits(q), torch_bf16_bits(kc), torch_bf16_bits(vc), offset + M, offset, True,
+                   np.float32(scale))
+    yb = torch_bf16_bits(gpu.attention(q, kc, vc, offset, scale))
+    assert max_rel_err(bf16_to_f32(yb), bf16_to_f32(ref)) < 1e-2
+    assert _close(yb, ref, ulps=2, floor=2e-3) > 0.999
+
+
 def test_attention_workspace_reuse(gpu, orc):
     """One zero-filled workspace over calls of different split counts and row
     tilings: the arrival counters come back to zero after every call."""
