@@ -247,7 +247,9 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
   // splits in reverse launch order: the last, partly filled split goes out
   // first, so that where a CU holds two workgroups the second is a full one
   // and the short one does not queue its loads behind a full one's
-  const int kvh = blockIdx.x, split = gridDim.y - 1 - blockIdx.y;
+  // (p.ns == gridDim.y: the split is known from the first kernel-argument
+  // lines, without the round trip to the grid size behind the arguments)
+  const int kvh = blockIdx.x, split = p.ns - 1 - blockIdx.y;
   const int r0 = blockIdx.z * RMAX;   // first row of this workgroup's tile
   const int RT = min(RMAX, R - r0);   // rows in the tile
   constexpr int KPS = kDecWaveKeys * NW;  // keys per split
@@ -263,6 +265,12 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
   uint16_t ra[kI], rb[kI], rv0[kI], rv1[kI], wa[kI], wb[kI];
   float freq = 0.0f;
   if constexpr (FUSED) {
+    // every kernel-argument field of the loads below, in one round of
+    // scalar loads: left to itself the compiler requests the norm weights'
+    // argument line after the first round has returned, one more memory
+    // round trip ahead of every load of the launch
+    asm volatile("" ::"s"(p.q), "s"(p.k), "s"(p.offset_dev), "s"(f.k_new), "s"(f.v_new), "s"(f.q_norm),
+                 "s"(f.k_norm));
     freq = f.tab.inv_freq[lane];
 #pragma unroll
     for (int u = 0; u < kItems; u++) {
@@ -280,7 +288,31 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
       wb[u] = nw[lane + 64];
     }
   }
-  const int offset = p.offset_dev ? *p.offset_dev : p.offset;
+  // ---- K of this workgroup's keys, issued before the cache position is
+  // known (its addresses do not depend on it), through a buffer resource
+  // that ends at the cache capacity: a key past the capacity reads zeros
+  // without a memory access.  Keys at or beyond the L visible positions may
+  // come back with any bits (rows not written yet, or this call's new rows
+  // while they are written); their scores are replaced by -inf with a
+  // select, never combined arithmetically, and the new rows come from LDS ----
+  const int kbase = split * KPS;
+  const int c0 = kbase + wave * kDecWaveKeys;
+  const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.k) + hbase, static_cast<short>(0), p.cap * kD * 2, kBufferConfig);
+  uint4 kb[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const int kofs = (c0 + t * 16 + li) * (kD * 2) + g * 16;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+      kb[t][ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, kofs + ks * 64, 0, 0));
+  }
+  // the position through the constant address space: a scalar load, waited
+  // for apart from the vector loads above (earlier kernels write it, this
+  // one only reads it)
+  const int offset =
+      p.offset_dev ? *(const __attribute__((address_space(4))) int*)(p.offset_dev) : p.offset;
   if constexpr (FUSED) __builtin_amdgcn_sched_barrier(0);
   const int L = offset + p.M;
   // The grid holds a split per KPS keys of the largest context the launch
@@ -291,12 +323,13 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
   // without visible keys contributes nothing to the merge either way:
   // results are the same bits as with every split taking part.)
   const int ns_live = min(p.ns, (L + KPS - 1) / KPS);
-  if (split >= ns_live) return;
+  if (split >= ns_live) {
+    // the K loads above land before the wave ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
   // this workgroup's keys: [kbase, kbase + KPS), of which those < kend exist
-  const int kbase = split * KPS;
   const int kend = min(L, kbase + KPS);
-  const int c0 = kbase + wave * kDecWaveKeys;
-  const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
   // new tokens whose keys fall in this workgroup's range
   const int t_lo = max(0, kbase - offset);
   const int t_hi = min(p.M, kbase + KPS - offset);
@@ -307,22 +340,12 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) qa[ks] = *reinterpret_cast<const uint4*>(qrow + ks * 32);
   }
-  // K and V rows of this kv head through buffer resources that end at the
-  // L visible positions: a lane whose key lies beyond them gets zeros
-  // without a memory access (a raw buffer load past num_records), so a
-  // partly filled split moves only its keys' bytes
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(p.k) + hbase, static_cast<short>(0), L * kD * 2, kBufferConfig);
+  // V rows of this kv head through a buffer resource that ends at the L
+  // visible positions: a lane whose key lies beyond them gets zeros without
+  // a memory access (a raw buffer load past num_records), so a partly
+  // filled split moves only its keys' V bytes, and an unweighted row is zero
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(p.v) + hbase, static_cast<short>(0), L * kD * 2, kBufferConfig);
-  uint4 kb[2][4];
-#pragma unroll
-  for (int t = 0; t < 2; t++) {
-    const int kofs = (c0 + t * 16 + li) * (kD * 2) + g * 16;
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++)
-      kb[t][ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, kofs + ks * 64, 0, 0));
-  }
   // V: lane holds dims 8 vc .. 8 vc + 7 of keys vq + 4 j, j < 8 (one 16-byte
   // load per key; an instruction reads 4 whole key rows).  With the fused
   // prologue the V loads go out after its barrier: a wave whose loads
