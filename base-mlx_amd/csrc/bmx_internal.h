@@ -107,6 +107,21 @@ enum QmmEpilogue { QMM_STORE = 0, QMM_RESIDUAL = 1, QMM_SWIGLU = 2 };
 int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                    const uint32_t* w2, const uint16_t* s2, const uint16_t* b2, const uint16_t* res, uint16_t* y, int M,
                    int N, int K, float* ws, size_t ws_floats, hipStream_t stream);
+// The same products over group-major copies of the weights (launch_qmm_repack):
+// W as [K/64][N][8] words and s|b as [K/64][N] words s | b << 16, so the
+// rows of one group in a tile are contiguous.  Bit-identical to the MLX-layout
+// launches; kNoFit (nothing launched) where the one-launch segments form or
+// the SwiGLU form does not fit, for the caller's MLX-layout fallback.
+int launch_qmm_epi_gm(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const uint32_t* sb, const uint32_t* w2,
+                      const uint32_t* sb2, const uint16_t* res, uint16_t* y, int M, int N, int K, float* ws,
+                      size_t ws_floats, hipStream_t stream);
+int launch_qmm_segments_gm(const uint16_t* x, int nseg, const uint32_t* const* w, const uint32_t* const* sb,
+                           uint16_t* const* y, const int* n, int M, int K, float* ws, size_t ws_floats,
+                           hipStream_t stream);
+// Writes the group-major copy (wt: N * K / 8 words, sbt: N * K / 64 words)
+// of an MLX-layout weight w, s, b of N rows by K.
+int launch_qmm_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b, int N, int K, uint32_t* wt,
+                      uint32_t* sbt, hipStream_t stream);
 // Split-K partial floats the GEMM needs for any M up to max_M (0 if none).
 size_t qmm_workspace_floats(int max_M, int N, int K);
 // A device buffer of at least `floats` floats owned by the library for the

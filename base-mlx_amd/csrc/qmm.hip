@@ -85,7 +85,7 @@ struct QmmParams {
   int M, N, K;
   int gps;     // groups per split
   int mtiles;  // row tiles of x (the grid's x dimension enumerates mtiles x column tiles)
-  int xcd;     // XCD-grouped tile order (vocabulary-sized N), else row-major
+  int xcd;     // tile order: 0 row-major; XCD-grouped 1 column-major, 2 row-major
   // Store epilogue over up to 3 column segments (q | k | v of one layer in
   // one launch): segment i covers output columns [seg_n0[i], seg_n0[i+1])
   // of the launch (multiples of the tile width) with its own W, s, b and y
@@ -96,6 +96,13 @@ struct QmmParams {
   const uint16_t* seg_s[3];
   const uint16_t* seg_b[3];
   uint16_t* seg_y[3];
+  // Group-major weights (the model's prefill copy): w, w2 and seg_w hold
+  // [K/64][N][8] words (each row's 64 nibbles of one group, rows of a group
+  // consecutive), and sb, sb2 and seg_sb [K/64][N] words s | b << 16, so a
+  // tile's W and s|b of one group are contiguous
+  const uint32_t* sb;
+  const uint32_t* sb2;
+  const uint32_t* seg_sb[3];
 };
 
 // two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
@@ -104,8 +111,9 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 }
 
 // BN: W rows per tile, 128 (waves of 64 x 64) or 256 (waves of 64 x 128:
-// the x tile serves twice the W rows, for large grids)
-template <int EPI, int BN>
+// the x tile serves twice the W rows, for large grids).  GM: weights in the
+// group-major layout (QmmParams), else MLX's row-major one.
+template <int EPI, int BN, bool GM>
 __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   static_assert(BN == 128 || BN == 160 || BN == 256, "W tile rows");
   static_assert(EPI != QMM_SWIGLU || BN % 64 == 0, "SwiGLU pairs gate and up rows per wave");
@@ -137,8 +145,14 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
       const int q8 = T >> 3, r8 = T & 7;
       const int k = blockIdx.x & 7, i = blockIdx.x >> 3;
       const int lin = k < r8 ? k * (q8 + 1) + i : r8 * (q8 + 1) + (k - r8) * q8 + i;
-      mt = lin % p.mtiles;
-      nt = lin / p.mtiles;
+      if (p.xcd == 2) {
+        const int ntiles = T / p.mtiles;
+        mt = lin / ntiles;
+        nt = lin - mt * ntiles;
+      } else {
+        mt = lin % p.mtiles;
+        nt = lin / p.mtiles;
+      }
     } else {
       const int ntiles = T / p.mtiles;
       mt = blockIdx.x / ntiles;
@@ -151,6 +165,7 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   // the segment holding this workgroup's columns (uniform)
   const uint32_t* pw = p.w;
   const uint16_t *ps = p.s, *pb = p.b;
+  const uint32_t* psb = p.sb;
   uint16_t* py = p.y;
   if constexpr (EPI == QMM_STORE) {
     if (p.nseg > 1) {
@@ -158,6 +173,7 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
       pw = p.seg_w[si];
       ps = p.seg_s[si];
       pb = p.seg_b[si];
+      psb = p.seg_sb[si];
       py = p.seg_y[si];
       n0 -= p.seg_n0[si];
       N = p.seg_n0[si + 1] - p.seg_n0[si];
@@ -176,20 +192,28 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   // SwiGLU: each wave's BN / 2 W rows are BN / 4 gate rows and the up rows
   // of the same output columns, so a lane holds both products of its
   // outputs (gate in tiles j < NJ / 2, up in j + NJ / 2)
-  auto wsrc = [&](int row, const uint32_t*& w_, const uint16_t*& s_, const uint16_t*& b_) {
+  // (group-major: W row wrow of group g at (g N + wrow) 8 words, its s|b
+  // at g N + wrow, so the tile's rows of one group are consecutive)
+  auto wsrc = [&](int row, const uint32_t*& w_, const uint16_t*& s_, const uint16_t*& b_, const uint32_t*& sb_) {
     const int r = row % (BN / 2), col = (row / (BN / 2)) * (BN / 4) + r % (BN / 4);
     const bool up_row = EPI == QMM_SWIGLU && r >= BN / 4;
     const int64_t wrow = min(n0 + (EPI == QMM_SWIGLU ? col : row), N - 1);
-    w_ = (up_row ? p.w2 : pw) + wrow * (K / 8) + wh * 4;
-    s_ = (up_row ? p.s2 : ps) + wrow * G;
-    b_ = (up_row ? p.b2 : pb) + wrow * G;
+    if constexpr (GM) {
+      w_ = (up_row ? p.w2 : pw) + wrow * 8 + wh * 4;
+      sb_ = (up_row ? p.sb2 : psb) + wrow;
+    } else {
+      w_ = (up_row ? p.w2 : pw) + wrow * (K / 8) + wh * 4;
+      s_ = (up_row ? p.s2 : ps) + wrow * G;
+      b_ = (up_row ? p.b2 : pb) + wrow * G;
+    }
   };
   const uint32_t *wp0, *wp1 = nullptr;
-  const uint16_t *sp0, *bp0, *sp1 = nullptr, *bp1 = nullptr;
-  wsrc(wr, wp0, sp0, bp0);
+  const uint16_t *sp0 = nullptr, *bp0 = nullptr, *sp1 = nullptr, *bp1 = nullptr;
+  const uint32_t *sbp0 = nullptr, *sbp1 = nullptr;
+  wsrc(wr, wp0, sp0, bp0, sbp0);
   // (BN 160: the second row exists for wr < 32, i.e. wave 0; uniform per wave)
   const bool row1 = WR == 2 && wr + 128 < BN;
-  if (row1) wsrc(wr + 128, wp1, sp1, bp1);
+  if (row1) wsrc(wr + 128, wp1, sp1, bp1, sbp1);
   uint4 xr0, xr1, xr2, xr3, wq0, wq1;
   uint16_t sr0, br0, sr1, br1;
   auto load = [&](int g) {
@@ -197,13 +221,27 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     xr1 = *reinterpret_cast<const uint4*>(xp1 + g * 64);
     xr2 = *reinterpret_cast<const uint4*>(xp2 + g * 64);
     xr3 = *reinterpret_cast<const uint4*>(xp3 + g * 64);
-    wq0 = *reinterpret_cast<const uint4*>(wp0 + g * 8);
-    sr0 = sp0[g];
-    br0 = bp0[g];
-    if (row1) {
-      wq1 = *reinterpret_cast<const uint4*>(wp1 + g * 8);
-      sr1 = sp1[g];
-      br1 = bp1[g];
+    if constexpr (GM) {
+      const int64_t go = static_cast<int64_t>(g) * N;
+      wq0 = *reinterpret_cast<const uint4*>(wp0 + go * 8);
+      const uint32_t sb0 = sbp0[go];
+      sr0 = static_cast<uint16_t>(sb0 & 0xffffu);
+      br0 = static_cast<uint16_t>(sb0 >> 16);
+      if (row1) {
+        wq1 = *reinterpret_cast<const uint4*>(wp1 + go * 8);
+        const uint32_t sb1 = sbp1[go];
+        sr1 = static_cast<uint16_t>(sb1 & 0xffffu);
+        br1 = static_cast<uint16_t>(sb1 >> 16);
+      }
+    } else {
+      wq0 = *reinterpret_cast<const uint4*>(wp0 + g * 8);
+      sr0 = sp0[g];
+      br0 = bp0[g];
+      if (row1) {
+        wq1 = *reinterpret_cast<const uint4*>(wp1 + g * 8);
+        sr1 = sp1[g];
+        br1 = bp1[g];
+      }
     }
   };
   // ---- registers -> LDS: x as is, W dequantized to bf16 ----
@@ -491,9 +529,21 @@ size_t qmm_workspace_floats(int max_M, int N, int K) {
   return need;
 }
 
-int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
-                   const uint32_t* w2, const uint16_t* s2, const uint16_t* b2, const uint16_t* res, uint16_t* y, int M,
-                   int N, int K, float* ws, size_t ws_floats, hipStream_t stream) {
+namespace {
+
+template <int EPI, int BN>
+const void* qmm_kernel_for(bool gm) {
+  return gm ? reinterpret_cast<const void*>(qmm_kernel<EPI, BN, true>)
+            : reinterpret_cast<const void*>(qmm_kernel<EPI, BN, false>);
+}
+
+// The GEMM with an epilogue over MLX-layout (sb == nullptr) or group-major
+// weights (w, w2 and sb, sb2 in the layout of QmmParams)
+int qmm_epi_impl(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                 const uint32_t* sb, const uint32_t* w2, const uint16_t* s2, const uint16_t* b2, const uint32_t* sb2,
+                 const uint16_t* res, uint16_t* y, int M, int N, int K, float* ws, size_t ws_floats,
+                 hipStream_t stream) {
+  const bool gm = sb != nullptr;
   if (M <= 0) return BMX_OK;
   if (K % 64 || N <= 0) return set_error(BMX_E_SHAPE, "qmm: N=%d K=%d", N, K);
   if (!aligned(x, 16) || !aligned(w, 16) || (epi == QMM_SWIGLU && !aligned(w2, 16)))
@@ -511,27 +561,36 @@ int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const 
   // SwiGLU needs both products of an output in one workgroup: no K split
   if (epi == QMM_SWIGLU && splits > 1) return kNoFit;
   const int mtiles = (M + QBM - 1) / QBM, ntiles = (N + cols - 1) / cols;
-  // (measured: vocabulary-sized N x K = 151936 x 4096 at M = 2048 runs 1.5x
-  // faster grouped by XCD; the model's projections run 4-9% slower so)
-  const int xcd = ntiles > 512 ? 1 : 0;
+  // Tile order.  Vocabulary-sized N: grouped by XCD in column-major order
+  // (151936 x 4096 at M = 2048 runs 1.5x faster; the model's projections
+  // ran 4-9% slower so).  The residual GEMMs (o, down: K 4096 / 9728, so a
+  // large x) grouped by XCD in row-major order, so each XCD's L2 takes the x
+  // rows of its own row tiles and every column tile's W instead of every x
+  // row tile and its own W: 207.2 -> 201.3 us per call averaged over o and
+  // down in the Qwen3-4B 4096-token prefill (q | k | v and gate | up measured
+  // equal or slower that way).
+  const int xcd = ntiles > 512 ? 1 : epi == QMM_RESIDUAL ? 2 : 0;
   QmmParams p{x, w, s, b, w2, s2, b2, res, y, nullptr, M, N, K, gps, mtiles, xcd};
+  p.sb = sb;
+  p.sb2 = sb2;
   if (splits > 1) {
     if (int rc = split_scratch(static_cast<size_t>(splits) * M * N, ws, ws_floats, stream, &p.part)) return rc;
   }
   const dim3 grid(static_cast<unsigned>(mtiles) * ntiles, 1, splits);
-  auto launch = [&](auto kern, int bn) {
-    if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(kern), qmm_lds(bn))) return rc;
-    hipLaunchKernelGGL(kern, grid, dim3(QT), qmm_lds(bn), stream, p);
+  auto launch = [&](const void* kern, int bn) {
+    if (int rc = allow_lds_ptr(kern, qmm_lds(bn))) return rc;
+    void* args[] = {&p};
+    if (int rc = check_hip(hipLaunchKernel(kern, grid, dim3(QT), args, qmm_lds(bn), stream), "qmm launch")) return rc;
     return check_launch("qmm");
   };
-  const int rc = bn == 256   ? (epi == QMM_SWIGLU    ? launch(qmm_kernel<QMM_SWIGLU, 256>, 256)
-                                : epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL, 256>, 256)
-                                                      : launch(qmm_kernel<QMM_STORE, 256>, 256))
-                 : bn == 160 ? (epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL, 160>, 160)
-                                                    : launch(qmm_kernel<QMM_STORE, 160>, 160))
-                             : (epi == QMM_SWIGLU    ? launch(qmm_kernel<QMM_SWIGLU, 128>, 128)
-                                : epi == QMM_RESIDUAL ? launch(qmm_kernel<QMM_RESIDUAL, 128>, 128)
-                                                      : launch(qmm_kernel<QMM_STORE, 128>, 128));
+  const int rc = bn == 256   ? (epi == QMM_SWIGLU    ? launch(qmm_kernel_for<QMM_SWIGLU, 256>(gm), 256)
+                                : epi == QMM_RESIDUAL ? launch(qmm_kernel_for<QMM_RESIDUAL, 256>(gm), 256)
+                                                      : launch(qmm_kernel_for<QMM_STORE, 256>(gm), 256))
+                 : bn == 160 ? (epi == QMM_RESIDUAL ? launch(qmm_kernel_for<QMM_RESIDUAL, 160>(gm), 160)
+                                                    : launch(qmm_kernel_for<QMM_STORE, 160>(gm), 160))
+                             : (epi == QMM_SWIGLU    ? launch(qmm_kernel_for<QMM_SWIGLU, 128>(gm), 128)
+                                : epi == QMM_RESIDUAL ? launch(qmm_kernel_for<QMM_RESIDUAL, 128>(gm), 128)
+                                                      : launch(qmm_kernel_for<QMM_STORE, 128>(gm), 128));
   if (rc) return rc;
   if (splits > 1) {
     const int64_t mn = static_cast<int64_t>(M) * N;
@@ -544,9 +603,12 @@ int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const 
   return BMX_OK;
 }
 
-int launch_qmm_segments(const uint16_t* x, int nseg, const uint32_t* const* w, const uint16_t* const* s,
-                        const uint16_t* const* b, uint16_t* const* y, const int* n, int M, int K, float* ws,
-                        size_t ws_floats, hipStream_t stream) {
+// q | k | v (up to 3 column segments) in one launch where every segment is
+// whole tiles and K is not split; else kNoFit (gm) or a launch per segment
+int qmm_segments_impl(const uint16_t* x, int nseg, const uint32_t* const* w, const uint16_t* const* s,
+                      const uint16_t* const* b, const uint32_t* const* sb, uint16_t* const* y, const int* n, int M,
+                      int K, float* ws, size_t ws_floats, hipStream_t stream) {
+  const bool gm = sb != nullptr;
   if (M <= 0) return BMX_OK;
   if (nseg < 1 || nseg > 3) return set_error(BMX_E_ARG, "qmm: %d segments", nseg);
   int ntot = 0;
@@ -568,6 +630,7 @@ int launch_qmm_segments(const uint16_t* x, int nseg, const uint32_t* const* w, c
   // one launch when every segment is whole tiles and K is not split (the
   // reduction writes one y); else a launch per segment
   if (!one || splits > 1 || (M + QBM - 1) / QBM > 65535) {
+    if (gm) return kNoFit;
     for (int i = 0; i < nseg; i++)
       if (int rc = launch_qmm(x, w[i], s[i], b[i], y[i], M, n[i], K, ws, ws_floats, stream)) return rc;
     return BMX_OK;
@@ -582,14 +645,73 @@ int launch_qmm_segments(const uint16_t* x, int nseg, const uint32_t* const* w, c
     p.seg_w[i] = w[i];
     p.seg_s[i] = s[i];
     p.seg_b[i] = b[i];
+    p.seg_sb[i] = gm ? sb[i] : nullptr;
     p.seg_y[i] = y[i];
     c += n[i];
   }
   for (int i = nseg; i < 4; i++) p.seg_n0[i] = c;
-  auto kern = wide ? qmm_kernel<QMM_STORE, 256> : qmm_kernel<QMM_STORE, 128>;
-  if (int rc = allow_lds_ptr(reinterpret_cast<const void*>(kern), qmm_lds(bn))) return rc;
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(mtiles) * ntiles, 1, 1), dim3(QT), qmm_lds(bn), stream, p);
+  const void* kern = wide ? qmm_kernel_for<QMM_STORE, 256>(gm) : qmm_kernel_for<QMM_STORE, 128>(gm);
+  if (int rc = allow_lds_ptr(kern, qmm_lds(bn))) return rc;
+  void* args[] = {&p};
+  if (int rc = check_hip(hipLaunchKernel(kern, dim3(static_cast<unsigned>(mtiles) * ntiles, 1, 1), dim3(QT), args,
+                                         qmm_lds(bn), stream),
+                         "qmm launch"))
+    return rc;
   return check_launch("qmm");
+}
+
+}  // namespace
+
+int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                   const uint32_t* w2, const uint16_t* s2, const uint16_t* b2, const uint16_t* res, uint16_t* y, int M,
+                   int N, int K, float* ws, size_t ws_floats, hipStream_t stream) {
+  return qmm_epi_impl(epi, x, w, s, b, nullptr, w2, s2, b2, nullptr, res, y, M, N, K, ws, ws_floats, stream);
+}
+
+int launch_qmm_epi_gm(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const uint32_t* sb, const uint32_t* w2,
+                      const uint32_t* sb2, const uint16_t* res, uint16_t* y, int M, int N, int K, float* ws,
+                      size_t ws_floats, hipStream_t stream) {
+  if (!sb || (epi == QMM_SWIGLU && !sb2)) return set_error(BMX_E_ARG, "qmm: group-major s|b missing");
+  return qmm_epi_impl(epi, x, w, nullptr, nullptr, sb, w2, nullptr, nullptr, sb2, res, y, M, N, K, ws, ws_floats,
+                      stream);
+}
+
+int launch_qmm_segments(const uint16_t* x, int nseg, const uint32_t* const* w, const uint16_t* const* s,
+                        const uint16_t* const* b, uint16_t* const* y, const int* n, int M, int K, float* ws,
+                        size_t ws_floats, hipStream_t stream) {
+  return qmm_segments_impl(x, nseg, w, s, b, nullptr, y, n, M, K, ws, ws_floats, stream);
+}
+
+int launch_qmm_segments_gm(const uint16_t* x, int nseg, const uint32_t* const* w, const uint32_t* const* sb,
+                           uint16_t* const* y, const int* n, int M, int K, float* ws, size_t ws_floats,
+                           hipStream_t stream) {
+  const uint16_t* none[3] = {nullptr, nullptr, nullptr};
+  return qmm_segments_impl(x, nseg, w, none, none, sb, y, n, M, K, ws, ws_floats, stream);
+}
+
+// The group-major copy of an MLX-layout weight: one thread per (group g,
+// row n), i = g N + n, so consecutive threads write consecutive 32-byte rows
+__global__ void __launch_bounds__(256) qmm_repack_kernel(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                                                         uint32_t* wt, uint32_t* sbt, int N, int G) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(G) * N) return;
+  const int g = static_cast<int>(i / N), n = static_cast<int>(i - static_cast<int64_t>(g) * N);
+  const int64_t src = static_cast<int64_t>(n) * G + g;
+  const uint4* ws = reinterpret_cast<const uint4*>(w + src * 8);
+  uint4* wd = reinterpret_cast<uint4*>(wt + i * 8);
+  wd[0] = ws[0];
+  wd[1] = ws[1];
+  sbt[i] = static_cast<uint32_t>(s[src]) | (static_cast<uint32_t>(b[src]) << 16);
+}
+
+int launch_qmm_repack(const uint32_t* w, const uint16_t* s, const uint16_t* b, int N, int K, uint32_t* wt,
+                      uint32_t* sbt, hipStream_t stream) {
+  if (N <= 0 || K <= 0 || K % 64) return set_error(BMX_E_SHAPE, "qmm repack: N=%d K=%d", N, K);
+  if (!aligned(w, 16) || !aligned(wt, 16)) return set_error(BMX_E_ALIGN, "qmm repack: W must be 16-byte aligned");
+  const int64_t n = static_cast<int64_t>(K / 64) * N;
+  hipLaunchKernelGGL(qmm_repack_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, w, s, b,
+                     wt, sbt, N, K / 64);
+  return check_launch("qmm_repack");
 }
 
 int launch_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y, int M, int N,

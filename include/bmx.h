@@ -309,7 +309,9 @@ int bmx_qwen3_config_from_json(const char *path, bmx_qwen3_config *out);
 int bmx_qwen3_load(const char *dir, int max_tokens, bmx_qwen3 **out);
 /* Device pointers of a projection: layer >= 0 with slot 0..6 = q,k,v,o,
  * gate,up,down; layer -1 = embed_tokens; layer -2 = lm head (tied: embed).
- * Mirrors the tensor map of Qwen3::load (qwen3.rs:205-273). */
+ * Mirrors the tensor map of Qwen3::load (qwen3.rs:205-273).  A layer
+ * projection may be written through them: the next forward of more than 8
+ * tokens first rewrites the group-major copies its GEMMs read. */
 int bmx_qwen3_qlinear(bmx_qwen3 *model, int layer, int slot, uint32_t **w, bmx_bf16 **scales,
                       bmx_bf16 **biases, int *N, int *K);
 

@@ -266,6 +266,48 @@ def test_prefill_unsplit_fused_epilogues(gpu, orc):
     assert _check_logits(g, o) >= 0.9
 
 
+def _write_projection(gpu, gm, layer, slot, arrays):
+    """Writes host arrays (w, s, b) into a projection of the GPU model
+    through the device pointers bmx_qwen3_qlinear hands out."""
+    import ctypes
+
+    ptrs = [ctypes.c_void_p() for _ in range(3)]
+    N, K = ctypes.c_int(), ctypes.c_int()
+    gpu.call("bmx_qwen3_qlinear", gm.h, layer, slot, *[ctypes.byref(q) for q in ptrs], ctypes.byref(N),
+             ctypes.byref(K))
+    for dst, src in zip(ptrs, arrays):
+        src = np.ascontiguousarray(src)
+        assert gpu._hip().hipMemcpy(dst, src.ctypes.data_as(ctypes.c_void_p), src.nbytes, 1) == 0
+
+
+def test_prefill_reads_weights_written_through_qlinear(gpu, orc):
+    """The prefill GEMMs of q | k | v and gate | up read a group-major copy
+    of their weights; a projection written through the pointers of
+    bmx_qwen3_qlinear is seen by the next prefill: with layer 1's gate and
+    layer 0's v projection replaced in both models the logits follow the
+    oracle's, and with the old weights written back they are the first
+    prefill's bit for bit."""
+    gm, om = _pair(gpu, orc)
+    toks = orc.fill_tokens(77, 40, SMALL["vocab"])
+    g0 = torch_bf16_bits(gm.forward(gm.new_cache(64), toks, all_logits=True))
+    old = {key: [a.copy() for a in gm.qlinear_numpy(*key)] for key in [(1, 4), (0, 2)]}
+    for (layer, slot), seed in [((1, 4), 5), ((0, 2), 6)]:
+        w, s, b = old[(layer, slot)]
+        rng = np.random.default_rng(seed)
+        new = (rng.integers(0, 2**32, w.shape, dtype=np.uint32), s[::-1].copy(), b[:, ::-1].copy())
+        _write_projection(gpu, gm, layer, slot, new)
+        for dst, src in zip(om.qlinear(layer, slot), new):
+            dst[...] = src
+    g1 = gm.forward(gm.new_cache(64), toks, all_logits=True)
+    o1 = om.forward(om.new_cache(64), toks, all_logits=True)
+    _check_logits(g1, o1)
+    assert not np.array_equal(torch_bf16_bits(g1), g0)
+    for key, arrays in old.items():
+        _write_projection(gpu, gm, *key, arrays)
+    g2 = torch_bf16_bits(gm.forward(gm.new_cache(64), toks, all_logits=True))
+    np.testing.assert_array_equal(g2, g0)
+
+
 def test_qwen3_4b_shape_prefill_and_decode(gpu, orc):
     """Full Qwen3-4B shape (36 layers, 151936 vocab) at short context: a
     9-token prefill, 32 teacher-forced decode steps and an 8-token verify
