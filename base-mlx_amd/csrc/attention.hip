@@ -89,6 +89,7 @@ constexpr int kAgentCoherent = 16;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
 typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+typedef __attribute__((ext_vector_type(2))) unsigned short u16x2_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
@@ -637,10 +638,11 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
   uint16_t* vt_s = kt_s + 2 * kFaK * kFaKS;             // [2][kD][kFaVS]
   uint16_t* vh_s = vt_s + 2 * kD * kFaVS;               // [2][kD][kFaVS] fp16
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // staging thread index: all 256 threads of a 4-wave workgroup stage K and
-  // V; with 8 waves, threads 0..255 stage V and 256..511 stage K
+  // staging: each of the 256 threads of a 4-wave workgroup stages a quarter
+  // of K's rows and a 4-key x 8-dim piece of V; each of the 512 threads of
+  // an 8-wave workgroup half as much (2 x 16 bytes of K, 4 keys x 4 dims of
+  // V), so that every wave does the same transposition work
   const int tid = threadIdx.x & 255;
-  const bool stage_k = NW == 4 || threadIdx.x >= 256, stage_v = NW == 4 || threadIdx.x < 256;
   const int n = lane & 15, g = lane >> 4;
   const int rep_h = p.Hq / p.Hkv;
   // blockIdx.y: kv head x head groups of HG
@@ -669,31 +671,30 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
   struct Stage {
     uint4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
   };
-  const int vdc = tid & 15, vkq = tid >> 4;  // V task: dims 8 vdc.., keys 4 vkq..
+  const int vdc = tid & 15, vkq = tid >> 4;  // V task (4 waves): dims 8 vdc.., keys 4 vkq..
+  const int vd4 = threadIdx.x & 31, vk4 = threadIdx.x >> 5;  // V task (8 waves): dims 4 vd4.., keys 4 vk4..
   auto kaddr = [&](int k0, int i) {
-    const int e = tid + 256 * i, key = e >> 4, ch = e & 15;
+    const int e = (NW == 8 ? static_cast<int>(threadIdx.x) : tid) + 64 * NW * i, key = e >> 4, ch = e & 15;
     return reinterpret_cast<const uint4*>(p.k + hbase + static_cast<int64_t>(min(k0 + key, L - 1)) * kD + ch * 8);
   };
   auto vaddr = [&](int k0, int j) {
     return reinterpret_cast<const uint4*>(p.v + hbase + static_cast<int64_t>(min(k0 + 4 * vkq + j, L - 1)) * kD +
                                           vdc * 8);
   };
-  // (with 8 waves a thread stages K or V, never both: its four loads go to
-  // kr0..kr3 either way, so a register set is 16 VGPRs, not 32)
+  auto vaddr4 = [&](int k0, int j) {
+    return reinterpret_cast<const uint2*>(p.v + hbase + static_cast<int64_t>(min(k0 + 4 * vk4 + j, L - 1)) * kD +
+                                          vd4 * 4);
+  };
+  // (with 8 waves a register set is 16 VGPRs: kr0, kr1 hold K, kr2 and kr3
+  // the V rows of keys 4 vk4 .. + 3, dims 4 vd4 .. + 3)
   auto load_block = [&](int k0) {
     Stage r;
     if constexpr (NW == 8) {
-      if (stage_k) {
-        r.kr0 = *kaddr(k0, 0);
-        r.kr1 = *kaddr(k0, 1);
-        r.kr2 = *kaddr(k0, 2);
-        r.kr3 = *kaddr(k0, 3);
-      } else {
-        r.kr0 = *vaddr(k0, 0);
-        r.kr1 = *vaddr(k0, 1);
-        r.kr2 = *vaddr(k0, 2);
-        r.kr3 = *vaddr(k0, 3);
-      }
+      r.kr0 = *kaddr(k0, 0);
+      r.kr1 = *kaddr(k0, 1);
+      const uint2 v0 = *vaddr4(k0, 0), v1 = *vaddr4(k0, 1), v2 = *vaddr4(k0, 2), v3 = *vaddr4(k0, 3);
+      r.kr2 = make_uint4(v0.x, v0.y, v1.x, v1.y);
+      r.kr3 = make_uint4(v2.x, v2.y, v3.x, v3.y);
     } else {
       r.kr0 = *kaddr(k0, 0);
       r.kr1 = *kaddr(k0, 1);
@@ -709,51 +710,80 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
   auto store_block = [&](const Stage r, int buf, int blk) {
     uint16_t* kb = kt_s + buf * kFaK * kFaKS;
     auto kput = [&](int i, const uint4& v) {
-      const int e = tid + 256 * i, key = e >> 4, ch = e & 15;
+      const int e = (NW == 8 ? static_cast<int>(threadIdx.x) : tid) + 64 * NW * i, key = e >> 4, ch = e & 15;
       *reinterpret_cast<uint4*>(kb + key * kFaKS + ch * 8) = v;
     };
-    if (stage_k) {
-      kput(0, r.kr0);
-      kput(1, r.kr1);
-      kput(2, r.kr2);
-      kput(3, r.kr3);
-    }
-    if (!stage_v) return;
-    const uint4 va0 = NW == 8 ? r.kr0 : r.vr0, va1 = NW == 8 ? r.kr1 : r.vr1;
-    const uint4 va2 = NW == 8 ? r.kr2 : r.vr2, va3 = NW == 8 ? r.kr3 : r.vr3;
-    // V^T: dim 8 vdc + d gets keys 4 vkq .. + 3 (8 bytes)
-    // 4-key chunk vkq of dim row r sits at chunk vkq ^ ((r >> 3) & 7): the
-    // 8 rows of one thread share r >> 3 = vdc, so the 16 vdc lanes of a
-    // store spread over 8 chunk columns instead of one bank pair
-    uint16_t* vb = vt_s + buf * kD * kFaVS + 4 * (vkq ^ (vdc & 7));
-    uint16_t* vh = vh_s + buf * kD * kFaVS + 4 * (vkq ^ (vdc & 7));
-    // fp16 copy: v_cvt_pkrtz is exact for every bf16 value in fp16's normal
-    // range and saturates beyond it; a bf16 magnitude of 0x4780 (2^16) or
-    // more -- past fp16's largest, 65504, or inf / NaN -- marks the block for
-    // the two-term product (|v| + 0x3880 carries into bit 15 of its half)
-    uint32_t sat = 0;
-    auto chk = [&](uint32_t w) { sat |= ((w & 0x7fff7fffu) + 0x38803880u) & 0x80008000u; };
-    chk(va0.x), chk(va0.y), chk(va0.z), chk(va0.w), chk(va1.x), chk(va1.y), chk(va1.z), chk(va1.w);
-    chk(va2.x), chk(va2.y), chk(va2.z), chk(va2.w), chk(va3.x), chk(va3.y), chk(va3.z), chk(va3.w);
-    if (sat != 0 && blk < 32 * kFaSatWords) atomicOr(&vsat[blk >> 5], 1u << (blk & 31));
+    // V^T tiles: 4-key chunk c of dim row d sits at chunk c ^ ((d >> 3) & 7)
+    // (a thread's rows share d >> 3, so the lanes of a store spread over 8
+    // chunk columns instead of one bank pair).  The fp16 copy comes from
+    // v_cvt_pkrtz, exact for every bf16 value in fp16's normal range and
+    // saturating beyond it; a bf16 magnitude of 0x4780 (2^16) or more --
+    // past fp16's largest, 65504, or inf / NaN -- marks the block for the
+    // two-term product (|v| + 0x3880 carries into bit 15 of its half)
     auto h2 = [](uint32_t lo16, uint32_t hi16) {
       return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(lo16 << 16),
                                                                      __uint_as_float(hi16 << 16)));
     };
-    auto vput = [&](int c, uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
-      const uint2 lo = make_uint2((a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16));
-      const uint2 hi = make_uint2((a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u));
-      *reinterpret_cast<uint2*>(vb + (vdc * 8 + 2 * c) * kFaVS) = lo;
-      *reinterpret_cast<uint2*>(vb + (vdc * 8 + 2 * c + 1) * kFaVS) = hi;
-      *reinterpret_cast<uint2*>(vh + (vdc * 8 + 2 * c) * kFaVS) =
-          make_uint2(h2(a0 & 0xffffu, a1 & 0xffffu), h2(a2 & 0xffffu, a3 & 0xffffu));
-      *reinterpret_cast<uint2*>(vh + (vdc * 8 + 2 * c + 1) * kFaVS) =
-          make_uint2(h2(a0 >> 16, a1 >> 16), h2(a2 >> 16, a3 >> 16));
+    auto mark = [&](uint32_t sat) {
+      if (sat != 0 && blk < 32 * kFaSatWords) atomicOr(&vsat[blk >> 5], 1u << (blk & 31));
     };
-    vput(0, va0.x, va1.x, va2.x, va3.x);
-    vput(1, va0.y, va1.y, va2.y, va3.y);
-    vput(2, va0.z, va1.z, va2.z, va3.z);
-    vput(3, va0.w, va1.w, va2.w, va3.w);
+    if constexpr (NW == 8) {
+      kput(0, r.kr0);
+      kput(1, r.kr1);
+      // keys 0..3 of the piece: words (dims 4 vd4, +1) and (+2, +3)
+      const uint32_t w[4][2] = {{r.kr2.x, r.kr2.y}, {r.kr2.z, r.kr2.w}, {r.kr3.x, r.kr3.y}, {r.kr3.z, r.kr3.w}};
+      // saturation: the largest magnitude of each half over the 8 words
+      u16x2_t mx = u16x2_t{0, 0};
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int e = 0; e < 2; e++)
+          mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, w[k][e] & 0x7fff7fffu));
+      mark((__builtin_bit_cast(uint32_t, mx) + 0x38803880u) & 0x80008000u);
+      const int cs = 4 * (vk4 ^ ((vd4 >> 1) & 7));
+      uint16_t* vb = vt_s + buf * kD * kFaVS + cs;
+      uint16_t* vh = vh_s + buf * kD * kFaVS + cs;
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        // dim rows 4 vd4 + 2 e (low halves) and + 1 (high halves): keys 0..3
+        const uint32_t a = w[0][e], b = w[1][e], c = w[2][e], d = w[3][e];
+        const int r0 = (4 * vd4 + 2 * e) * kFaVS, r1 = r0 + kFaVS;
+        *reinterpret_cast<uint2*>(vb + r0) =
+            make_uint2(__builtin_amdgcn_perm(b, a, 0x05040100u), __builtin_amdgcn_perm(d, c, 0x05040100u));
+        *reinterpret_cast<uint2*>(vb + r1) =
+            make_uint2(__builtin_amdgcn_perm(b, a, 0x07060302u), __builtin_amdgcn_perm(d, c, 0x07060302u));
+        *reinterpret_cast<uint2*>(vh + r0) = make_uint2(h2(a & 0xffffu, b & 0xffffu), h2(c & 0xffffu, d & 0xffffu));
+        *reinterpret_cast<uint2*>(vh + r1) = make_uint2(h2(a >> 16, b >> 16), h2(c >> 16, d >> 16));
+      }
+    } else {
+      kput(0, r.kr0);
+      kput(1, r.kr1);
+      kput(2, r.kr2);
+      kput(3, r.kr3);
+      const uint4 va0 = r.vr0, va1 = r.vr1, va2 = r.vr2, va3 = r.vr3;
+      // V^T: dim 8 vdc + d gets keys 4 vkq .. + 3 (8 bytes)
+      uint16_t* vb = vt_s + buf * kD * kFaVS + 4 * (vkq ^ (vdc & 7));
+      uint16_t* vh = vh_s + buf * kD * kFaVS + 4 * (vkq ^ (vdc & 7));
+      uint32_t sat = 0;
+      auto chk = [&](uint32_t w) { sat |= ((w & 0x7fff7fffu) + 0x38803880u) & 0x80008000u; };
+      chk(va0.x), chk(va0.y), chk(va0.z), chk(va0.w), chk(va1.x), chk(va1.y), chk(va1.z), chk(va1.w);
+      chk(va2.x), chk(va2.y), chk(va2.z), chk(va2.w), chk(va3.x), chk(va3.y), chk(va3.z), chk(va3.w);
+      mark(sat);
+      auto vput = [&](int c, uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
+        const uint2 lo = make_uint2((a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16));
+        const uint2 hi = make_uint2((a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u));
+        *reinterpret_cast<uint2*>(vb + (vdc * 8 + 2 * c) * kFaVS) = lo;
+        *reinterpret_cast<uint2*>(vb + (vdc * 8 + 2 * c + 1) * kFaVS) = hi;
+        *reinterpret_cast<uint2*>(vh + (vdc * 8 + 2 * c) * kFaVS) =
+            make_uint2(h2(a0 & 0xffffu, a1 & 0xffffu), h2(a2 & 0xffffu, a3 & 0xffffu));
+        *reinterpret_cast<uint2*>(vh + (vdc * 8 + 2 * c + 1) * kFaVS) =
+            make_uint2(h2(a0 >> 16, a1 >> 16), h2(a2 >> 16, a3 >> 16));
+      };
+      vput(0, va0.x, va1.x, va2.x, va3.x);
+      vput(1, va0.y, va1.y, va2.y, va3.y);
+      vput(2, va0.z, va1.z, va2.z, va3.z);
+      vput(3, va0.w, va1.w, va2.w, va3.w);
+    }
   };
 
   f32x4_t o[8];
@@ -761,6 +791,9 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
   for (int j = 0; j < 8; j++) o[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = -INFINITY, l_run = 0.0f;
   const int lim = p.causal ? min(L, offset + t + 1) : L;  // keys < lim are visible to query t
+  // keys below lim_w are visible to every query of the wave: a block
+  // entirely below it needs no mask
+  const int lim_w = p.causal ? min(L, offset + tw + 1) : L;
   const float scale2 = p.scale * 1.44269504088896340736f;  // scale * log2(e)
 
   Stage sg0 = load_block(0);
@@ -794,17 +827,25 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
       }
     }
     // ---- online softmax of the lane's query over the block's 64 keys, in
-    // base 2: scores carry scale * log2(e), p = 2^(s - m) on v_exp_f32 ----
+    // base 2: p = 2^(s c - m) with c = scale * log2(e) on v_exp_f32, the
+    // scaling fused into the exponent's FMA; the running max m is of the
+    // scaled scores, fl(max(s) c) = max(fl(s c)) as c > 0.  A masked key's
+    // score is -inf (a select), so its p is 0 ----
+    if (k0 + kFaK > lim_w) {  // uniform: the block reaches past some query's last key
+#pragma unroll
+      for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int key = k0 + kt * 16 + 4 * g + i;
+          sc[kt][i] = key < lim ? sc[kt][i] : -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int key = k0 + kt * 16 + 4 * g + i;
-        sc[kt][i] = key < lim ? sc[kt][i] * scale2 : -INFINITY;
-        mx = fmaxf(mx, sc[kt][i]);
-      }
-    mx = max_xor32(max_xor16(mx));
+      for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[kt][i]);
+    mx = max_xor32(max_xor16(mx)) * scale2;
     const float m_new = fmaxf(m_run, mx);
     // 2^(-inf) = 0 covers the first block (m_run = -inf) and masked keys; a
     // row with nothing visible yet keeps m = -inf and is skipped
@@ -828,8 +869,8 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int kt = 2 * c + (u >> 1), i0 = 2 * (u & 1);
-        const float r0 = __builtin_amdgcn_exp2f(sc[kt][i0] - m_use);
-        const float r1 = __builtin_amdgcn_exp2f(sc[kt][i0 + 1] - m_use);
+        const float r0 = __builtin_amdgcn_exp2f(fmaf(sc[kt][i0], scale2, -m_use));
+        const float r1 = __builtin_amdgcn_exp2f(fmaf(sc[kt][i0 + 1], scale2, -m_use));
         sum += r0 + r1;
         pv_[8 * c + 2 * u] = r0;
         pv_[8 * c + 2 * u + 1] = r1;
