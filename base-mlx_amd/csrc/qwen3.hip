@@ -49,7 +49,7 @@ struct QLin {
   uint16_t* s = nullptr;
   uint16_t* b = nullptr;
   int N = 0, K = 0;
-  // the group-major copy the prefill GEMMs read (q, k, v, gate and up;
+  // the group-major copy the prefill GEMMs read (layer projections;
   // launch_qmm_repack): W [K/64][N][8] words, s|b [K/64][N] words
   uint32_t* wt = nullptr;
   uint32_t* sbt = nullptr;
@@ -155,13 +155,6 @@ int alloc_qlin(bmx_qwen3* m, QLin* q, int N, int K, bool group_major = false) {
   if (int rc = dalloc_t(m, &q->wt, static_cast<size_t>(N) * (K / 8))) return rc;
   return dalloc_t(m, &q->sbt, static_cast<size_t>(N) * (K / 64));
 }
-
-// Projections whose prefill GEMM reads a group-major copy: q | k | v and
-// gate | up (M = 4096 on the Qwen3-4B shape: 159.7 -> 147.2 and 478.3 ->
-// 448.6 us per layer).  The o and down GEMMs, with the residual epilogue
-// and a long K, measured slower on it (207.3 -> 222.1 us) and keep MLX's
-// layout.
-bool group_major_slot(int slot) { return slot != SLOT_O && slot != SLOT_DOWN; }
 
 // Rewrites every group-major copy from its MLX-layout weight (after the
 // weights are set, or after a caller was handed pointers it may have
@@ -292,8 +285,8 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       p.part_floats = m->qmm_ws_floats;
       if (int rc = launch_qmv(p, QMV_RESIDUAL, st)) return rc;
     } else {
-      if (int rc = launch_qmm_epi(QMM_RESIDUAL, m->att, L.p[SLOT_O].w, L.p[SLOT_O].s, L.p[SLOT_O].b, nullptr, nullptr,
-                                  nullptr, m->x, m->x, M, H, qd, m->qmm_ws, m->qmm_ws_floats, st))
+      if (int rc = launch_qmm_epi_gm(QMM_RESIDUAL, m->att, L.p[SLOT_O].wt, L.p[SLOT_O].sbt, nullptr, nullptr, m->x,
+                                     m->x, M, H, qd, m->qmm_ws, m->qmm_ws_floats, st))
         return rc;
     }
     // ---- mlp_block + residual (kernels.rs:55-78; qwen3.rs:523-541) ----
@@ -335,8 +328,8 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
         if (int rc = launch_qmm(m->h, uw.w, uw.s, uw.b, m->u, M, I, H, m->qmm_ws, m->qmm_ws_floats, st)) return rc;
         if (int rc = launch_silu_mul(m->g, m->u, m->a, static_cast<int64_t>(M) * I, st)) return rc;
       }
-      if (int rc = launch_qmm_epi(QMM_RESIDUAL, m->a, L.p[SLOT_DOWN].w, L.p[SLOT_DOWN].s, L.p[SLOT_DOWN].b, nullptr,
-                                  nullptr, nullptr, m->x, m->x, M, H, I, m->qmm_ws, m->qmm_ws_floats, st))
+      if (int rc = launch_qmm_epi_gm(QMM_RESIDUAL, m->a, L.p[SLOT_DOWN].wt, L.p[SLOT_DOWN].sbt, nullptr, nullptr, m->x,
+                                     m->x, M, H, I, m->qmm_ws, m->qmm_ws_floats, st))
         return rc;
     }
   }
@@ -451,8 +444,7 @@ int qwen3_alloc(const bmx_qwen3_config* cfg, int max_tokens, bmx_qwen3** out) {
   const int dims[NSLOT][2] = {{qd, H}, {kvd, H}, {kvd, H}, {H, qd}, {I, H}, {I, H}, {H, I}};
   for (int l = 0; !rc && l < cfg->layers; l++) {
     Layer& L = m->layers[l];
-    for (int sl = 0; !rc && sl < NSLOT; sl++)
-      rc = alloc_qlin(m, &L.p[sl], dims[sl][0], dims[sl][1], group_major_slot(sl));
+    for (int sl = 0; !rc && sl < NSLOT; sl++) rc = alloc_qlin(m, &L.p[sl], dims[sl][0], dims[sl][1], true);
     if (!rc) rc = dalloc_t(m, &L.in_norm, static_cast<size_t>(H));
     if (!rc) rc = dalloc_t(m, &L.post_norm, static_cast<size_t>(H));
     if (!rc) rc = dalloc_t(m, &L.q_norm, static_cast<size_t>(cfg->head_dim));

@@ -281,17 +281,17 @@ def _write_projection(gpu, gm, layer, slot, arrays):
 
 
 def test_prefill_reads_weights_written_through_qlinear(gpu, orc):
-    """The prefill GEMMs of q | k | v and gate | up read a group-major copy
-    of their weights; a projection written through the pointers of
-    bmx_qwen3_qlinear is seen by the next prefill: with layer 1's gate and
-    layer 0's v projection replaced in both models the logits follow the
-    oracle's, and with the old weights written back they are the first
-    prefill's bit for bit."""
+    """The prefill GEMMs read a group-major copy of each layer projection;
+    a projection written through the pointers of bmx_qwen3_qlinear is seen
+    by the next prefill: with layer 1's gate and down and layer 0's v
+    projection replaced in both models the logits follow the oracle's, and
+    with the old weights written back they are the first prefill's bit for
+    bit."""
     gm, om = _pair(gpu, orc)
     toks = orc.fill_tokens(77, 40, SMALL["vocab"])
     g0 = torch_bf16_bits(gm.forward(gm.new_cache(64), toks, all_logits=True))
-    old = {key: [a.copy() for a in gm.qlinear_numpy(*key)] for key in [(1, 4), (0, 2)]}
-    for (layer, slot), seed in [((1, 4), 5), ((0, 2), 6)]:
+    old = {key: [a.copy() for a in gm.qlinear_numpy(*key)] for key in [(1, 4), (1, 6), (0, 2)]}
+    for (layer, slot), seed in [((1, 4), 5), ((1, 6), 7), ((0, 2), 6)]:
         w, s, b = old[(layer, slot)]
         rng = np.random.default_rng(seed)
         new = (rng.integers(0, 2**32, w.shape, dtype=np.uint32), s[::-1].copy(), b[:, ::-1].copy())
