@@ -620,7 +620,7 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
 // product against 4 waves over one head; with 8 waves, waves 0-3 stage V
 // and waves 4-7 stage K.
 constexpr int kFaQ = 64, kFaK = 64;  // queries per 4-wave workgroup, keys per block
-constexpr int kFaKS = kD + 8;        // K tile row stride (elements)
+constexpr int kFaKS = kD + 16;       // K tile row stride (elements)
 constexpr int kFaVS = kFaK + 8;      // V^T tile row stride (elements)
 // K, V^T (bf16) and V^T (fp16), double-buffered
 constexpr size_t kFaLds = 2ull * (kFaK * kFaKS + 2 * kD * kFaVS) * sizeof(uint16_t);
