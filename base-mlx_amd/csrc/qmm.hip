@@ -12,13 +12,13 @@
 // Workgroup tile: 128 rows of x by 128 rows of W, 4 waves (2 x 2), each
 // 64 x 64 = 4 x 4 tiles of v_mfma_f32_16x16x32_bf16, 3 workgroups per CU;
 // on large grids 128 x 256 (waves of 64 x 128, 2 workgroups per CU).  Per K
-// step (one 64-wide group) the workgroup stages x (128 x 64 bf16) and the
-// dequantized W tile (128 or 256 x 64 bf16: nibble bytes
-// through v_cvt_f32_ubyte, one FMA, v_cvt_pk_bf16_f32 per pair) in LDS.  The
-// next group's global loads are issued before this group's products and
-// land in LDS after them.  When the tile grid is small, K is split over
-// workgroups: fp32 partial tiles go to a workspace and a reduction kernel
-// writes y.
+// step (one 64-wide group) the workgroup has x (128 x 64 bf16) and the
+// dequantized W tile (128 or 256 x 64 bf16: nibble bytes through
+// v_cvt_f32_ubyte, one FMA, v_cvt_pk_bf16_f32 per pair) in LDS: x comes
+// straight from memory into one of two LDS tiles (global_load_lds_dwordx4)
+// a group ahead, W through registers.  When the tile grid is small, K is
+// split over workgroups: fp32 partial tiles go to a workspace and a
+// reduction kernel writes y.
 //
 // Epilogues (the prefill's MLX op sequence fused, with the same bf16
 // roundings): store; residual, y = res + bf16(x W^T) (qwen3.rs:520-521, 541);
@@ -49,8 +49,9 @@ constexpr int QBM = 128, QBN = 128, QT = 256;  // tile rows of x, of W; threads
 // bytes) left the operand reads or the W stores 4-8 cycles per instruction
 // in conflicts.
 constexpr int RS = 64;  // LDS row stride (elements)
-// LDS of a workgroup with a BN-row W tile: 32 KB (BN 128) or 48 KB (BN 256)
-constexpr size_t qmm_lds(int bn) { return (1ull * QBM * RS + 1ull * bn * RS) * 2; }
+// LDS of a workgroup with a BN-row W tile: two x tiles and the W tile
+// (48, 52 or 64 KB for BN 128, 160, 256)
+constexpr size_t qmm_lds(int bn) { return (2ull * QBM * RS + 1ull * bn * RS) * 2; }
 // 256-row W tiles where the grid of them still spans two or more rounds of
 // the 512 resident workgroups they allow (2 per CU): at M = 4096 on
 // 12288 x 4096 / 9728 x 2560 / 19456 x 2560, 10-17% faster than 128-row
@@ -120,8 +121,8 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   constexpr int NJ = BN / 32;                // 16-row W tiles per wave
   constexpr int WR = (BN + 127) / 128;       // W rows staged per thread (the second only below BN)
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [QBM][RS], swizzled
-  uint16_t* ws = xs + QBM * RS;                      // [BN][RS], swizzled
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [2][QBM][RS], swizzled
+  uint16_t* ws = xs + 2 * QBM * RS;                  // [BN][RS], swizzled
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;  // wave sub-tile: x rows 64 wm, W rows BN/2 wn
   const int li = lane & 15, q = lane >> 4;
@@ -180,13 +181,23 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     }
   }
 
-  // ---- global -> registers for one group (rows clamped: their results are
-  // never stored) ----
-  auto xrow = [&](int e) { return p.x + static_cast<int64_t>(min(m0 + (e >> 3), M - 1)) * K + (e & 7) * 8; };
-  const uint16_t* xp0 = xrow(tid);
-  const uint16_t* xp1 = xrow(tid + QT);
-  const uint16_t* xp2 = xrow(tid + 2 * QT);
-  const uint16_t* xp3 = xrow(tid + 3 * QT);
+  // ---- global -> LDS / registers for one group (rows clamped: their
+  // results are never stored) ----
+  // x straight into LDS (global_load_lds_dwordx4: lane l's 16 bytes land
+  // at the instruction's LDS base + 16 l): wave w's instruction i fills
+  // tile rows 8 (4 i + w) .. + 7, lane l row l / 8 and physical chunk l % 8,
+  // so it loads logical chunk (l % 8) ^ (row & 7), the swz layout
+  const uint16_t* xd[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int row = 8 * (4 * i + wave) + (lane >> 3), lc = (lane & 7) ^ (row & 7);
+    xd[i] = p.x + static_cast<int64_t>(min(m0 + row, M - 1)) * K + lc * 8;
+  }
+  auto issue_x = [&](int g, uint16_t* xb) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      __builtin_amdgcn_global_load_lds(xd[i] + g * 64, xb + 512 * (4 * i + wave), 16, 0, 0);
+  };
   // W rows wr (and wr + 128 with BN 256) of the tile, half wh of the group
   const int wr = tid >> 1, wh = tid & 1;
   // SwiGLU: each wave's BN / 2 W rows are BN / 4 gate rows and the up rows
@@ -214,23 +225,19 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   // (BN 160: the second row exists for wr < 32, i.e. wave 0; uniform per wave)
   const bool row1 = WR == 2 && wr + 128 < BN;
   if (row1) wsrc(wr + 128, wp1, sp1, bp1, sbp1);
-  // One group's operands in registers: x (4 x 16 bytes per thread), W (one
-  // or two 16-byte row halves) and their scales and biases -- one word
-  // s | b << 16 per row in the group-major layout, two 16-bit loads in
-  // MLX's.  Raw loaded words only: the split into s and b happens at the
-  // store, so no wait for a load comes before its data is needed.  Plain
-  // members passed by value, so a set stays in registers.
+  // One group's W operands in registers: one or two 16-byte row halves and
+  // their scales and biases -- one word s | b << 16 per row in the
+  // group-major layout, two 16-bit loads in MLX's.  Raw loaded words only:
+  // the split into s and b happens at the store, so no wait for a load
+  // comes before its data is needed.  Plain members passed by value, so a
+  // set stays in registers.
   struct QStage {
-    uint4 x0, x1, x2, x3, w0, w1;
+    uint4 w0, w1;
     uint32_t sb0, sb1;
     uint16_t s0, b0, s1, b1;
   };
   auto load = [&](int g) {
     QStage r;
-    r.x0 = *reinterpret_cast<const uint4*>(xp0 + g * 64);
-    r.x1 = *reinterpret_cast<const uint4*>(xp1 + g * 64);
-    r.x2 = *reinterpret_cast<const uint4*>(xp2 + g * 64);
-    r.x3 = *reinterpret_cast<const uint4*>(xp3 + g * 64);
     if constexpr (GM) {
       const int64_t go = static_cast<int64_t>(g) * N;
       r.w0 = *reinterpret_cast<const uint4*>(wp0 + go * 8);
@@ -251,13 +258,8 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     }
     return r;
   };
-  // ---- registers -> LDS: x as is, W dequantized to bf16 ----
+  // ---- registers -> LDS: W dequantized to bf16 ----
   auto store = [&](const QStage r) {
-    auto put_x = [&](int e, const uint4& v) { *reinterpret_cast<uint4*>(xs + swz(e >> 3, e & 7)) = v; };
-    put_x(tid, r.x0);
-    put_x(tid + QT, r.x1);
-    put_x(tid + 2 * QT, r.x2);
-    put_x(tid + 3 * QT, r.x3);
     // sv, bv: the row's scale and bias as floats
     auto put_row = [&](int row, const uint4 wq, float sv, float bv) {
       auto put_word = [&](int chunk, uint32_t word) {
@@ -297,13 +299,13 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     for (int j = 0; j < NJ; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // ---- the products of one group from LDS ----
-  auto compute = [&]() {
+  auto compute = [&](const uint16_t* xt) {
     bf16x8_t af[4][2];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int t = 0; t < 2; t++)
-        af[i][t] = *reinterpret_cast<const bf16x8_t*>(xs + swz(wm * 64 + i * 16 + li, t * 4 + q));
+        af[i][t] = *reinterpret_cast<const bf16x8_t*>(xt + swz(wm * 64 + i * 16 + li, t * 4 + q));
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
       const int c = wn * (BN / 2) + j * 16 + li;
@@ -317,45 +319,30 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     }
   };
 
-  if constexpr (BN == 128) {
-    // Two register sets: group g + 2's loads go out while group g's
-    // products run and group g + 1 moves from registers into LDS, so a load
-    // has two steps to return.  At the end the last group is requested
-    // again: every step issues the same loads, so each wait is for one
-    // specific group.  (Qwen3-4B q | k | v at 4096 tokens: 150.6 -> 144.6
-    // us; the 160-row tiles of o and down measured slower with two sets,
-    // 203.4 -> 217.7 us, and the 256-row ones have no registers for them.)
-    QStage sa = load(gb), sb = load(min(gb + 1, ge - 1));
-    store(sa);
-    __syncthreads();
-    auto step = [&](const int g, auto par_c) {
-      constexpr int P = decltype(par_c)::value;
-      if constexpr (P == 0) sa = load(min(g + 2, ge - 1));
-      else sb = load(min(g + 2, ge - 1));
-      compute();
-      if (g + 1 < ge) {
-        __syncthreads();  // every read of this group's tiles is done
-        store(P == 0 ? sb : sa);
-        __syncthreads();
-      }
-    };
-    for (int g = gb; g < ge; g += 2) {
-      step(g, std::integral_constant<int, 0>{});
-      if (g + 1 < ge) step(g + 1, std::integral_constant<int, 1>{});
+  // x of group g + 1 goes straight into the other x tile while group g's
+  // products run; W and s|b come through registers, dequantized into the one
+  // W tile once every read of the last group's is done.  (Against x staged
+  // through registers and two W register sets for 128-row tiles, Qwen3-4B
+  // 4096-token prefill: q | k | v 139.5 -> 136.8 us, o / down 174.9 ->
+  // 171.4, gate | up 423.0 -> 418.6.)
+  issue_x(gb, xs);
+  QStage sa = load(gb);
+  store(sa);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // x of group gb is in LDS
+  __syncthreads();
+  for (int g = gb; g < ge; g++) {
+    const int cur = (g - gb) & 1;
+    const bool more = g + 1 < ge;
+    if (more) {
+      issue_x(g + 1, xs + (cur ^ 1) * QBM * RS);
+      sa = load(g + 1);
     }
-  } else {
-    QStage sa = load(gb);
+    compute(xs + cur * QBM * RS);
+    if (!more) break;
+    __syncthreads();  // every read of this group's W tile (and x tile) is done
     store(sa);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // x of group g + 1 is in LDS
     __syncthreads();
-    for (int g = gb; g < ge; g++) {
-      const bool more = g + 1 < ge;
-      if (more) sa = load(g + 1);
-      compute();
-      if (!more) break;
-      __syncthreads();  // every read of this group's tiles is done
-      store(sa);
-      __syncthreads();
-    }
   }
 
   // ---- epilogue: lane holds W row 16 j + li, x rows 4 q + r of each tile ----
