@@ -490,6 +490,28 @@ def profile_mfma(bmx, torch, launches=20):
     log(f"profile-mfma: {launches} causal prefill attentions, 4096 tokens, 32 q / 8 kv heads")
 
 
+def profile_bf16_gemm(torch, launches=50):
+    """Reference figures for the prefill GEMMs: torch.matmul (hipBLASLt) on bf16
+    operands of the Qwen3-4B 4096-token prefill shapes (x [4096, K] times a
+    bf16 W^T [K, N]), timed with HIP events over `launches` back-to-back calls."""
+    for name, (N, K) in [("q|k|v", (6144, 2560)), ("o", (2560, 4096)), ("gate|up", (19456, 2560)),
+                         ("down", (2560, 9728))]:
+        x = torch.randn(4096, K, device="cuda", dtype=torch.bfloat16)
+        w = torch.randn(N, K, device="cuda", dtype=torch.bfloat16)
+        for _ in range(5):
+            y = x @ w.t()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(launches):
+            y = x @ w.t()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / launches
+        log(f"bf16 GEMM ({name}) 4096 x {N} x {K}: {us:.1f} us, {2 * 4096 * N * K / us / 1e6:.0f} TFLOP/s")
+        del x, w, y
+
+
 def cpu_baseline(tokens, ctx=4096, seed=42):
     """Oracle decode of `tokens` tokens at context `ctx` on the host cores."""
     import numpy as np
@@ -534,6 +556,8 @@ def main():
                     help="only run the roofline GEMV and a copy of known size (for rocprofv3 --pmc)")
     ap.add_argument("--profile-mfma", action="store_true",
                     help="only run the M = 2048 GEMMs and a 4096-token prefill attention (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-bf16-gemm", action="store_true",
+                    help="only time torch.matmul (hipBLASLt) on bf16 operands of the 4096-token prefill GEMM shapes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)", file=sys.stderr)
@@ -550,6 +574,9 @@ def main():
         return
     if args.profile_mfma:
         profile_mfma(bmx, torch)
+        return
+    if args.profile_bf16_gemm:
+        profile_bf16_gemm(torch)
         return
     cap = args.prompt + max(args.steps, args.warmup)
     stream = torch.cuda.Stream()
