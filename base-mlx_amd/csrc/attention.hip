@@ -12,14 +12,16 @@
 // Two kernels, chosen by the number of query rows per kv head
 // (R = new tokens x q heads per kv head):
 //   R <= 64 (decode, speculative verify): attn_decode_kernel splits the key
-//     range over workgroups of 256 keys (flash-decoding) and
-//     attn_combine_kernel merges the unnormalised partials (o, m, l);
+//     range over workgroups of 256 keys (flash-decoding), and the last
+//     workgroup of each kv head to finish merges the unnormalised partials
+//     (o, m, l);
 //   otherwise (prefill): attn_prefill_kernel, flash attention with one
 //     workgroup per (query head, 64 query tokens) walking all visible keys.
 // Both run Q K^T and (prefill) P V on the matrix cores.
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "bmx_device.h"
 
@@ -44,6 +46,7 @@ struct AttnParams {
   int causal;
   float scale;
   int kps;    // keys per split (decode kernel: a multiple of 32, at most 256)
+  int local;  // decode kernel: every workgroup of a kv head runs on one XCD (shares its L2)
 };
 
 // Inputs of the fused QK-norm + RoPE + KV-write prologue of the decode
@@ -58,8 +61,8 @@ struct FuseParams {
   RopeTable tab;
 };
 
-// The split partials travel between workgroups on different XCDs (each with
-// its own L2).  Every access to them is agent-coherent: the writers store
+// In general the split partials travel between workgroups on different XCDs
+// (each with its own L2).  Every access to them is then agent-coherent: the writers store
 // them with agent-scope atomic stores (relaxed, issued with sc1: written
 // through to memory), every thread waits for its stores to complete
 // (s_waitcnt), the workgroup meets at a barrier, and one thread bumps the
@@ -69,21 +72,44 @@ struct FuseParams {
 // increment is issued and the loads are issued after it returned, so the
 // loads see them; no L2 write-back (release) or invalidation (acquire) is
 // needed, and these cost microseconds when many workgroups issue them.
-// This holds only while store_agent2 (and the s_waitcnt before the arrival)
+// This holds only while store_part2<false> (and the s_waitcnt before the arrival)
 // stays the only way the partials are written: a plain store into the
 // split workspace could sit in one XCD's L2, and would need the release
 // increment and the acquire fence back.
 // Pairs of floats are stored as one 8-byte access (8-byte aligned addresses).
-__device__ __forceinline__ void store_agent2(float* a, float x, float y) {
-  const uint64_t v = static_cast<uint64_t>(__float_as_uint(x)) | (static_cast<uint64_t>(__float_as_uint(y)) << 32);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(a), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+//
+// XCD-local variant (AttnParams::local).  The hardware hands the workgroups
+// of a launch to the XCDs round-robin by linear workgroup id, so with the
+// kv head on the grid's x axis and a multiple of 8 kv heads, every
+// workgroup of one kv head runs on the same XCD (checked on the device
+// before the variant is first used: xcd_local_ok).  The partials and the
+// arrival then never leave that XCD's L2: plain stores (complete once the
+// L2 holds them), an increment executed in the L2 (workgroup scope), and
+// merge loads with sc0, which miss in the merging CU's L1 and are served by
+// the L2.  The local counters live 256 bytes from the agent-scope ones
+// (kLocalCounter), so a cache line is only ever updated in one place: in
+// memory by agent-scope increments or in an L2 by local ones.  Every
+// launch leaves each counter at zero, and writes every partial it merges
+// (on the merging XCD) before reading it, so nothing that another XCD's L2
+// held from an earlier launch is read.
+template <bool LOCAL>
+__device__ __forceinline__ void store_part2(float* a, float x, float y) {
+  if constexpr (LOCAL) {
+    *reinterpret_cast<float2*>(a) = make_float2(x, y);
+  } else {
+    const uint64_t v =
+        static_cast<uint64_t>(__float_as_uint(x)) | (static_cast<uint64_t>(__float_as_uint(y)) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(a), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // Third word of a raw gfx9 buffer resource (no format conversion, range
 // checked against num_records in bytes)
 constexpr int kBufferConfig = 0x00020000;
-// Buffer-load cache policy sc1: agent-coherent
+// Buffer-load cache policies: sc1 (agent-coherent) and sc0 (misses in L1,
+// served by the XCD's L2)
 constexpr int kAgentCoherent = 16;
+constexpr int kL2Coherent = 1;
 
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
@@ -112,7 +138,7 @@ struct Fold {
 // context, not on the row, so they leave a row's bits unchanged.  Each half
 // of the wave folds its splits in increasing order; the halves are added at
 // the end (merge_halves).
-template <int NR>
+template <int NR, int AUX>
 __device__ __forceinline__ void combine_splits(const AttnParams& p, const int (&wids)[NR], int lane, int ns,
                                                Fold (&r)[NR]) {
   constexpr int B = 24;  // 16-byte o loads per row and batch: 48 splits
@@ -133,12 +159,11 @@ __device__ __forceinline__ void combine_splits(const AttnParams& p, const int (&
           p.part_ml + base * 2, static_cast<short>(0), nb * 8, kBufferConfig);
       const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
           p.part_o + base * kD, static_cast<short>(0), nb * kD * 4, kBufferConfig);
-      ml[i] = __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rml, min(lane, nb - 1) * 8, 0,
-                                                                               kAgentCoherent));
+      ml[i] = __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rml, min(lane, nb - 1) * 8, 0, AUX));
 #pragma unroll
       for (int u = 0; u < B; u++)
         ov[i][u] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   ro, (min(2 * u + half, nb - 1) * kD + dl) * 4, 0, kAgentCoherent));
+                                                   ro, (min(2 * u + half, nb - 1) * kD + dl) * 4, 0, AUX));
     }
     // every load of the batch goes out before any use of the first
     __builtin_amdgcn_sched_barrier(0);
@@ -189,6 +214,29 @@ __device__ __forceinline__ void store_fold(const AttnParams& p, int wid, int lan
   *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
 }
 
+// The merge by the last workgroup of a (kv head, row tile): rows w0 ..
+// w0 + RT - 1, one per wave; with more rows than waves, a wave folds two
+// rows with the loads of both in flight together.  AUX: the cache policy of
+// the partial loads.
+template <int NW, int AUX>
+__device__ __forceinline__ void merge_rows(const AttnParams& p, int w0, int RT, int wave, int lane, int ns) {
+  if (RT <= NW) {
+    if (wave < RT) {
+      const int wid[1] = {w0 + wave};
+      Fold r[1];
+      combine_splits<1, AUX>(p, wid, lane, ns, r);
+      store_fold(p, wid[0], lane, r[0]);
+    }
+  } else {
+    const int rb = min(wave + NW, RT - 1);
+    const int wid[2] = {w0 + wave, w0 + rb};
+    Fold r[2];
+    combine_splits<2, AUX>(p, wid, lane, ns, r);
+    store_fold(p, wid[0], lane, r[0]);
+    if (wave + NW < RT) store_fold(p, wid[1], lane, r[1]);
+  }
+}
+
 
 // Decode / short verify (R = tokens x heads-per-kv-head query rows of one kv
 // head, up to 64).  A workgroup of NW waves owns one kv head, one tile of
@@ -224,13 +272,15 @@ constexpr int kDecMaxRows = 64;  // query rows per kv head on this path
 constexpr int kMergeRows = 8;    // rows merged per LDS pass
 constexpr int kFuseMaxM = 16;    // new tokens of the fused prologue
 constexpr int kQS = kD + 8;      // LDS row stride of the prologue's q / k rows
-// Arrival counters at the head of the workspace, one per (kv head, row
-// tile), each in its own 256-byte block: agent-scope atomics on one memory
-// line complete one after another, so counters packed into one line made
-// the arrivals of every kv head queue on each other
-constexpr int kCounterStride = 64;                        // uints
+// Arrival counters at the head of the workspace, one block of 512 bytes per
+// (kv head, row tile): agent-scope atomics on one memory line complete one
+// after another, so counters packed into one line made the arrivals of
+// every kv head queue on each other.  The block's first word is the
+// agent-scope counter, the word 256 bytes on the XCD-local one.
+constexpr int kCounterStride = 128;                       // uints
 constexpr int kMaxCounters = 64;                          // kv heads x row tiles
 constexpr int kCounters = kMaxCounters * kCounterStride;  // floats
+constexpr int kLocalCounter = 64;                         // uints into the block
 template <int RMAX, bool FUSED, int NW>
 __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p, const FuseParams f) {
   __shared__ __align__(16) float ps[NW][kDecWaveKeys][RMAX];
@@ -548,9 +598,15 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
       // (h * M + token) * ns + split
       const int64_t base = (static_cast<int64_t>(kvh) * R + r0 + r) * p.ns + split;
       float* po = p.part_o + base * kD + d4 * 4;
-      store_agent2(po, o.x, o.y);
-      store_agent2(po + 2, o.z, o.w);
-      if (d4 == 0) store_agent2(p.part_ml + base * 2, m, l);
+      if (p.local) {
+        store_part2<true>(po, o.x, o.y);
+        store_part2<true>(po + 2, o.z, o.w);
+        if (d4 == 0) store_part2<true>(p.part_ml + base * 2, m, l);
+      } else {
+        store_part2<false>(po, o.x, o.y);
+        store_part2<false>(po + 2, o.z, o.w);
+        if (d4 == 0) store_part2<false>(p.part_ml + base * 2, m, l);
+      }
     }
   }
   // ---- the last of the ns_live workgroups of this (kv head, row tile) merges ----
@@ -562,29 +618,21 @@ __global__ void __launch_bounds__(64 * NW) attn_decode_kernel(const AttnParams p
     // stores (agent-coherent) completed before the barrier above; the last
     // arrival's threads read the partials with agent-coherent loads after
     // the next barrier.
-    last = __builtin_amdgcn_atomic_inc32(p.cnt + (kvh * gridDim.z + blockIdx.z) * kCounterStride,
-                                         static_cast<unsigned>(ns_live - 1), __ATOMIC_RELAXED,
-                                         "agent") == static_cast<unsigned>(ns_live - 1);
+    // (XCD-local: the same with the increment executed in the L2 that holds
+    // the partials; their stores completed there.)
+    unsigned* const c = p.cnt + (kvh * gridDim.z + blockIdx.z) * kCounterStride;
+    const unsigned wrap = static_cast<unsigned>(ns_live - 1);
+    if (p.local)
+      last = __builtin_amdgcn_atomic_inc32(c + kLocalCounter, wrap, __ATOMIC_RELAXED, "workgroup") == wrap;
+    else
+      last = __builtin_amdgcn_atomic_inc32(c, wrap, __ATOMIC_RELAXED, "agent") == wrap;
   }
   __syncthreads();
   if (!last) return;
-  // one row per wave; with more rows than waves, a wave folds two rows with
-  // the loads of both in flight together
-  if (RT <= NW) {
-    if (wave < RT) {
-      const int wid[1] = {kvh * R + r0 + wave};
-      Fold r[1];
-      combine_splits<1>(p, wid, lane, ns_live, r);
-      store_fold(p, wid[0], lane, r[0]);
-    }
-  } else {
-    const int rb = min(wave + NW, RT - 1);
-    const int wid[2] = {kvh * R + r0 + wave, kvh * R + r0 + rb};
-    Fold r[2];
-    combine_splits<2>(p, wid, lane, ns_live, r);
-    store_fold(p, wid[0], lane, r[0]);
-    if (wave + NW < RT) store_fold(p, wid[1], lane, r[1]);
-  }
+  if (p.local)
+    merge_rows<NW, kL2Coherent>(p, kvh * R + r0, RT, wave, lane, ns_live);
+  else
+    merge_rows<NW, kAgentCoherent>(p, kvh * R + r0, RT, wave, lane, ns_live);
 }
 
 // Prefill / long verify: flash attention on MFMA.  A workgroup of 4 waves
@@ -983,6 +1031,58 @@ size_t attention_workspace_floats(int Hq, int M, int ns) {
 
 namespace {
 
+// ---- where the workgroups of a launch run: the XCD-local merge's premise ----
+// xcd_probe_kernel records the XCD (hardware register XCC_ID) of every
+// workgroup of a grid shaped like the decode kernel's (x = 8 kv heads);
+// the merge may stay in one L2 when every workgroup with the same x runs on
+// one XCD.  Checked once per device, at the first uncaptured call.
+constexpr int kProbeX = 8, kProbeY = 24, kProbeZ = 3;  // 576 workgroups
+constexpr int kProbeWgs = kProbeX * kProbeY * kProbeZ;
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) unsigned xcd_probe_out[kProbeWgs];
+
+__global__ void __launch_bounds__(64) xcd_probe_kernel(unsigned* out) {
+  // s_getreg_b32 of XCC_ID (hardware register 20), bits 0-3
+  if (threadIdx.x == 0)
+    out[blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] =
+        __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) & 15u;
+}
+
+std::mutex g_xcd_mu;
+signed char g_xcd_local[kMaxDevices];  // 0 unchecked, 1 holds, -1 does not
+
+bool xcd_local_ok(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return false;
+  }
+  std::lock_guard<std::mutex> lock(g_xcd_mu);
+  if (g_xcd_local[dev]) return g_xcd_local[dev] > 0;
+  // not under capture: the check waits for its result (a later call checks)
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  if (cs != hipStreamCaptureStatusNone) return false;
+  void* ptr = nullptr;
+  unsigned host[kProbeWgs];
+  bool ok = hipGetSymbolAddress(&ptr, HIP_SYMBOL(xcd_probe_out)) == hipSuccess;
+  if (ok) {
+    hipLaunchKernelGGL(xcd_probe_kernel, dim3(kProbeX, kProbeY, kProbeZ), dim3(64), 0, stream,
+                       static_cast<unsigned*>(ptr));
+    ok = hipGetLastError() == hipSuccess &&
+         hipMemcpyAsync(host, ptr, sizeof host, hipMemcpyDeviceToHost, stream) == hipSuccess &&
+         hipStreamSynchronize(stream) == hipSuccess;
+  }
+  if (!ok) (void)hipGetLastError();
+  for (int i = 0; ok && i < kProbeWgs; i++) ok = host[i] == host[i % kProbeX];
+  g_xcd_local[dev] = ok ? 1 : -1;
+  return ok;
+}
+
 // The split-key decode path, if the call fits it: R = M * rep <= 64 rows per
 // kv head, a workspace with room for one split per 256 keys, and (fused) at
 // most kFuseMaxM new tokens.  Returns kNoFit when it does not apply.
@@ -1021,6 +1121,9 @@ int launch_decode(const AttnParams& base, const FuseParams* fuse, float* ws, siz
   p.ns = chunks;
   p.kps = kps;
   p.causal = M > 1 ? 1 : 0;
+  // x = kv head: with a multiple of 8 kv heads, every workgroup of a kv
+  // head shares the XCD of its x
+  p.local = Hkv % 8 == 0 && xcd_local_ok(stream);
   const FuseParams f = fuse ? *fuse : FuseParams{};
   const dim3 grid(Hkv, chunks, tiles), block(64 * nw);
 #define BMX_DECODE_LAUNCH(RM, NW)                                                        \
@@ -1051,6 +1154,8 @@ int check_attention_shape(int Hq, int Hkv, int M, int D, int cap, int offset, co
 }
 
 }  // namespace
+
+void attention_prepare(hipStream_t stream) { (void)xcd_local_ok(stream); }
 
 int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, float* ws,
                      size_t ws_floats, int Hq, int Hkv, int M, int D, int cap, int offset, const int* offset_dev,

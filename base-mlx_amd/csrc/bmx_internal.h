@@ -171,6 +171,9 @@ constexpr int kNoFit = -100;
 // Attention workspace (floats): arrival counters, then split partials; the
 // counters must be zero before the first call, and every call leaves them so.
 size_t attention_workspace_floats(int Hq, int M, int ns);
+// Runs the decode kernel's one-time device check (waits for the stream);
+// call before capturing a graph that holds decode attention.
+void attention_prepare(hipStream_t stream);
 // QK-norm + RoPE + KV write + decode attention in one kernel; kNoFit unless
 // M <= 16, M * (Hq / Hkv) <= 64 and ws holds one split per 256 keys of L_max.
 int launch_qkv_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,

@@ -474,6 +474,7 @@ int qwen3_alloc(const bmx_qwen3_config* cfg, int max_tokens, bmx_qwen3** out) {
   if (!rc) rc = dalloc_t(m, &m->attn_ws, m->attn_ws_floats);
   // the arrival counters at its head start at zero (and every call leaves them so)
   if (!rc) rc = check_hip(hipMemsetAsync(m->attn_ws, 0, m->attn_ws_floats * sizeof(float), st), "hipMemsetAsync");
+  if (!rc) attention_prepare(st);
   for (int sl = 0; sl < NSLOT; sl++)
     m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmm_workspace_floats(max_tokens, dims[sl][0], dims[sl][1]));
   m->qmm_ws_floats = std::max(m->qmm_ws_floats, qmm_workspace_floats(max_tokens, cfg->vocab, H));
