@@ -130,9 +130,10 @@ struct Fold {
 // into r[i]; one wave.  Splits come in batches of 48 at fixed boundaries:
 // lane s loads the (max, sum) pair of split s0 + s (one load per row), and
 // each 16-byte load of o partials brings split s0 + 2u to lanes 0-31 and
-// split s0 + 2u + 1 to lanes 32-63 (24 loads per row and batch, every load
-// of the batch issued before the first is used, from clamped addresses so
-// that the count in flight is fixed).  The weights exp(m_s - max) come from
+// split s0 + 2u + 1 to lanes 32-63 (up to 24 loads per row and batch, one
+// per pair of splits present, every load of the batch issued before the
+// first is used; an odd count's last upper half reads the last split
+// again, from a clamped address, and is never weighted).  The weights exp(m_s - max) come from
 // the lane that holds m_s; a split without visible keys (m = -inf) is left
 // out -- how many such trailing splits a launch has depends on its
 // context, not on the row, so they leave a row's bits unchanged.  Each half
@@ -161,9 +162,12 @@ __device__ __forceinline__ void combine_splits(const AttnParams& p, const int (&
           p.part_o + base * kD, static_cast<short>(0), nb * kD * 4, kBufferConfig);
       ml[i] = __builtin_bit_cast(f32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rml, min(lane, nb - 1) * 8, 0, AUX));
 #pragma unroll
-      for (int u = 0; u < B; u++)
-        ov[i][u] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   ro, (min(2 * u + half, nb - 1) * kD + dl) * 4, 0, AUX));
+      for (int u = 0; u < B; u++) {
+        // only the pairs that hold splits (uniform); the fold stops there
+        ov[i][u] = 2 * u < nb ? __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                ro, (min(2 * u + half, nb - 1) * kD + dl) * 4, 0, AUX))
+                              : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
     }
     // every load of the batch goes out before any use of the first
     __builtin_amdgcn_sched_barrier(0);
