@@ -103,7 +103,7 @@ int launch_qmm_segments(const uint16_t* x, int nseg, const uint32_t* const* w, c
 // (res may alias y); SwiGLU of the gate W and up W2 weights,
 // y = bf16(silu(bf16(x W^T)) * bf16(x W2^T)) with MLX's roundings.  SwiGLU
 // returns kNoFit (nothing launched) when the shape would split K.
-enum QmmEpilogue { QMM_STORE = 0, QMM_RESIDUAL = 1, QMM_SWIGLU = 2 };
+enum QmmEpilogue { QMM_STORE = 0, QMM_RESIDUAL = 1, QMM_SWIGLU = 2, QMM_QKV_ROPE = 3 };
 int launch_qmm_epi(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
                    const uint32_t* w2, const uint16_t* s2, const uint16_t* b2, const uint16_t* res, uint16_t* y, int M,
                    int N, int K, float* ws, size_t ws_floats, hipStream_t stream);
@@ -153,6 +153,31 @@ int launch_qk_norm_rope_kv(const uint16_t* q, const uint16_t* k, const uint16_t*
                            const uint16_t* k_norm, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int M,
                            int Hq, int Hkv, int D, int cap, int offset, const int* offset_dev, float eps,
                            const RopeTable& tab, hipStream_t stream);
+// (cos, sin) of the rotation of M tokens at positions offset + t (or
+// *offset_dev + t), frequency i < 64 at cs[t * 64 + i]: the values the
+// QK-norm / RoPE kernels compute per token (head_dim 128)
+int launch_rope_cs(float2* cs, int M, int offset, const int* offset_dev, const RopeTable& tab, hipStream_t stream);
+// Outputs of the q|k|v GEMM with the QK-norm / RoPE / KV-write epilogue
+// (the operation of launch_qk_norm_rope_kv, head_dim 128): q rotated into
+// q_out [Hq, M, 128], k rotated and v into the caches [Hkv, cap, 128] at
+// rows offset + t; cs from launch_rope_cs
+struct QkvRopeOut {
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  uint16_t* q_out;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  const float2* cs;
+  const int* offset_dev;
+  int offset;
+  int cap;
+  float eps;
+};
+// The q|k|v GEMM (group-major weights, segments q, k, v of n[i] columns,
+// whole 128-column head tiles) with that epilogue; kNoFit where the GEMM
+// would split K or take 256-column tiles (nothing launched).
+int launch_qmm_qkv_rope_gm(const uint16_t* x, const uint32_t* const* w, const uint32_t* const* sb, const int* n,
+                           int M, int K, const QkvRopeOut& out, hipStream_t stream);
 // A weight tensor of a bmx_qwen3 under its MLX checkpoint name: rows x cols
 // of uint32 (packed 4-bit weights) or bf16 (scales, biases, norm weights).
 struct WeightSlot {

@@ -211,6 +211,28 @@ int launch_qk_norm_rope_kv(const uint16_t* q, const uint16_t* k, const uint16_t*
   return check_launch("qk_norm_rope_kv");
 }
 
+namespace {
+
+__global__ void __launch_bounds__(256) rope_cs_kernel(float2* cs, int M, int offset, const int* offset_dev,
+                                                      const RopeTable tab) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= static_cast<int64_t>(M) * 64) return;
+  const int t = static_cast<int>(e >> 6), i = static_cast<int>(e & 63);
+  const int off = offset_dev ? *offset_dev : offset;
+  float c, s;
+  rope_cs(tab.inv_freq[i], static_cast<float>(off + t), c, s);  // as qk_norm_rope_kv_kernel
+  cs[e] = make_float2(c, s);
+}
+
+}  // namespace
+
+int launch_rope_cs(float2* cs, int M, int offset, const int* offset_dev, const RopeTable& tab, hipStream_t stream) {
+  if (M <= 0) return BMX_OK;
+  hipLaunchKernelGGL(rope_cs_kernel, dim3(static_cast<unsigned>((static_cast<int64_t>(M) * 64 + 255) / 256)),
+                     dim3(256), 0, stream, cs, M, offset, offset_dev, tab);
+  return check_launch("rope_cs");
+}
+
 int launch_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t rows, int dim, float eps,
                     hipStream_t stream) {
   if (rows <= 0) return BMX_OK;

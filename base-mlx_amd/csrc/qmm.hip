@@ -104,6 +104,8 @@ struct QmmParams {
   const uint32_t* sb;
   const uint32_t* sb2;
   const uint32_t* seg_sb[3];
+  // QMM_QKV_ROPE: where the normed / rotated rows go
+  QkvRopeOut rope;
 };
 
 // two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
@@ -168,9 +170,10 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   const uint16_t *ps = p.s, *pb = p.b;
   const uint32_t* psb = p.sb;
   uint16_t* py = p.y;
-  if constexpr (EPI == QMM_STORE) {
+  int si = 0;
+  if constexpr (EPI == QMM_STORE || EPI == QMM_QKV_ROPE) {
     if (p.nseg > 1) {
-      const int si = (n0 >= p.seg_n0[1]) + (p.nseg > 2 && n0 >= p.seg_n0[2]);
+      si = (n0 >= p.seg_n0[1]) + (p.nseg > 2 && n0 >= p.seg_n0[2]);
       pw = p.seg_w[si];
       ps = p.seg_s[si];
       pb = p.seg_b[si];
@@ -346,6 +349,62 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   }
 
   // ---- epilogue: lane holds W row 16 j + li, x rows 4 q + r of each tile ----
+  if constexpr (EPI == QMM_QKV_ROPE) {
+    // The tile is one head (128 columns of the q, k or v segment) of 128
+    // tokens.  Its bf16 outputs -- the values the store epilogue writes --
+    // go to LDS, then each wave takes 32 tokens and does for each what
+    // qk_norm_rope_kv_kernel does for that (token, head): QK-norm and RoPE
+    // with the same lane function and the same (cos, sin) (qwen3.rs:392-413),
+    // q into q_out [Hq, M, 128], k and v into the caches at row offset + t
+    // (qwen3.rs:431-489).
+    static_assert(BN == 128, "one head per tile");
+    constexpr int TS = 128 + 8;  // LDS row stride (elements)
+    uint16_t* tl = xs;           // [QBM][TS]: 34 KB over the x and W tiles (48 KB)
+    __syncthreads();             // every wave's last products have read them
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          tl[(wm * 64 + i * 16 + 4 * q + r) * TS + wn * 64 + j * 16 + li] = f2bf(acc[i][j][r]);
+    __syncthreads();
+    const QkvRopeOut& o = p.rope;
+    const int head = n0 / 128;
+    const int offset = o.offset_dev ? *o.offset_dev : o.offset;
+    const uint16_t* nw = si == 0 ? o.q_norm : o.k_norm;
+    const float wa = si < 2 ? bf2f(nw[lane]) : 0.0f, wb = si < 2 ? bf2f(nw[lane + 64]) : 0.0f;
+    // every (cos, sin) of the wave's tokens requested before the first is
+    // used (the stores below may alias the table as far as the compiler
+    // knows, so a load inside the loop would wait behind them)
+    constexpr int TW = QBM / 4;  // tokens per wave
+    float2 csv[TW];
+#pragma unroll
+    for (int tt = 0; tt < TW; tt++) {
+      const int m = min(m0 + wave * TW + tt, M - 1);
+      csv[tt] = si < 2 ? o.cs[static_cast<int64_t>(m) * 64 + lane] : make_float2(0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int tt = 0; tt < TW; tt++) {
+      const int t = wave * TW + tt, m = m0 + t;
+      if (m >= M) break;  // uniform per wave
+      const uint16_t a = tl[t * TS + lane], b = tl[t * TS + lane + 64];
+      if (si == 2) {
+        uint16_t* dst = o.v_cache + (static_cast<int64_t>(head) * o.cap + offset + m) * 128;
+        dst[lane] = a;
+        dst[lane + 64] = b;
+      } else {
+        const float2 cs = csv[tt];
+        uint16_t o1, o2;
+        qk_norm_rope_lane_cs(bf2f(a), bf2f(b), wa, wb, cs.x, cs.y, o.eps, o1, o2);
+        uint16_t* dst = si == 0 ? o.q_out + (static_cast<int64_t>(head) * M + m) * 128
+                                : o.k_cache + (static_cast<int64_t>(head) * o.cap + offset + m) * 128;
+        dst[lane] = o1;
+        dst[lane + 64] = o2;
+      }
+    }
+    return;
+  }
   if constexpr (EPI == QMM_SWIGLU) {
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -719,6 +778,45 @@ int launch_qmm_segments_gm(const uint16_t* x, int nseg, const uint32_t* const* w
                            hipStream_t stream) {
   const uint16_t* none[3] = {nullptr, nullptr, nullptr};
   return qmm_segments_impl(x, nseg, w, none, none, sb, y, n, M, K, ws, ws_floats, stream);
+}
+
+int launch_qmm_qkv_rope_gm(const uint16_t* x, const uint32_t* const* w, const uint32_t* const* sb, const int* n,
+                           int M, int K, const QkvRopeOut& out, hipStream_t stream) {
+  if (M <= 0) return BMX_OK;
+  if (!out.offset_dev && (out.offset < 0 || out.offset + M > out.cap))
+    return set_error(BMX_E_KV_CAPACITY, "KV cache exhausted: requested %d positions, max %d", out.offset + M, out.cap);
+  if (K % 64 || !aligned(x, 16)) return kNoFit;
+  int ntot = 0;
+  for (int i = 0; i < 3; i++) {
+    if (n[i] <= 0 || n[i] % QBN || !aligned(w[i], 16) || !sb[i]) return kNoFit;
+    ntot += n[i];
+  }
+  // the tiling the store form takes: whole 128-column tiles, K not split
+  if (qmm_wide(M, ntot / (2 * QBN))) return kNoFit;
+  int splits = 1, gps = 0;
+  qmm_split(M, ntot, K, &splits, &gps, QBN);
+  if (splits > 1 || (M + QBM - 1) / QBM > 65535) return kNoFit;
+  const int mtiles = (M + QBM - 1) / QBM, ntiles = ntot / QBN;
+  QmmParams p{x, w[0], nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, ntot, K, gps,
+              mtiles, 0};
+  p.nseg = 3;
+  int c = 0;
+  for (int i = 0; i < 3; i++) {
+    p.seg_n0[i] = c;
+    p.seg_w[i] = w[i];
+    p.seg_sb[i] = sb[i];
+    c += n[i];
+  }
+  p.seg_n0[3] = c;
+  p.rope = out;
+  const void* kern = reinterpret_cast<const void*>(qmm_kernel<QMM_QKV_ROPE, QBN, true>);
+  if (int rc = allow_lds_ptr(kern, qmm_lds(QBN))) return rc;
+  void* args[] = {&p};
+  if (int rc = check_hip(hipLaunchKernel(kern, dim3(static_cast<unsigned>(mtiles) * ntiles, 1, 1), dim3(QT), args,
+                                         qmm_lds(QBN), stream),
+                         "qmm launch"))
+    return rc;
+  return check_launch("qmm_qkv_rope");
 }
 
 // The group-major copy of an MLX-layout weight: one thread per (group g,

@@ -83,6 +83,10 @@ constexpr int kAhead = 3;
 constexpr uint32_t kRingEmpty = 0xffffffffu;
 // verify width of speculative decoding (leader + drafts), at most
 constexpr int kMaxSpecK = 8;
+// forwards of more tokens than this norm and rotate q / k in the q|k|v GEMM
+// (more than 64 query rows per kv head: the attention is the flash kernel,
+// which reads the rotated rows, never the fused decode kernel)
+constexpr int kRopeGemmMinM = 64;
 
 struct bmx_kv_cache {
   uint64_t id = 0;  // unique per cache: keys the captured decode graph
@@ -100,6 +104,7 @@ struct bmx_qwen3 {
   uint16_t* final_norm = nullptr;
   std::vector<Layer> layers;
   RopeTable rope{};
+  float2* rope_cs = nullptr;  // (cos, sin) of a long forward's positions (launch_rope_cs)
   std::vector<void*> allocs;
   // workspace (rows = max_tokens)
   uint16_t *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *att = nullptr,
@@ -218,11 +223,19 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
   if (M > 8 && m->gm_stale) {
     if (int rc = repack_prefill_weights(m, st)) return rc;
   }
+  // long forwards norm and rotate q / k in the q|k|v GEMM's epilogue (the
+  // attention then takes the flash kernel, which reads them from q_out and
+  // the caches); the rotation's (cos, sin) once per forward
+  const bool rope_gemm = M > kRopeGemmMinM && hd == 128;
+  if (rope_gemm) {
+    if (int rc = launch_rope_cs(m->rope_cs, M, offset, pos_dev, m->rope, st)) return rc;
+  }
   // x = embed.lookup(tokens)  (qwen3.rs:328-333)
   if (int rc = launch_dequant_gather(ids ? ids : m->ids, M, cf.vocab, m->embed.w, m->embed.s, m->embed.b, m->x, H, st))
     return rc;
   for (int l = 0; l < cf.layers; l++) {
     const Layer& L = m->layers[l];
+    bool roped = false;  // q / k normed and rotated, caches written, by the q|k|v GEMM
     // ---- qkv_block: rms_norm + q/k/v projections (kernels.rs:28-46) ----
     if (M <= 8) {
       QmvParams p{};
@@ -245,7 +258,13 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
       const uint32_t* sb3[3] = {L.p[SLOT_Q].sbt, L.p[SLOT_K].sbt, L.p[SLOT_V].sbt};
       uint16_t* y3[3] = {m->q, m->k, m->v};
       const int n3[3] = {qd, kvd, kvd};
-      int rc = launch_qmm_segments_gm(m->h, 3, wt3, sb3, y3, n3, M, H, m->qmm_ws, m->qmm_ws_floats, st);
+      int rc = kNoFit;
+      if (rope_gemm) {
+        const QkvRopeOut ro{L.q_norm, L.k_norm, m->qr, c->k(l), c->v(l), m->rope_cs, pos_dev, offset, c->cap, cf.eps};
+        rc = launch_qmm_qkv_rope_gm(m->h, wt3, sb3, n3, M, H, ro, st);
+        if (rc == BMX_OK) roped = true;
+      }
+      if (rc == kNoFit) rc = launch_qmm_segments_gm(m->h, 3, wt3, sb3, y3, n3, M, H, m->qmm_ws, m->qmm_ws_floats, st);
       if (rc == kNoFit) {
         const uint32_t* w3[3] = {L.p[SLOT_Q].w, L.p[SLOT_K].w, L.p[SLOT_V].w};
         const uint16_t* s3[3] = {L.p[SLOT_Q].s, L.p[SLOT_K].s, L.p[SLOT_V].s};
@@ -257,15 +276,18 @@ int forward_device(bmx_qwen3* m, bmx_kv_cache* c, int M, int offset, const int* 
     // ---- QK-norm, RoPE at the cache offset, KV write (qwen3.rs:392-489) and
     // SDPA over [0, offset + M) with the causal-offset mask (qwen3.rs:491-518):
     // one fused kernel for decode / short verify, else two steps ----
-    const int fused = launch_qkv_attention(m->q, m->k, m->v, L.q_norm, L.k_norm, c->k(l), c->v(l), m->att,
-                                           m->attn_ws, m->attn_ws_floats, nq, nkv, M, hd, c->cap, offset, pos_dev,
-                                           L_max, cf.eps, m->rope, scale, st);
+    const int fused = roped ? kNoFit
+                            : launch_qkv_attention(m->q, m->k, m->v, L.q_norm, L.k_norm, c->k(l), c->v(l), m->att,
+                                                   m->attn_ws, m->attn_ws_floats, nq, nkv, M, hd, c->cap, offset,
+                                                   pos_dev, L_max, cf.eps, m->rope, scale, st);
     if (fused != kNoFit) {
       if (fused) return fused;
     } else {
-      if (int rc = launch_qk_norm_rope_kv(m->q, m->k, m->v, L.q_norm, L.k_norm, m->qr, c->k(l), c->v(l), M, nq,
-                                          nkv, hd, c->cap, offset, pos_dev, cf.eps, m->rope, st))
-        return rc;
+      if (!roped) {
+        if (int rc = launch_qk_norm_rope_kv(m->q, m->k, m->v, L.q_norm, L.k_norm, m->qr, c->k(l), c->v(l), M, nq,
+                                            nkv, hd, c->cap, offset, pos_dev, cf.eps, m->rope, st))
+          return rc;
+      }
       if (int rc = launch_attention(m->qr, c->k(l), c->v(l), m->att, m->attn_ws, m->attn_ws_floats, nq, nkv, M, hd,
                                     c->cap, offset, pos_dev, L_max, scale, st))
         return rc;
@@ -458,6 +480,7 @@ int qwen3_alloc(const bmx_qwen3_config* cfg, int max_tokens, bmx_qwen3** out) {
   if (!rc) rc = dalloc_t(m, &m->k, T * kvd);
   if (!rc) rc = dalloc_t(m, &m->v, T * kvd);
   if (!rc) rc = dalloc_t(m, &m->qr, T * qd);
+  if (!rc) rc = dalloc_t(m, &m->rope_cs, T * 64);
   if (!rc) rc = dalloc_t(m, &m->att, T * qd);
   if (!rc) rc = dalloc_t(m, &m->o, T * H);
   if (!rc) rc = dalloc_t(m, &m->g, T * I);

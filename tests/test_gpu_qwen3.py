@@ -251,19 +251,26 @@ def test_long_context_decode_and_verify(gpu, orc):
 
 def test_prefill_unsplit_fused_epilogues(gpu, orc):
     """A 2048-token prefill through one Qwen3-4B-shaped layer: at this size
-    the o and down GEMMs run unsplit with the residual add in their epilogue
-    and gate|up runs as one GEMM with the SwiGLU epilogue (the smaller
-    prefills above split K and add the residual in the reduction); logits of
-    every position against the oracle."""
+    the o and down GEMMs run unsplit with the residual add in their epilogue,
+    gate|up runs as one GEMM with the SwiGLU epilogue (the smaller prefills
+    above split K and add the residual in the reduction), and the q|k|v GEMM
+    norms and rotates q and k and writes the cache rows in its epilogue;
+    logits of every position and the cache rows against the oracle."""
     shape = dict(hidden=2560, inter=9728, layers=1, n_heads=32, n_kv_heads=8, head_dim=128, vocab=1024)
     gm = gpu.Qwen3(gpu.qwen3_config(**shape), 5, 0.02, max_tokens=2048)
     om = orc.Qwen3(orc.make_config(**shape), 5, 0.02)
     toks = orc.fill_tokens(21, 2048, shape["vocab"])
-    gc, oc = gm.new_cache(2048), om.new_cache(2048)
+    gc, oc = gm.new_cache(2100), om.new_cache(2100)
     g = gm.forward(gc, toks, all_logits=True)
     print("oracle forward (2048 tokens)", flush=True)
     o = om.forward(oc, toks, all_logits=True)
     assert _check_logits(g, o) >= 0.9
+    for kv in (0, 1):
+        ref = oc.data()[0, kv][:, :2048]
+        got = gc.layer_numpy(0, kv)[:, :2048]
+        assert l2_rel_err(bf16_to_f32(got), bf16_to_f32(ref)) < 2e-2, kv
+        # rows past the prefill are not written
+        assert not gc.layer_numpy(0, kv)[:, 2048:].any(), kv
 
 
 def _write_projection(gpu, gm, layer, slot, arrays):
