@@ -51,7 +51,7 @@ constexpr int QBM = 128, QBN = 128, QT = 256;  // tile rows of x, of W; threads
 constexpr int RS = 64;  // LDS row stride (elements)
 // LDS of a workgroup with a BN-row W tile: two x tiles and the W tile
 // (48, 52 or 64 KB for BN 128, 160, 256)
-constexpr size_t qmm_lds(int bn) { return (2ull * QBM * RS + 1ull * bn * RS) * 2; }
+constexpr size_t qmm_lds(int bn, int qm = QBM) { return (2ull * qm * RS + 1ull * bn * RS) * 2; }
 // 256-row W tiles where the grid of them still spans two or more rounds of
 // the 512 resident workgroups they allow (2 per CU): at M = 4096 on
 // 12288 x 4096 / 9728 x 2560 / 19456 x 2560, 10-17% faster than 128-row
@@ -116,15 +116,17 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 // BN: W rows per tile, 128 (waves of 64 x 64) or 256 (waves of 64 x 128:
 // the x tile serves twice the W rows, for large grids).  GM: weights in the
 // group-major layout (QmmParams), else MLX's row-major one.
-template <int EPI, int BN, bool GM>
-__global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
+template <int EPI, int BN, bool GM, int QM = QBM>
+__global__ void __launch_bounds__(2 * QM, QM == QBM ? 2 : 1) qmm_kernel(const QmmParams p) {
   static_assert(BN == 128 || BN == 160 || BN == 256, "W tile rows");
+  static_assert(QM == QBM || (QM == 2 * QBM && EPI != QMM_QKV_ROPE), "x tile rows");
+  constexpr int NWV = QM / 32;  // waves: 2 per 64 x rows
   static_assert(EPI != QMM_SWIGLU || BN % 64 == 0, "SwiGLU pairs gate and up rows per wave");
   constexpr int NJ = BN / 32;                // 16-row W tiles per wave
-  constexpr int WR = (BN + 127) / 128;       // W rows staged per thread (the second only below BN)
+  constexpr int WR = (BN + QM - 1) / QM;     // W rows staged per thread (the second only below BN)
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [2][QBM][RS], swizzled
-  uint16_t* ws = xs + 2 * QBM * RS;                  // [BN][RS], swizzled
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [2][QM][RS], swizzled
+  uint16_t* ws = xs + 2 * QM * RS;                   // [BN][RS], swizzled
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;  // wave sub-tile: x rows 64 wm, W rows BN/2 wn
   const int li = lane & 15, q = lane >> 4;
@@ -162,7 +164,7 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
       nt = blockIdx.x % ntiles;
     }
   }
-  const int m0 = mt * QBM;
+  const int m0 = mt * QM;
   int n0 = nt * CN;
   const int gb = blockIdx.z * p.gps, ge = min(G, gb + p.gps);
   // the segment holding this workgroup's columns (uniform)
@@ -188,21 +190,23 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   // results are never stored) ----
   // x straight into LDS (global_load_lds_dwordx4: lane l's 16 bytes land
   // at the instruction's LDS base + 16 l): wave w's instruction i fills
-  // tile rows 8 (4 i + w) .. + 7, lane l row l / 8 and physical chunk l % 8,
-  // so it loads logical chunk (l % 8) ^ (row & 7), the swz layout
+  // tile rows 8 (NWV i + w) .. + 7, lane l row l / 8 and physical chunk
+  // l % 8, so it loads logical chunk (l % 8) ^ (row & 7), the swz layout
   const uint16_t* xd[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const int row = 8 * (4 * i + wave) + (lane >> 3), lc = (lane & 7) ^ (row & 7);
+    const int row = 8 * (NWV * i + wave) + (lane >> 3), lc = (lane & 7) ^ (row & 7);
     xd[i] = p.x + static_cast<int64_t>(min(m0 + row, M - 1)) * K + lc * 8;
   }
   auto issue_x = [&](int g, uint16_t* xb) {
 #pragma unroll
     for (int i = 0; i < 4; i++)
-      __builtin_amdgcn_global_load_lds(xd[i] + g * 64, xb + 512 * (4 * i + wave), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(xd[i] + g * 64, xb + 512 * (NWV * i + wave), 16, 0, 0);
   };
-  // W rows wr (and wr + 128 with BN 256) of the tile, half wh of the group
+  // W rows wr (and wr + QM with BN above QM) of the tile, half wh of the
+  // group; with 512 threads the rows past BN stage nothing
   const int wr = tid >> 1, wh = tid & 1;
+  const bool row0 = QM < BN || wr < BN;  // (uniform per wave: BN is a multiple of 32)
   // SwiGLU: each wave's BN / 2 W rows are BN / 4 gate rows and the up rows
   // of the same output columns, so a lane holds both products of its
   // outputs (gate in tiles j < NJ / 2, up in j + NJ / 2)
@@ -224,10 +228,10 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   const uint32_t *wp0, *wp1 = nullptr;
   const uint16_t *sp0 = nullptr, *bp0 = nullptr, *sp1 = nullptr, *bp1 = nullptr;
   const uint32_t *sbp0 = nullptr, *sbp1 = nullptr;
-  wsrc(wr, wp0, sp0, bp0, sbp0);
+  wsrc(min(wr, BN - 1), wp0, sp0, bp0, sbp0);
   // (BN 160: the second row exists for wr < 32, i.e. wave 0; uniform per wave)
-  const bool row1 = WR == 2 && wr + 128 < BN;
-  if (row1) wsrc(wr + 128, wp1, sp1, bp1, sbp1);
+  const bool row1 = WR == 2 && wr + QM < BN;
+  if (row1) wsrc(wr + QM, wp1, sp1, bp1, sbp1);
   // One group's W operands in registers: one or two 16-byte row halves and
   // their scales and biases -- one word s | b << 16 per row in the
   // group-major layout, two 16-bit loads in MLX's.  Raw loaded words only:
@@ -241,6 +245,7 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
   };
   auto load = [&](int g) {
     QStage r;
+    if (!row0) return r;
     if constexpr (GM) {
       const int64_t go = static_cast<int64_t>(g) * N;
       r.w0 = *reinterpret_cast<const uint4*>(wp0 + go * 8);
@@ -286,12 +291,13 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
       put_word(wh * 4 + 2, wq.z);
       put_word(wh * 4 + 3, wq.w);
     };
+    if (!row0) return;
     if constexpr (GM) {
       put_row(wr, r.w0, __uint_as_float(r.sb0 << 16), __uint_as_float(r.sb0 & 0xffff0000u));
-      if (row1) put_row(wr + 128, r.w1, __uint_as_float(r.sb1 << 16), __uint_as_float(r.sb1 & 0xffff0000u));
+      if (row1) put_row(wr + QM, r.w1, __uint_as_float(r.sb1 << 16), __uint_as_float(r.sb1 & 0xffff0000u));
     } else {
       put_row(wr, r.w0, bf2f(r.s0), bf2f(r.b0));
-      if (row1) put_row(wr + 128, r.w1, bf2f(r.s1), bf2f(r.b1));
+      if (row1) put_row(wr + QM, r.w1, bf2f(r.s1), bf2f(r.b1));
     }
   };
 
@@ -337,10 +343,10 @@ __global__ void __launch_bounds__(QT, 2) qmm_kernel(const QmmParams p) {
     const int cur = (g - gb) & 1;
     const bool more = g + 1 < ge;
     if (more) {
-      issue_x(g + 1, xs + (cur ^ 1) * QBM * RS);
+      issue_x(g + 1, xs + (cur ^ 1) * QM * RS);
       sa = load(g + 1);
     }
-    compute(xs + cur * QBM * RS);
+    compute(xs + cur * QM * RS);
     if (!more) break;
     __syncthreads();  // every read of this group's W tile (and x tile) is done
     store(sa);
@@ -622,10 +628,10 @@ size_t qmm_workspace_floats(int max_M, int N, int K) {
 
 namespace {
 
-template <int EPI, int BN>
+template <int EPI, int BN, int QM = QBM>
 const void* qmm_kernel_for(bool gm) {
-  return gm ? reinterpret_cast<const void*>(qmm_kernel<EPI, BN, true>)
-            : reinterpret_cast<const void*>(qmm_kernel<EPI, BN, false>);
+  return gm ? reinterpret_cast<const void*>(qmm_kernel<EPI, BN, true, QM>)
+            : reinterpret_cast<const void*>(qmm_kernel<EPI, BN, false, QM>);
 }
 
 // The GEMM with an epilogue over MLX-layout (sb == nullptr) or group-major
@@ -651,7 +657,9 @@ int qmm_epi_impl(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const ui
   if (bn == 128) qmm_split(M, N, K, &splits, &gps, cols);
   // SwiGLU needs both products of an output in one workgroup: no K split
   if (epi == QMM_SWIGLU && splits > 1) return kNoFit;
-  const int mtiles = (M + QBM - 1) / QBM, ntiles = (N + cols - 1) / cols;
+  // 256-row x tiles on 8 waves for 160-column tiles and SwiGLU
+  const int qm = (bn == 160 || (bn == 256 && epi == QMM_SWIGLU)) && M >= 2048 ? 2 * QBM : QBM;
+  const int mtiles = (M + qm - 1) / qm, ntiles = (N + cols - 1) / cols;
   // Tile order.  Vocabulary-sized N: grouped by XCD in column-major order
   // (151936 x 4096 at M = 2048 runs 1.5x faster; the model's projections
   // ran 4-9% slower so).  The residual GEMMs (o, down: K 4096 / 9728, so a
@@ -669,14 +677,19 @@ int qmm_epi_impl(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const ui
   }
   const dim3 grid(static_cast<unsigned>(mtiles) * ntiles, 1, splits);
   auto launch = [&](const void* kern, int bn) {
-    if (int rc = allow_lds_ptr(kern, qmm_lds(bn))) return rc;
+    if (int rc = allow_lds_ptr(kern, qmm_lds(bn, qm))) return rc;
     void* args[] = {&p};
-    if (int rc = check_hip(hipLaunchKernel(kern, grid, dim3(QT), args, qmm_lds(bn), stream), "qmm launch")) return rc;
+    if (int rc = check_hip(hipLaunchKernel(kern, grid, dim3(2 * qm), args, qmm_lds(bn, qm), stream), "qmm launch"))
+      return rc;
     return check_launch("qmm");
   };
-  const int rc = bn == 256   ? (epi == QMM_SWIGLU    ? launch(qmm_kernel_for<QMM_SWIGLU, 256>(gm), 256)
+  const int rc = bn == 256   ? (epi == QMM_SWIGLU    ? (qm > QBM ? launch(qmm_kernel_for<QMM_SWIGLU, 256, 2 * QBM>(gm), 256)
+                                                                 : launch(qmm_kernel_for<QMM_SWIGLU, 256>(gm), 256))
                                 : epi == QMM_RESIDUAL ? launch(qmm_kernel_for<QMM_RESIDUAL, 256>(gm), 256)
                                                       : launch(qmm_kernel_for<QMM_STORE, 256>(gm), 256))
+                 : bn == 160 && qm > QBM
+                     ? (epi == QMM_RESIDUAL ? launch(qmm_kernel_for<QMM_RESIDUAL, 160, 2 * QBM>(gm), 160)
+                                            : launch(qmm_kernel_for<QMM_STORE, 160, 2 * QBM>(gm), 160))
                  : bn == 160 ? (epi == QMM_RESIDUAL ? launch(qmm_kernel_for<QMM_RESIDUAL, 160>(gm), 160)
                                                     : launch(qmm_kernel_for<QMM_STORE, 160>(gm), 160))
                              : (epi == QMM_SWIGLU    ? launch(qmm_kernel_for<QMM_SWIGLU, 128>(gm), 128)
