@@ -1025,6 +1025,309 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
   }
 }
 
+// Prefill / long verify with 32 queries per wave (v_mfma_f32_32x32x16):
+// the same staging, LDS tiles, online softmax and V-range guard as
+// attn_prefill_kernel<8, HG>, arranged so that each query's softmax state
+// stays in one lane.  A workgroup of 8 waves owns HG q heads of one kv head
+// and 256 / HG consecutive tokens, 32 per wave.  Per 64-key block:
+//   S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = 32 keys of the K tile, B =
+//     the wave's q rows, 16 dims a step): lane l holds query l % 32 and
+//     keys 32 kt + 8 (r / 4) + 4 (l / 32) + r % 4 of the two key tiles kt;
+//     row max and sum run over the lane's 32 scores and the other half of
+//     the wave (one lane swap);
+//   O^T += V^T P^T on v_mfma_f32_32x32x16_f16 (A = 32 dims of V^T from LDS,
+//     two 4-key chunks per lane; B = the probabilities as they lie in the
+//     score registers: keys 16 s + 4 (l / 32) + 0..3 and + 8 of step s are
+//     eight consecutive score registers), so O^T puts query l % 32 in lane
+//     l as well, and its rescale by exp(m_old - m_new) needs no shuffle.
+// Half the LDS operand reads per product of the 16-query layout, and the
+// cross-lane reductions of a block halve.
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+// Its LDS rows (strides chosen with a bank-conflict probe of each access:
+// 16-byte operand reads of 32 consecutive rows are conflict-free at 272
+// bytes for K and at 192 bytes with the (d >> 3) & 7 pair swizzle for V^T)
+constexpr int kF32KS = kD + 8;   // K tile row stride (elements)
+constexpr int kF32VS = kFaK + 32;  // V^T tile row stride (elements)
+constexpr size_t kF32Lds = 2ull * (kFaK * kF32KS + 2 * kD * kF32VS) * sizeof(uint16_t);
+
+template <int HG>
+__global__ void __launch_bounds__(512) attn_flash32_kernel(const AttnParams p) {
+  constexpr int NW = 8;
+  constexpr int TQ = 32 * NW / HG;  // tokens per workgroup
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ unsigned vsat[kFaSatWords];
+  uint16_t* kt_s = reinterpret_cast<uint16_t*>(smem);  // [2][kFaK][kF32KS]
+  uint16_t* vt_s = kt_s + 2 * kFaK * kF32KS;            // [2][kD][kF32VS]
+  uint16_t* vh_s = vt_s + 2 * kD * kF32VS;              // [2][kD][kF32VS] fp16
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 31, hf = lane >> 5;  // query column, lane half
+  const int rep_h = p.Hq / p.Hkv;
+  const int kvh = static_cast<int>(blockIdx.y) / (rep_h / HG);
+  const int h = kvh * rep_h + (static_cast<int>(blockIdx.y) % (rep_h / HG)) * HG + wave % HG;
+  const int t0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * TQ;  // longest rows first
+  const int offset = p.offset_dev ? *p.offset_dev : p.offset;
+  const int L = offset + p.M;
+  const int kend = p.causal ? min(L, offset + min(t0 + TQ, p.M)) : L;
+  const int nkb = (kend + kFaK - 1) / kFaK;
+  const int tw = t0 + 32 * (wave / HG);  // the wave's first query
+  const int t = tw + j;                  // this lane's query
+  const int64_t hbase = static_cast<int64_t>(kvh) * p.cap * kD;
+
+  // q of the lane's query: dims 16 ks + 8 hf .. + 7 (B of S^T = K Q^T)
+  uint4 qf[8];
+  {
+    const uint16_t* qrow = p.q + (static_cast<int64_t>(h) * p.M + min(t, p.M - 1)) * kD + 8 * hf;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) qf[ks] = *reinterpret_cast<const uint4*>(qrow + 16 * ks);
+  }
+  // staging of one key block by the 512 threads: K rows (2 x 16 bytes) and V
+  // (4 keys x 4 dims, transposed in registers), as attn_prefill_kernel<8, .>
+  struct Stage {
+    uint4 kr0, kr1, kr2, kr3;
+  };
+  // V piece of a thread: dims 4 vd4 .. + 3, keys 4 vk4 .. + 3.  Lanes 0-15
+  // and 32-47 of a wave read one 256-byte key row, lanes 16-31 and 48-63 the
+  // row 8 keys on, and the V^T stores below fall in distinct LDS banks.
+  const int tid9 = static_cast<int>(threadIdx.x);
+  const int vd4 = (tid9 & 15) | (((tid9 >> 5) & 1) << 4);
+  const int vk4 = (((tid9 >> 4) & 1) << 1) | ((tid9 >> 6) & 1) | ((tid9 >> 7) << 2);
+  auto kaddr = [&](int k0, int i) {
+    const int e = static_cast<int>(threadIdx.x) + 512 * i, key = e >> 4, ch = e & 15;
+    return reinterpret_cast<const uint4*>(p.k + hbase + static_cast<int64_t>(min(k0 + key, L - 1)) * kD + ch * 8);
+  };
+  auto vaddr4 = [&](int k0, int jj) {
+    return reinterpret_cast<const uint2*>(p.v + hbase + static_cast<int64_t>(min(k0 + 4 * vk4 + jj, L - 1)) * kD +
+                                          vd4 * 4);
+  };
+  auto load_block = [&](int k0) {
+    Stage r;
+    r.kr0 = *kaddr(k0, 0);
+    r.kr1 = *kaddr(k0, 1);
+    const uint2 v0 = *vaddr4(k0, 0), v1 = *vaddr4(k0, 1), v2 = *vaddr4(k0, 2), v3 = *vaddr4(k0, 3);
+    r.kr2 = make_uint4(v0.x, v0.y, v1.x, v1.y);
+    r.kr3 = make_uint4(v2.x, v2.y, v3.x, v3.y);
+    return r;
+  };
+  auto store_block = [&](const Stage r, int buf, int blk) {
+    uint16_t* kb = kt_s + buf * kFaK * kF32KS;
+    auto kput = [&](int i, const uint4& v) {
+      const int e = static_cast<int>(threadIdx.x) + 512 * i, key = e >> 4, ch = e & 15;
+      *reinterpret_cast<uint4*>(kb + key * kF32KS + ch * 8) = v;
+    };
+    // V^T: a dim row holds its 64 keys as 8 pairs of 4-key chunks, pair P =
+    // 2 g + (c & 1) holding chunks c and c + 2 of 16-key group g (keys
+    // 16 g + 4 c.. ), so the 8 keys a lane feeds one P V product are 16
+    // contiguous bytes; pair P of dim row d sits at P ^ ((d >> 3) & 7).
+    // fp16 copy by v_cvt_pkrtz (exact in fp16's normal range); a bf16
+    // magnitude of 2^16 or more marks the block for the two-term product
+    auto h2 = [](uint32_t lo16, uint32_t hi16) {
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(lo16 << 16),
+                                                                     __uint_as_float(hi16 << 16)));
+    };
+    kput(0, r.kr0);
+    kput(1, r.kr1);
+    const uint32_t w[4][2] = {{r.kr2.x, r.kr2.y}, {r.kr2.z, r.kr2.w}, {r.kr3.x, r.kr3.y}, {r.kr3.z, r.kr3.w}};
+    u16x2_t mx = u16x2_t{0, 0};
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int e = 0; e < 2; e++) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, w[k][e] & 0x7fff7fffu));
+    const uint32_t sat = (__builtin_bit_cast(uint32_t, mx) + 0x38803880u) & 0x80008000u;
+    if (sat != 0 && blk < 32 * kFaSatWords) atomicOr(&vsat[blk >> 5], 1u << (blk & 31));
+    const int cs = 8 * ((2 * (vk4 >> 2) + (vk4 & 1)) ^ ((vd4 >> 1) & 7)) + 4 * ((vk4 >> 1) & 1);
+    uint16_t* vb = vt_s + buf * kD * kF32VS + cs;
+    uint16_t* vh = vh_s + buf * kD * kF32VS + cs;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const uint32_t a = w[0][e], b = w[1][e], c = w[2][e], d = w[3][e];
+      const int r0 = (4 * vd4 + 2 * e) * kF32VS, r1 = r0 + kF32VS;
+      *reinterpret_cast<uint2*>(vb + r0) =
+          make_uint2(__builtin_amdgcn_perm(b, a, 0x05040100u), __builtin_amdgcn_perm(d, c, 0x05040100u));
+      *reinterpret_cast<uint2*>(vb + r1) =
+          make_uint2(__builtin_amdgcn_perm(b, a, 0x07060302u), __builtin_amdgcn_perm(d, c, 0x07060302u));
+      *reinterpret_cast<uint2*>(vh + r0) = make_uint2(h2(a & 0xffffu, b & 0xffffu), h2(c & 0xffffu, d & 0xffffu));
+      *reinterpret_cast<uint2*>(vh + r1) = make_uint2(h2(a >> 16, b >> 16), h2(c >> 16, d >> 16));
+    }
+  };
+
+  f32x16_t o[4];  // O^T: dims 32 dt + 8 (r / 4) + 4 hf + r % 4 of query t
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+  const int lim = p.causal ? min(L, offset + t + 1) : L;       // keys < lim are visible to query t
+  const int lim_w = p.causal ? min(L, offset + tw + 1) : L;    // ... to every query of the wave
+  const int lim_hi = p.causal ? min(L, offset + tw + 32) : L;  // ... to some query of the wave
+  const float scale2 = p.scale * 1.44269504088896340736f;      // scale * log2(e)
+  // V^T reads: dim row d = 32 dt + j, pair P = 2 s + hf (keys 16 s + 4 hf
+  // .. and 16 s + 8 + 4 hf ..), at pair P ^ ((d >> 3) & 7).  The swizzle's
+  // bits are (j >> 3) & 1, (j >> 4) & 1 and dt & 1, so the position is a
+  // lane part for each parity of s plus constants:
+  //   P ^ sw = (hf ^ sw0) + 2 ((s & 1) ^ sw1) + 4 ((s >> 1) ^ (dt & 1))
+  const int sw0 = (j >> 3) & 1, sw1 = (j >> 4) & 1;
+  const int vle = j * kF32VS + 8 * ((hf ^ sw0) + 2 * sw1);        // s even
+  const int vlo = j * kF32VS + 8 * ((hf ^ sw0) + 2 * (1 - sw1));  // s odd
+  auto vaddr = [&](int dt, int s) {
+    return ((s & 1) ? vlo : vle) + 32 * dt * kF32VS + 32 * ((s >> 1) ^ (dt & 1));
+  };
+
+  // two register sets: block jb + 2 is requested while block jb's products
+  // run and block jb + 1 moves from registers into LDS
+  Stage sg0 = load_block(0);
+  Stage sg1 = load_block(min(1, nkb - 1) * kFaK);
+  for (int i = threadIdx.x; i < kFaSatWords; i += 512) vsat[i] = 0u;
+  __syncthreads();
+  store_block(sg0, 0, 0);
+  __syncthreads();
+  auto iter = [&](const int jb, auto par_c) {
+    constexpr int P = decltype(par_c)::value;
+    const int buf = jb & 1, k0 = jb * kFaK;
+    const bool more = jb + 1 < nkb;
+    if constexpr (P == 0) sg0 = load_block(min(jb + 2, nkb - 1) * kFaK);
+    else sg1 = load_block(min(jb + 2, nkb - 1) * kFaK);
+    if (k0 < lim_hi) {  // uniform per wave: some query of the wave sees a key of this block
+      const uint16_t* kb = kt_s + buf * kFaK * kF32KS;
+      const uint16_t* vb = vt_s + buf * kD * kF32VS;
+      const uint16_t* vhb = vh_s + buf * kD * kF32VS;
+      // ---- S^T = K Q^T: 2 key tiles of 32, 8 dim steps of 16 ----
+      f32x16_t sc[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) sc[kt][r] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+          // (K reads hoisted one dim step at most: registers)
+          if (kt == 0) __builtin_amdgcn_sched_barrier(0);
+          const uint4 a = *reinterpret_cast<const uint4*>(kb + (kt * 32 + j) * kF32KS + 16 * ks + 8 * hf);
+          sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                           __builtin_bit_cast(bf16x8_t, qf[ks]), sc[kt], 0, 0, 0);
+        }
+      // ---- online softmax of query t over the block, base 2 (as the
+      // 16-query kernel: p = 2^(s c - m), masked keys -inf by a select) ----
+      if (k0 + kFaK > lim_w) {  // uniform: the block reaches past some query's last key
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const int key = k0 + 32 * kt + 8 * (r >> 2) + 4 * hf + (r & 3);
+            sc[kt][r] = key < lim ? sc[kt][r] : -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) mx = fmaxf(mx, sc[kt][r]);
+      mx = max_xor32(mx) * scale2;
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      const bool two = jb >= 32 * kFaSatWords || ((vsat[jb >> 5] >> (jb & 31)) & 1u) != 0u;
+      float sum = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(sc[kt][r], scale2, -m_use));
+          sum += e;
+          sc[kt][r] = e;
+        }
+      sum = add_xor32(sum);
+      l_run = l_run * alpha + sum;
+      m_run = m_new;
+      // ---- rescale O^T where a running max moved (each lane its own query) ----
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) o[dt][r] *= alpha;
+      }
+      // ---- O^T += V^T P^T: key step s = registers 8 (s & 1) .. + 7 of tile
+      // s / 2.  p in fp16 against V in fp16; a block holding a V value beyond
+      // fp16's range takes p = hi + lo instead, hi = bf16(p) against V in bf16
+      // and lo = p - hi (exact in fp32) in fp16 against V in fp16 (saturated
+      // there) ----
+      f16x8_t ph[4];
+      bf16x8_t pa[4];
+      if (two) {  // uniform; bf16(p) and the fp16 residual only where needed
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+          uint32_t hw[4], lw[4];
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            const float r0 = sc[s >> 1][8 * (s & 1) + 2 * u], r1 = sc[s >> 1][8 * (s & 1) + 2 * u + 1];
+            const uint16_t b0 = f2bf(r0), b1 = f2bf(r1);
+            hw[u] = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
+            lw[u] = __builtin_bit_cast(
+                uint32_t, f16x2_t{static_cast<_Float16>(r0 - bf2f(b0)), static_cast<_Float16>(r1 - bf2f(b1))});
+          }
+          pa[s] = __builtin_bit_cast(bf16x8_t, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+          ph[s] = __builtin_bit_cast(f16x8_t, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+          uint32_t pl[4];
+#pragma unroll
+          for (int u = 0; u < 4; u++)
+            pl[u] = __builtin_bit_cast(uint32_t, f16x2_t{static_cast<_Float16>(sc[s >> 1][8 * (s & 1) + 2 * u]),
+                                                         static_cast<_Float16>(sc[s >> 1][8 * (s & 1) + 2 * u + 1])});
+          ph[s] = __builtin_bit_cast(f16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
+          pa[s] = bf16x8_t{};
+        }
+      }
+      // the fp16 product always; a block with V beyond fp16's range adds its
+      // bf16 term in a second pass
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++) {
+        __builtin_amdgcn_sched_barrier(0);  // (V reads of one dim tile at a time)
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+          const uint4 hv = *reinterpret_cast<const uint4*>(vhb + vaddr(dt, s));
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, hv), ph[s], o[dt], 0, 0, 0);
+        }
+      }
+      if (two) {
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int s = 0; s < 4; s++) {
+            const uint4 vv = *reinterpret_cast<const uint4*>(vb + vaddr(dt, s));
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), pa[s], o[dt], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (more) store_block(P == 0 ? sg1 : sg0, buf ^ 1, jb + 1);
+    __syncthreads();
+  };
+  for (int jb = 0; jb < nkb; jb += 2) {
+    iter(jb, std::integral_constant<int, 0>{});
+    if (jb + 1 < nkb) iter(jb + 1, std::integral_constant<int, 1>{});
+  }
+  // ---- normalise and write: dims 32 dt + 8 r4 + 4 hf .. + 3 of query t ----
+  if (t < p.M) {
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    uint16_t* orow = p.out + static_cast<int64_t>(t) * p.Hq * kD + h * kD + 4 * hf;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; r4++) {
+        const f32x16_t& a = o[dt];
+        const uint32_t w0 = static_cast<uint32_t>(f2bf(a[4 * r4] * inv)) |
+                            (static_cast<uint32_t>(f2bf(a[4 * r4 + 1] * inv)) << 16);
+        const uint32_t w1 = static_cast<uint32_t>(f2bf(a[4 * r4 + 2] * inv)) |
+                            (static_cast<uint32_t>(f2bf(a[4 * r4 + 3] * inv)) << 16);
+        *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * r4) = make_uint2(w0, w1);
+      }
+  }
+}
+
 }  // namespace
 
 // Workspace floats of one call: the arrival counters, then the split
@@ -1178,10 +1481,16 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
     hipLaunchKernelGGL(kern, dim3((M + tq - 1) / tq, Hkv * (rep / hg)), dim3(64 * nw), kFaLds, stream, p);
     return check_launch("attention_prefill");
   };
-  if (rep % 8 == 0) return launch(attn_prefill_kernel<8, 8>, 8, 8);
-  if (rep == 4) return launch(attn_prefill_kernel<8, 4>, 8, 4);
-  if (rep == 2) return launch(attn_prefill_kernel<8, 2>, 8, 2);
-  if (rep == 1) return launch(attn_prefill_kernel<8, 1>, 8, 1);
+  auto launch32 = [&](auto kern, int hg) {
+    if (int e = allow_lds_ptr(reinterpret_cast<const void*>(kern), kF32Lds)) return e;
+    const int tq = 256 / hg;
+    hipLaunchKernelGGL(kern, dim3((M + tq - 1) / tq, Hkv * (rep / hg)), dim3(512), kF32Lds, stream, p);
+    return check_launch("attention_prefill");
+  };
+  if (rep % 8 == 0) return launch32(attn_flash32_kernel<8>, 8);
+  if (rep == 4) return launch32(attn_flash32_kernel<4>, 4);
+  if (rep == 2) return launch32(attn_flash32_kernel<2>, 2);
+  if (rep == 1) return launch32(attn_flash32_kernel<1>, 1);
   return launch(attn_prefill_kernel<4, 1>, 4, 1);
 }
 
