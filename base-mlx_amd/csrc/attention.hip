@@ -9,15 +9,17 @@
 // (qwen3.rs:629-653) lets query t attend keys j <= offset + t, which is
 // applied here as a predicate (masked keys contribute exactly 0).
 //
-// Two kernels, chosen by the number of query rows per kv head
-// (R = new tokens x q heads per kv head):
+// Kernels chosen by the number of query rows per kv head (R = new tokens x
+// q heads per kv head):
 //   R <= 64 (decode, speculative verify): attn_decode_kernel splits the key
 //     range over workgroups of 256 keys (flash-decoding), and the last
 //     workgroup of each kv head to finish merges the unnormalised partials
 //     (o, m, l);
-//   otherwise (prefill): attn_prefill_kernel, flash attention with one
-//     workgroup per (query head, 64 query tokens) walking all visible keys.
-// Both run Q K^T and (prefill) P V on the matrix cores.
+//   otherwise (prefill): flash attention walking all visible keys,
+//     attn_flash32_kernel (32 queries per wave, a GQA group per workgroup)
+//     where the q heads per kv head are a power of two, else
+//     attn_prefill_kernel (16 queries per wave).
+// All run Q K^T and (prefill) P V on the matrix cores.
 #include <math.h>
 
 #include <algorithm>
