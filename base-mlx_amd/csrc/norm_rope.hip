@@ -38,6 +38,48 @@ __global__ void __launch_bounds__(256)
   const int lane = threadIdx.x & 63;
   if (r >= rows) return;
   const uint16_t* xr = x + r * dim;
+  if (dim <= 4096) {
+    // the row (at most 8 chunks of 8 per lane) and the weight in registers:
+    // x read once, every load in flight together; the same operations in
+    // the same order as the loops below
+    uint4 d[8], wn[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const int k = lane * 8 + 512 * c;
+      if (k < dim) {
+        d[c] = *reinterpret_cast<const uint4*>(xr + k);
+        wn[c] = *reinterpret_cast<const uint4*>(w + k);
+      }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      if (lane * 8 + 512 * c >= dim) break;
+      const uint32_t v[4] = {d[c].x, d[c].y, d[c].z, d[c].w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float lo = bf2f(v[i] & 0xffffu), hi = bf2f(v[i] >> 16);
+        ss += lo * lo + hi * hi;
+      }
+    }
+    ss = wave_sum_xor(ss, 64);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const int k = lane * 8 + 512 * c;
+      if (k >= dim) break;
+      const uint32_t v[4] = {d[c].x, d[c].y, d[c].z, d[c].w}, wv[4] = {wn[c].x, wn[c].y, wn[c].z, wn[c].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float lo = bf2f(wv[i] & 0xffffu) * round_bf(bf2f(v[i] & 0xffffu) * inv);
+        const float hi = bf2f(wv[i] >> 16) * round_bf(bf2f(v[i] >> 16) * inv);
+        o[i] = static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+      }
+      *reinterpret_cast<uint4*>(y + r * dim + k) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    return;
+  }
   float ss = 0.0f;
   for (int k = lane * 8; k < dim; k += 512) {
     const uint4 d = *reinterpret_cast<const uint4*>(xr + k);
