@@ -50,8 +50,12 @@ constexpr int QBM = 128, QBN = 128, QT = 256;  // tile rows of x, of W; threads
 // in conflicts.
 constexpr int RS = 64;  // LDS row stride (elements)
 // LDS of a workgroup with a BN-row W tile: two x tiles and the W tile
-// (48, 52 or 64 KB for BN 128, 160, 256)
-constexpr size_t qmm_lds(int bn, int qm = QBM) { return (2ull * qm * RS + 1ull * bn * RS) * 2; }
+// (48, 52 or 64 KB for BN 128, 160, 256); with 256-row x tiles (one
+// workgroup per CU) two W tiles (104 KB for BN 160, 128 KB for BN 256)
+constexpr int qmm_wbufs(int qm) { return qm == QBM ? 1 : 2; }
+constexpr size_t qmm_lds(int bn, int qm = QBM) {
+  return (2ull * qm * RS + 1ull * qmm_wbufs(qm) * bn * RS) * 2;
+}
 // 256-row W tiles where the grid of them still spans two or more rounds of
 // the 512 resident workgroups they allow (2 per CU): at M = 4096 on
 // 12288 x 4096 / 9728 x 2560 / 19456 x 2560, 10-17% faster than 128-row
@@ -126,7 +130,8 @@ __global__ void __launch_bounds__(2 * QM, QM == QBM ? 2 : 1) qmm_kernel(const Qm
   constexpr int WR = (BN + QM - 1) / QM;     // W rows staged per thread (the second only below BN)
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);  // [2][QM][RS], swizzled
-  uint16_t* ws = xs + 2 * QM * RS;                   // [BN][RS], swizzled
+  uint16_t* ws = xs + 2 * QM * RS;                   // [NWB][BN][RS], swizzled
+  constexpr int NWB = qmm_wbufs(QM);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;  // wave sub-tile: x rows 64 wm, W rows BN/2 wn
   const int li = lane & 15, q = lane >> 4;
@@ -267,7 +272,7 @@ __global__ void __launch_bounds__(2 * QM, QM == QBM ? 2 : 1) qmm_kernel(const Qm
     return r;
   };
   // ---- registers -> LDS: W dequantized to bf16 ----
-  auto store = [&](const QStage r) {
+  auto store = [&](const QStage r, uint16_t* wt) {
     // sv, bv: the row's scale and bias as floats
     auto put_row = [&](int row, const uint4 wq, float sv, float bv) {
       auto put_word = [&](int chunk, uint32_t word) {
@@ -284,7 +289,7 @@ __global__ void __launch_bounds__(2 * QM, QM == QBM ? 2 : 1) qmm_kernel(const Qm
         o.z = pk_bf16(fmaf(sv, static_cast<float>((lo >> 16) & 0xffu), bv),
                       fmaf(sv, static_cast<float>((hi >> 16) & 0xffu), bv));
         o.w = pk_bf16(fmaf(sv, static_cast<float>(lo >> 24), bv), fmaf(sv, static_cast<float>(hi >> 24), bv));
-        *reinterpret_cast<uint4*>(ws + swz(row, chunk)) = o;
+        *reinterpret_cast<uint4*>(wt + swz(row, chunk)) = o;
       };
       put_word(wh * 4, wq.x);
       put_word(wh * 4 + 1, wq.y);
@@ -308,7 +313,7 @@ __global__ void __launch_bounds__(2 * QM, QM == QBM ? 2 : 1) qmm_kernel(const Qm
     for (int j = 0; j < NJ; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // ---- the products of one group from LDS ----
-  auto compute = [&](const uint16_t* xt) {
+  auto compute = [&](const uint16_t* xt, const uint16_t* wt) {
     bf16x8_t af[4][2];
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -318,8 +323,8 @@ __global__ void __launch_bounds__(2 * QM, QM == QBM ? 2 : 1) qmm_kernel(const Qm
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
       const int c = wn * (BN / 2) + j * 16 + li;
-      const bf16x8_t b0 = *reinterpret_cast<const bf16x8_t*>(ws + swz(c, q));
-      const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(ws + swz(c, 4 + q));
+      const bf16x8_t b0 = *reinterpret_cast<const bf16x8_t*>(wt + swz(c, q));
+      const bf16x8_t b1 = *reinterpret_cast<const bf16x8_t*>(wt + swz(c, 4 + q));
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i][0], b0, acc[i][j], 0, 0, 0);
@@ -334,9 +339,13 @@ __global__ void __launch_bounds__(2 * QM, QM == QBM ? 2 : 1) qmm_kernel(const Qm
   // through registers and two W register sets for 128-row tiles, Qwen3-4B
   // 4096-token prefill: q | k | v 139.5 -> 136.8 us, o / down 174.9 ->
   // 171.4, gate | up 423.0 -> 418.6.)
+  // With two W tiles (256-row x tiles) group g + 1's W goes into the tile
+  // group g - 1 used, whose reads all ended before the last barrier, so a
+  // wave dequantizes while the others' products run and one barrier per
+  // group remains.
   issue_x(gb, xs);
   QStage sa = load(gb);
-  store(sa);
+  store(sa, ws);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // x of group gb is in LDS
   __syncthreads();
   for (int g = gb; g < ge; g++) {
@@ -346,10 +355,10 @@ __global__ void __launch_bounds__(2 * QM, QM == QBM ? 2 : 1) qmm_kernel(const Qm
       issue_x(g + 1, xs + (cur ^ 1) * QM * RS);
       sa = load(g + 1);
     }
-    compute(xs + cur * QM * RS);
+    compute(xs + cur * QM * RS, ws + (NWB == 2 ? cur * BN * RS : 0));
     if (!more) break;
-    __syncthreads();  // every read of this group's W tile (and x tile) is done
-    store(sa);
+    if constexpr (NWB == 1) __syncthreads();  // every read of this group's W tile (and x tile) is done
+    store(sa, ws + (NWB == 2 ? (cur ^ 1) * BN * RS : 0));
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // x of group g + 1 is in LDS
     __syncthreads();
   }
