@@ -642,6 +642,10 @@ const void* qmm_kernel_for(bool gm) {
   return gm ? reinterpret_cast<const void*>(qmm_kernel<EPI, BN, true, QM>)
             : reinterpret_cast<const void*>(qmm_kernel<EPI, BN, false, QM>);
 }
+template <int EPI, int BN>
+const void* qmm_kernel_rows(bool gm, int qm) {
+  return qm > QBM ? qmm_kernel_for<EPI, BN, 2 * QBM>(gm) : qmm_kernel_for<EPI, BN>(gm);
+}
 
 // The GEMM with an epilogue over MLX-layout (sb == nullptr) or group-major
 // weights (w, w2 and sb, sb2 in the layout of QmmParams)
@@ -666,8 +670,16 @@ int qmm_epi_impl(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const ui
   if (bn == 128) qmm_split(M, N, K, &splits, &gps, cols);
   // SwiGLU needs both products of an output in one workgroup: no K split
   if (epi == QMM_SWIGLU && splits > 1) return kNoFit;
-  // 256-row x tiles on 8 waves for 160-column tiles and SwiGLU
-  const int qm = (bn == 160 || (bn == 256 && epi == QMM_SWIGLU)) && M >= 2048 ? 2 * QBM : QBM;
+  // 256-row x tiles on 8 waves (one workgroup per CU) from M = 2048 on:
+  // for 160- and 256-column tiles, and for 128-column tiles where their grid
+  // fills its last round of 256 CUs to 90% or more.  Public entry point,
+  // MLX layout, against 128-row tiles: 4096 x 12288 x 4096 464 -> 410 us,
+  // 4096 x 4096 x 12288 549 -> 474 us, 2048 x 151936 x 4096 3080 -> 2689
+  // us; but 2048 x 9728 x 2560 (608 tiles of 256 rows: 79% of the last
+  // round) 132 -> 152 us.
+  const int64_t t256 = static_cast<int64_t>((M + 2 * QBM - 1) / (2 * QBM)) * ((N + cols - 1) / cols);
+  const bool fills = t256 * 10 >= (t256 + 255) / 256 * 256 * 9;
+  const int qm = splits == 1 && M >= 2048 && (bn != 128 || fills) ? 2 * QBM : QBM;
   const int mtiles = (M + qm - 1) / qm, ntiles = (N + cols - 1) / cols;
   // Tile order.  Vocabulary-sized N: grouped by XCD in column-major order
   // (151936 x 4096 at M = 2048 runs 1.5x faster; the model's projections
@@ -692,18 +704,15 @@ int qmm_epi_impl(QmmEpilogue epi, const uint16_t* x, const uint32_t* w, const ui
       return rc;
     return check_launch("qmm");
   };
-  const int rc = bn == 256   ? (epi == QMM_SWIGLU    ? (qm > QBM ? launch(qmm_kernel_for<QMM_SWIGLU, 256, 2 * QBM>(gm), 256)
-                                                                 : launch(qmm_kernel_for<QMM_SWIGLU, 256>(gm), 256))
-                                : epi == QMM_RESIDUAL ? launch(qmm_kernel_for<QMM_RESIDUAL, 256>(gm), 256)
-                                                      : launch(qmm_kernel_for<QMM_STORE, 256>(gm), 256))
-                 : bn == 160 && qm > QBM
-                     ? (epi == QMM_RESIDUAL ? launch(qmm_kernel_for<QMM_RESIDUAL, 160, 2 * QBM>(gm), 160)
-                                            : launch(qmm_kernel_for<QMM_STORE, 160, 2 * QBM>(gm), 160))
-                 : bn == 160 ? (epi == QMM_RESIDUAL ? launch(qmm_kernel_for<QMM_RESIDUAL, 160>(gm), 160)
-                                                    : launch(qmm_kernel_for<QMM_STORE, 160>(gm), 160))
-                             : (epi == QMM_SWIGLU    ? launch(qmm_kernel_for<QMM_SWIGLU, 128>(gm), 128)
-                                : epi == QMM_RESIDUAL ? launch(qmm_kernel_for<QMM_RESIDUAL, 128>(gm), 128)
-                                                      : launch(qmm_kernel_for<QMM_STORE, 128>(gm), 128));
+  const void* kern = bn == 256 ? (epi == QMM_SWIGLU     ? qmm_kernel_rows<QMM_SWIGLU, 256>(gm, qm)
+                                  : epi == QMM_RESIDUAL ? qmm_kernel_rows<QMM_RESIDUAL, 256>(gm, qm)
+                                                        : qmm_kernel_rows<QMM_STORE, 256>(gm, qm))
+                     : bn == 160 ? (epi == QMM_RESIDUAL ? qmm_kernel_rows<QMM_RESIDUAL, 160>(gm, qm)
+                                                        : qmm_kernel_rows<QMM_STORE, 160>(gm, qm))
+                                 : (epi == QMM_SWIGLU     ? qmm_kernel_rows<QMM_SWIGLU, 128>(gm, qm)
+                                    : epi == QMM_RESIDUAL ? qmm_kernel_rows<QMM_RESIDUAL, 128>(gm, qm)
+                                                          : qmm_kernel_rows<QMM_STORE, 128>(gm, qm));
+  const int rc = launch(kern, bn);
   if (rc) return rc;
   if (splits > 1) {
     const int64_t mn = static_cast<int64_t>(M) * N;
