@@ -11,7 +11,10 @@
 //
 // Workgroup tile: 128 rows of x by 128 rows of W, 4 waves (2 x 2), each
 // 64 x 64 = 4 x 4 tiles of v_mfma_f32_16x16x32_bf16, 3 workgroups per CU;
-// on large grids 128 x 256 (waves of 64 x 128, 2 workgroups per CU).  Per K
+// on large grids 128 x 256 (waves of 64 x 128, 2 workgroups per CU); from
+// M = 2048 on, where their grid fills the chip, 256 rows of x on 8 waves,
+// one workgroup per CU, with two W tiles so that dequantizing the next
+// group's W overlaps the other waves' products.  Per K
 // step (one 64-wide group) the workgroup has x (128 x 64 bf16) and the
 // dequantized W tile (128 or 256 x 64 bf16: nibble bytes through
 // v_cvt_f32_ubyte, one FMA, v_cvt_pk_bf16_f32 per pair) in LDS: x comes
