@@ -1064,9 +1064,14 @@ __global__ void __launch_bounds__(512) attn_flash32_kernel(const AttnParams p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 31, hf = lane >> 5;  // query column, lane half
   const int rep_h = p.Hq / p.Hkv;
-  const int kvh = static_cast<int>(blockIdx.y) / (rep_h / HG);
-  const int h = kvh * rep_h + (static_cast<int>(blockIdx.y) % (rep_h / HG)) * HG + wave % HG;
-  const int t0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * TQ;  // longest rows first
+  // Grid: x the head groups, y the query tiles, longest rows first.  The
+  // hardware hands out workgroups in linear order (x fastest), so every
+  // head's longest tiles go out before any shorter one, and with 8 head
+  // groups workgroup b's XCD (b % 8) is that of its head group: one kv
+  // head's K / V stays in one L2.
+  const int kvh = static_cast<int>(blockIdx.x) / (rep_h / HG);
+  const int h = kvh * rep_h + (static_cast<int>(blockIdx.x) % (rep_h / HG)) * HG + wave % HG;
+  const int t0 = (static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y)) * TQ;
   const int offset = p.offset_dev ? *p.offset_dev : p.offset;
   const int L = offset + p.M;
   const int kend = p.causal ? min(L, offset + min(t0 + TQ, p.M)) : L;
@@ -1485,8 +1490,9 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
   };
   auto launch32 = [&](auto kern, int hg) {
     if (int e = allow_lds_ptr(reinterpret_cast<const void*>(kern), kF32Lds)) return e;
-    const int tq = 256 / hg;
-    hipLaunchKernelGGL(kern, dim3((M + tq - 1) / tq, Hkv * (rep / hg)), dim3(512), kF32Lds, stream, p);
+    const int tq = 256 / hg, tiles = (M + tq - 1) / tq;
+    if (tiles > 65535) return set_error(BMX_E_SHAPE, "attention: M=%d too large for one prefill launch", M);
+    hipLaunchKernelGGL(kern, dim3(Hkv * (rep / hg), tiles), dim3(512), kF32Lds, stream, p);
     return check_launch("attention_prefill");
   };
   if (rep % 8 == 0) return launch32(attn_flash32_kernel<8>, 8);
