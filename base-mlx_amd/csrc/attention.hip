@@ -699,10 +699,12 @@ __global__ void __launch_bounds__(64 * NW) attn_prefill_kernel(const AttnParams 
   const int tid = threadIdx.x & 255;
   const int n = lane & 15, g = lane >> 4;
   const int rep_h = p.Hq / p.Hkv;
-  // blockIdx.y: kv head x head groups of HG
-  const int kvh = static_cast<int>(blockIdx.y) / (rep_h / HG);
-  const int h = kvh * rep_h + (static_cast<int>(blockIdx.y) % (rep_h / HG)) * HG + wave % HG;
-  const int t0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * TQ;  // longest rows first
+  // Grid: x the head groups, y the query tiles, longest rows first (as in
+  // attn_flash32_kernel: all heads' longest tiles go out first, and a head
+  // group's workgroups share an XCD when there are 8 head groups).
+  const int kvh = static_cast<int>(blockIdx.x) / (rep_h / HG);
+  const int h = kvh * rep_h + (static_cast<int>(blockIdx.x) % (rep_h / HG)) * HG + wave % HG;
+  const int t0 = (static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y)) * TQ;
   const int offset = p.offset_dev ? *p.offset_dev : p.offset;
   const int L = offset + p.M;
   const int kend = p.causal ? min(L, offset + min(t0 + TQ, p.M)) : L;
@@ -1484,8 +1486,9 @@ int launch_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
   const int rep = Hq / Hkv;
   auto launch = [&](auto kern, int nw, int hg) {
     if (int e = allow_lds_ptr(reinterpret_cast<const void*>(kern), kFaLds)) return e;
-    const int tq = 16 * nw / hg;
-    hipLaunchKernelGGL(kern, dim3((M + tq - 1) / tq, Hkv * (rep / hg)), dim3(64 * nw), kFaLds, stream, p);
+    const int tq = 16 * nw / hg, tiles = (M + tq - 1) / tq;
+    if (tiles > 65535) return set_error(BMX_E_SHAPE, "attention: M=%d too large for one prefill launch", M);
+    hipLaunchKernelGGL(kern, dim3(Hkv * (rep / hg), tiles), dim3(64 * nw), kFaLds, stream, p);
     return check_launch("attention_prefill");
   };
   auto launch32 = [&](auto kern, int hg) {
